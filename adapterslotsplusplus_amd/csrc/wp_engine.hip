@@ -1,0 +1,979 @@
+// wp_engine.hip -- host side of the C ABI declared in include/warppipe_mi355x.h.
+//
+// Replaces the reference's pybind11 WarpPipeExtension (csrc/pybind/warp_pipe_bindings.cpp),
+// AdapterStore (csrc/memory/adapter_store.h), StagingBufferPool
+// (csrc/memory/staging_buffer.h), build_segment_table (csrc/dispatch/segment_builder.cpp)
+// and the rank dispatcher (csrc/dispatch/warp_pipe_dispatcher.cpp).
+//
+// Design points that differ from the reference, each fixing a behaviour it
+// documents as a defect or limit:
+//   * The segment table and the by-adapter plan live in HBM, written by the
+//     plan kernel or by a stream-ordered upload from pinned memory (the
+//     reference writes mapped host memory from the CPU, unordered with in-flight
+//     kernels, and every kernel block reads it over PCIe).
+//   * Registered weights are copied into engine-owned memory from a stream-ordered
+//     pool (hipMallocFromPoolAsync / hipFreeAsync), so eviction can never free
+//     memory a queued kernel still reads.  Cold adapters live in a pinned host
+//     store and become usable through prefetch (H2D on the prefetch stream).
+//   * Staging slots are sized per adapter (the reference's fixed 512 KiB slots
+//     overflow for rank 64 x 13824), eviction releases the id's slot, and a slot
+//     is never overwritten before the kernels that read it have finished.
+//   * Every scratch buffer (fp32 partials, H) is allocated at engine creation,
+//     so calls allocate nothing and graph replays keep valid pointers.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/warppipe_mi355x.h"
+#include "wp_apply.h"
+
+using namespace wp;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+#define WP_HIP(expr)                                                                           \
+  do {                                                                                         \
+    const hipError_t wp_e_ = (expr);                                                           \
+    if (wp_e_ != hipSuccess) return fail(WP_ERR_HIP, "%s: %s", #expr, hipGetErrorString(wp_e_)); \
+  } while (0)
+
+struct DeviceGuard {
+  int prev = -1;
+  bool changed = false;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) == hipSuccess && prev != dev) {
+      changed = hipSetDevice(dev) == hipSuccess;
+    }
+  }
+  ~DeviceGuard() {
+    if (changed) (void)hipSetDevice(prev);
+  }
+};
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline bool aligned(const void* p, uintptr_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; }
+inline bool rank_ok(int r) { return r == 8 || r == 16 || r == 32 || r == 64; }
+
+struct Adapter {
+  int32_t rank = 0, d = 0, o = 0, dtype = 0;
+  float alpha = 0.f;
+  void* dA = nullptr;  // device copies (pool)
+  void* dB = nullptr;
+  void* hA = nullptr;  // pinned host copies (host-resident adapters)
+  void* hB = nullptr;
+  size_t a_bytes = 0, b_bytes = 0;
+  hipEvent_t copied = nullptr;  // recorded after the registration copy
+};
+
+struct Slot {
+  int32_t adapter = -1;
+  void* A = nullptr;
+  void* B = nullptr;
+  size_t cap_a = 0, cap_b = 0;
+  hipEvent_t ready = nullptr;     // prefetch stream, after the copy
+  hipEvent_t last_use = nullptr;  // compute stream, after kernels that read the slot
+  bool issued = false;
+  bool used = false;
+};
+
+// d-range per shrink workgroup: at most 16 chunks, each a multiple of 128.
+inline void shrink_chunks(int d, int* dc, int* n_chunks) {
+  const int nc = static_cast<int>(std::min<int64_t>(16, ceil_div(d, 128)));
+  const int c = static_cast<int>(ceil_div(ceil_div(d, nc), 128) * 128);
+  *dc = c;
+  *n_chunks = static_cast<int>(ceil_div(d, c));
+}
+
+constexpr int kMaxChunks = 16;
+constexpr int kGridCapWorkgroups = 4096;
+
+}  // namespace
+
+struct wp_engine {
+  int device = 0;
+  wp_config cfg{};
+  hipStream_t pstream = nullptr;
+  hipMemPool_t pool = nullptr;
+  std::unordered_map<int32_t, Adapter> adapters;
+  std::vector<Slot> slots;
+
+  // Workspace (one allocation).
+  char* ws = nullptr;
+  uint32_t* header = nullptr;
+  Segment* segs = nullptr;
+  Block* blocks = nullptr;
+  int32_t* perm = nullptr;
+  uint32_t* counters = nullptr;
+  Entry* plan_entries = nullptr;
+  void* hscratch = nullptr;
+  int seg_cap = 0, block_cap = 0, tok_cap = 0, entry_cap = 0;
+  float* partials = nullptr;
+
+  // Id-indexed adapter table for table-mode kernels on device-built plans.
+  Entry* dtable = nullptr;
+  int dtable_cap = 0;
+  std::vector<Entry> htable;
+  bool table_dirty = true;
+  uint32_t table_staged_mask = 0;
+  char* pinned_table = nullptr;
+  size_t pinned_table_bytes = 0;
+  hipEvent_t table_done = nullptr;
+  bool table_done_pending = false;
+
+  // Pinned upload buffer for host-built plans.
+  char* pinned = nullptr;
+  size_t pinned_bytes = 0;
+  hipEvent_t upload_done = nullptr;
+  bool upload_pending = false;
+  uint32_t* pinned_zero = nullptr;
+
+  // Host view of the current plan.
+  int plan_kind = 0;          // 0 none, 1 host-built (build_segments), 2 device-built (build_seg_bounds)
+  int64_t plan_T = 0;         // device: T of build_seg_bounds; host: max token end
+  int plan_blocks = 0;        // host: exact block count
+  int plan_valid = 0;         // host: exact token count in perm
+  std::vector<int32_t> plan_entry_ids;  // host: adapter id per entry
+  std::vector<int> plan_entry_slot;     // host: staging slot read by the entry, or -1
+};
+
+namespace {
+
+int find_slot(const wp_engine* e, int32_t id) {
+  for (size_t i = 0; i < e->slots.size(); ++i)
+    if (e->slots[i].adapter == id) return static_cast<int>(i);
+  return -1;
+}
+
+bool slot_ready(const Slot& s) { return s.adapter >= 0 && s.issued && hipEventQuery(s.ready) == hipSuccess; }
+
+bool stream_capturing(hipStream_t s) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &st) != hipSuccess) return false;
+  return st != hipStreamCaptureStatusNone;
+}
+
+int wait_event_host(hipEvent_t ev, bool* pending) {
+  if (*pending) {
+    WP_HIP(hipEventSynchronize(ev));
+    *pending = false;
+  }
+  return WP_OK;
+}
+
+Entry entry_for(const wp_engine* e, int32_t id, const Adapter& ad, int* slot_used) {
+  Entry en{};
+  en.alpha = ad.alpha;
+  en.rank = ad.rank;
+  en.d_model = ad.d;
+  en.out_features = ad.o;
+  *slot_used = -1;
+  const int s = find_slot(e, id);
+  if (s >= 0 && slot_ready(e->slots[s])) {
+    en.a_ptr = reinterpret_cast<uint64_t>(e->slots[s].A);
+    en.b_ptr = reinterpret_cast<uint64_t>(e->slots[s].B);
+    *slot_used = s;
+  } else {
+    en.a_ptr = reinterpret_cast<uint64_t>(ad.dA);
+    en.b_ptr = reinterpret_cast<uint64_t>(ad.dB);
+  }
+  return en;
+}
+
+// Refreshes the device adapter table (stream-ordered) when registrations or
+// staging readiness changed.  Returns the staged-slot mask in use.
+int sync_table(wp_engine* e, hipStream_t stream, uint32_t* mask_out) {
+  if (stream_capturing(stream)) {
+    // Event queries are not allowed while a graph is being captured: the
+    // table must already be current (the uncaptured warm-up call made it so).
+    *mask_out = e->table_staged_mask;
+    if (e->table_dirty)
+      return fail(WP_ERR_STATE, "adapter table changed before graph capture; run the call once before capturing");
+    return WP_OK;
+  }
+  uint32_t mask = 0;
+  for (size_t i = 0; i < e->slots.size(); ++i)
+    if (slot_ready(e->slots[i]) && e->adapters.count(e->slots[i].adapter)) mask |= 1u << i;
+  *mask_out = mask;
+  if (!e->table_dirty && mask == e->table_staged_mask) return WP_OK;
+  if (e->dtable_cap == 0) return WP_OK;
+  std::fill(e->htable.begin(), e->htable.end(), Entry{});
+  for (const auto& kv : e->adapters) {
+    if (kv.first < 0 || kv.first >= e->dtable_cap) continue;
+    int su = -1;
+    e->htable[kv.first] = entry_for(e, kv.first, kv.second, &su);
+  }
+  const size_t bytes = sizeof(Entry) * static_cast<size_t>(e->dtable_cap);
+  int rc = wait_event_host(e->table_done, &e->table_done_pending);
+  if (rc != WP_OK) return rc;
+  if (e->pinned_table_bytes < bytes) {
+    if (e->pinned_table) WP_HIP(hipHostFree(e->pinned_table));
+    e->pinned_table = nullptr;
+    WP_HIP(hipHostMalloc(reinterpret_cast<void**>(&e->pinned_table), bytes, hipHostMallocDefault));
+    e->pinned_table_bytes = bytes;
+  }
+  std::memcpy(e->pinned_table, e->htable.data(), bytes);
+  WP_HIP(hipMemcpyAsync(e->dtable, e->pinned_table, bytes, hipMemcpyHostToDevice, stream));
+  WP_HIP(hipEventRecord(e->table_done, stream));
+  e->table_done_pending = true;
+  e->table_dirty = false;
+  e->table_staged_mask = mask;
+  return WP_OK;
+}
+
+int grow_table(wp_engine* e, int32_t id, hipStream_t stream) {
+  if (id < 0 || id < e->dtable_cap) return WP_OK;
+  constexpr int32_t kMaxTableIds = 1 << 20;
+  if (id >= kMaxTableIds) return WP_OK;  // usable through build_segments only
+  int cap = std::max(256, e->dtable_cap);
+  while (cap <= id) cap *= 2;
+  Entry* nt = nullptr;
+  WP_HIP(hipMallocFromPoolAsync(reinterpret_cast<void**>(&nt), sizeof(Entry) * cap, e->pool, stream));
+  if (e->dtable) WP_HIP(hipFreeAsync(e->dtable, stream));
+  e->dtable = nt;
+  e->dtable_cap = cap;
+  e->htable.assign(cap, Entry{});
+  e->table_dirty = true;
+  return WP_OK;
+}
+
+void invalidate_host_plan_for(wp_engine* e, int32_t id) {
+  if (e->plan_kind != 1) return;
+  for (int32_t pid : e->plan_entry_ids)
+    if (pid == id) {
+      e->plan_kind = 0;
+      return;
+    }
+}
+
+int release_slot(wp_engine* e, int s) {
+  if (s < 0) return WP_OK;
+  e->slots[s].adapter = -1;
+  e->slots[s].issued = false;
+  e->table_dirty = true;
+  return WP_OK;
+}
+
+int evict_impl(wp_engine* e, int32_t id, hipStream_t stream) {
+  auto it = e->adapters.find(id);
+  if (it == e->adapters.end()) return WP_OK;
+  Adapter& ad = it->second;
+  const int s = find_slot(e, id);
+  if (s >= 0) {
+    // The slot copy may still read the pinned host copy.
+    if (e->slots[s].issued) WP_HIP(hipEventSynchronize(e->slots[s].ready));
+    release_slot(e, s);
+  }
+  if (ad.dA) WP_HIP(hipFreeAsync(ad.dA, stream));
+  if (ad.dB) WP_HIP(hipFreeAsync(ad.dB, stream));
+  if (ad.hA) WP_HIP(hipHostFree(ad.hA));
+  if (ad.hB) WP_HIP(hipHostFree(ad.hB));
+  if (ad.copied) WP_HIP(hipEventDestroy(ad.copied));
+  e->adapters.erase(it);
+  if (id >= 0 && id < e->dtable_cap) e->table_dirty = true;
+  invalidate_host_plan_for(e, id);
+  return WP_OK;
+}
+
+// Slot reads are tracked for eager launches; inside a graph capture an event
+// record would become a graph node, so staged slots must not be recycled
+// while such a graph is still replayed.
+void record_slot_uses(wp_engine* e, const std::vector<int>& slot_ids, hipStream_t stream) {
+  if (stream_capturing(stream)) return;
+  for (int s : slot_ids) {
+    if (s < 0) continue;
+    if (hipEventRecord(e->slots[s].last_use, stream) == hipSuccess) e->slots[s].used = true;
+  }
+}
+
+void record_mask_uses(wp_engine* e, uint32_t mask, hipStream_t stream) {
+  if (stream_capturing(stream)) return;
+  for (size_t i = 0; i < e->slots.size(); ++i)
+    if (mask & (1u << i)) {
+      if (hipEventRecord(e->slots[i].last_use, stream) == hipSuccess) e->slots[i].used = true;
+    }
+}
+
+PlanView plan_view(const wp_engine* e) {
+  PlanView v;
+  v.header = e->header;
+  v.segments = e->segs;
+  v.blocks = e->blocks;
+  v.perm = e->perm;
+  v.counters = e->counters;
+  return v;
+}
+
+// Upper bound on the block count of the current plan, given at most `groups`
+// distinct adapters: sum_g ceil(n_g / TB) <= floor(T / TB) + G, and <= T.
+int block_bound(const wp_engine* e, int64_t groups) {
+  if (e->plan_kind == 1) return e->plan_blocks;
+  const int64_t T = e->plan_T;
+  const int64_t g = std::min<int64_t>(T, std::max<int64_t>(groups, 0));
+  return static_cast<int>(std::min<int64_t>(T, T / kBlockTokens + g));
+}
+
+int grid_block_slots(int bound, int per_block) {
+  const int cap = std::max(1, kGridCapWorkgroups / std::max(1, per_block));
+  return std::min(bound, cap);
+}
+
+}  // namespace
+
+// ============================================================================
+// C ABI
+// ============================================================================
+
+extern "C" {
+
+const char* wp_last_error(void) { return g_last_error.c_str(); }
+
+int wp_abi_version(void) { return WP_ABI_VERSION; }
+
+int wp_rank_supported(int32_t rank) { return rank_ok(rank) ? 1 : 0; }
+
+int wp_create(const wp_config* cfg_in, wp_engine** out) {
+  if (out == nullptr) return fail(WP_ERR_INVALID, "wp_create: out is NULL");
+  *out = nullptr;
+  wp_config cfg{};
+  cfg.device = 0;
+  cfg.num_staging_slots = 8;
+  cfg.max_tokens = kPlanMaxTokens;
+  cfg.max_rank = kMaxRank;
+  if (cfg_in) cfg = *cfg_in;
+  if (cfg.max_tokens <= 0 || cfg.max_tokens > kPlanMaxTokens)
+    return fail(WP_ERR_INVALID, "wp_create: max_tokens must be in [1, %d]", kPlanMaxTokens);
+  if (cfg.num_staging_slots < 0 || cfg.num_staging_slots > 32)
+    return fail(WP_ERR_INVALID, "wp_create: num_staging_slots must be in [0, 32]");
+  int ndev = 0;
+  const hipError_t ce = hipGetDeviceCount(&ndev);
+  if (ce != hipSuccess || ndev <= 0)
+    return fail(WP_ERR_NO_DEVICE, "wp_create: no HIP device available (%s)", hipGetErrorString(ce));
+  if (cfg.device < 0 || cfg.device >= ndev) return fail(WP_ERR_INVALID, "wp_create: device %d out of range", cfg.device);
+  DeviceGuard g(cfg.device);
+
+  wp_engine* e = new wp_engine();
+  e->device = cfg.device;
+  e->cfg = cfg;
+  auto bail = [&](int rc) {
+    wp_destroy(e);
+    return rc;
+  };
+
+  hipMemPoolProps props{};
+  props.allocType = hipMemAllocationTypePinned;
+  props.location.type = hipMemLocationTypeDevice;
+  props.location.id = cfg.device;
+  if (hipMemPoolCreate(&e->pool, &props) != hipSuccess)
+    return bail(fail(WP_ERR_HIP, "wp_create: hipMemPoolCreate failed"));
+  uint64_t keep = ~0ull;
+  (void)hipMemPoolSetAttribute(e->pool, hipMemPoolAttrReleaseThreshold, &keep);
+
+  e->tok_cap = cfg.max_tokens;
+  e->seg_cap = std::max(cfg.max_tokens, kRefMaxSegments);
+  e->block_cap = cfg.max_tokens + kRefMaxSegments;
+  e->entry_cap = kRefMaxSegments;
+  size_t off = 0;
+  auto carve = [&](size_t bytes) {
+    const size_t at = off;
+    off += (bytes + 255) & ~size_t(255);
+    return at;
+  };
+  const size_t o_hdr = carve(sizeof(uint32_t) * kHdrWords);
+  const size_t o_seg = carve(sizeof(Segment) * e->seg_cap);
+  const size_t o_blk = carve(sizeof(Block) * e->block_cap);
+  const size_t o_perm = carve(sizeof(int32_t) * e->tok_cap);
+  const size_t o_cnt = carve(sizeof(uint32_t) * e->block_cap);
+  const size_t o_ent = carve(sizeof(Entry) * e->entry_cap);
+  const size_t o_h = carve(sizeof(uint16_t) * static_cast<size_t>(e->tok_cap) * kMaxRank);
+  if (hipMalloc(reinterpret_cast<void**>(&e->ws), off) != hipSuccess)
+    return bail(fail(WP_ERR_HIP, "wp_create: workspace allocation (%zu bytes) failed", off));
+  if (hipMemset(e->ws, 0, off) != hipSuccess) return bail(fail(WP_ERR_HIP, "wp_create: workspace clear failed"));
+  e->header = reinterpret_cast<uint32_t*>(e->ws + o_hdr);
+  e->segs = reinterpret_cast<Segment*>(e->ws + o_seg);
+  e->blocks = reinterpret_cast<Block*>(e->ws + o_blk);
+  e->perm = reinterpret_cast<int32_t*>(e->ws + o_perm);
+  e->counters = reinterpret_cast<uint32_t*>(e->ws + o_cnt);
+  e->plan_entries = reinterpret_cast<Entry*>(e->ws + o_ent);
+  e->hscratch = e->ws + o_h;
+  const size_t pbytes = sizeof(float) * kMaxChunks * static_cast<size_t>(e->tok_cap) * kMaxRank;
+  if (hipMalloc(reinterpret_cast<void**>(&e->partials), pbytes) != hipSuccess)
+    return bail(fail(WP_ERR_HIP, "wp_create: partials allocation failed"));
+
+  e->pinned_bytes = sizeof(uint32_t) * kHdrWords + sizeof(Segment) * e->seg_cap + sizeof(Block) * e->block_cap +
+                    sizeof(int32_t) * e->tok_cap + sizeof(Entry) * e->entry_cap + 1024;
+  if (hipHostMalloc(reinterpret_cast<void**>(&e->pinned), e->pinned_bytes, hipHostMallocDefault) != hipSuccess)
+    return bail(fail(WP_ERR_HIP, "wp_create: pinned upload buffer failed"));
+  if (hipHostMalloc(reinterpret_cast<void**>(&e->pinned_zero), 64, hipHostMallocDefault) != hipSuccess)
+    return bail(fail(WP_ERR_HIP, "wp_create: pinned zero word failed"));
+  std::memset(e->pinned_zero, 0, 64);
+  if (hipEventCreateWithFlags(&e->upload_done, hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&e->table_done, hipEventDisableTiming) != hipSuccess)
+    return bail(fail(WP_ERR_HIP, "wp_create: event creation failed"));
+  // The prefetch engine's own stream, default priority, never synchronising
+  // with the null stream (reference: bindings:32).
+  if (hipStreamCreateWithFlags(&e->pstream, hipStreamNonBlocking) != hipSuccess)
+    return bail(fail(WP_ERR_HIP, "wp_create: prefetch stream creation failed"));
+  e->slots.resize(cfg.num_staging_slots);
+  for (auto& s : e->slots) {
+    if (hipEventCreateWithFlags(&s.ready, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&s.last_use, hipEventDisableTiming) != hipSuccess)
+      return bail(fail(WP_ERR_HIP, "wp_create: slot event creation failed"));
+  }
+  *out = e;
+  return WP_OK;
+}
+
+int wp_destroy(wp_engine* e) {
+  if (e == nullptr) return WP_OK;
+  DeviceGuard g(e->device);
+  (void)hipDeviceSynchronize();
+  for (auto& kv : e->adapters) {
+    Adapter& ad = kv.second;
+    if (ad.dA) (void)hipFree(ad.dA);
+    if (ad.dB) (void)hipFree(ad.dB);
+    if (ad.hA) (void)hipHostFree(ad.hA);
+    if (ad.hB) (void)hipHostFree(ad.hB);
+    if (ad.copied) (void)hipEventDestroy(ad.copied);
+  }
+  for (auto& s : e->slots) {
+    if (s.A) (void)hipFree(s.A);
+    if (s.B) (void)hipFree(s.B);
+    if (s.ready) (void)hipEventDestroy(s.ready);
+    if (s.last_use) (void)hipEventDestroy(s.last_use);
+  }
+  if (e->dtable) (void)hipFree(e->dtable);
+  if (e->ws) (void)hipFree(e->ws);
+  if (e->partials) (void)hipFree(e->partials);
+  if (e->pinned) (void)hipHostFree(e->pinned);
+  if (e->pinned_zero) (void)hipHostFree(e->pinned_zero);
+  if (e->pinned_table) (void)hipHostFree(e->pinned_table);
+  if (e->upload_done) (void)hipEventDestroy(e->upload_done);
+  if (e->table_done) (void)hipEventDestroy(e->table_done);
+  if (e->pstream) (void)hipStreamDestroy(e->pstream);
+  if (e->pool) (void)hipMemPoolDestroy(e->pool);
+  delete e;
+  return WP_OK;
+}
+
+int wp_register_adapter(wp_engine* e, int32_t adapter_id, const void* A, const void* B, int32_t rank, int32_t d_model,
+                        int32_t out_features, float alpha_scale, int32_t dtype, int32_t host_resident, void* stream_) {
+  if (!e) return fail(WP_ERR_INVALID, "register_adapter: engine is NULL");
+  if (!rank_ok(rank)) return fail(WP_ERR_INVALID, "register_adapter: unsupported rank %d (only 8/16/32/64)", rank);
+  if (dtype != WP_DTYPE_F16 && dtype != WP_DTYPE_BF16) return fail(WP_ERR_INVALID, "register_adapter: bad dtype");
+  if (d_model <= 0 || d_model % 8 != 0) return fail(WP_ERR_INVALID, "register_adapter: d_model must be a positive multiple of 8");
+  if (out_features <= 0 || out_features % 4 != 0)
+    return fail(WP_ERR_INVALID, "register_adapter: out_features must be a positive multiple of 4");
+  if (!A || !B) return fail(WP_ERR_INVALID, "register_adapter: null weights");
+  // Reference: AdapterStore::register_adapter rejects pointers that are not
+  // 16-byte aligned (adapter_store.h:23-25).
+  if (!aligned(A, 16) || !aligned(B, 16))
+    return fail(WP_ERR_INVALID, "AdapterStore::register_adapter: A/B pointer not 16-byte aligned");
+  DeviceGuard g(e->device);
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  int rc = evict_impl(e, adapter_id, stream);
+  if (rc != WP_OK) return rc;
+  Adapter ad;
+  ad.rank = rank;
+  ad.d = d_model;
+  ad.o = out_features;
+  ad.dtype = dtype;
+  ad.alpha = alpha_scale;
+  ad.a_bytes = sizeof(uint16_t) * static_cast<size_t>(rank) * d_model;
+  ad.b_bytes = sizeof(uint16_t) * static_cast<size_t>(out_features) * rank;
+  if (host_resident) {
+    WP_HIP(hipHostMalloc(&ad.hA, ad.a_bytes, hipHostMallocDefault));
+    WP_HIP(hipHostMalloc(&ad.hB, ad.b_bytes, hipHostMallocDefault));
+    std::memcpy(ad.hA, A, ad.a_bytes);
+    std::memcpy(ad.hB, B, ad.b_bytes);
+  } else {
+    WP_HIP(hipMallocFromPoolAsync(&ad.dA, ad.a_bytes, e->pool, stream));
+    WP_HIP(hipMallocFromPoolAsync(&ad.dB, ad.b_bytes, e->pool, stream));
+    WP_HIP(hipMemcpyAsync(ad.dA, A, ad.a_bytes, hipMemcpyDefault, stream));
+    WP_HIP(hipMemcpyAsync(ad.dB, B, ad.b_bytes, hipMemcpyDefault, stream));
+    WP_HIP(hipEventCreateWithFlags(&ad.copied, hipEventDisableTiming));
+    WP_HIP(hipEventRecord(ad.copied, stream));
+  }
+  rc = grow_table(e, adapter_id, stream);
+  if (rc != WP_OK) return rc;
+  e->adapters[adapter_id] = ad;
+  if (adapter_id >= 0 && adapter_id < e->dtable_cap) e->table_dirty = true;
+  return WP_OK;
+}
+
+int wp_evict_adapter(wp_engine* e, int32_t adapter_id, void* stream) {
+  if (!e) return fail(WP_ERR_INVALID, "evict_adapter: engine is NULL");
+  DeviceGuard g(e->device);
+  return evict_impl(e, adapter_id, static_cast<hipStream_t>(stream));
+}
+
+int wp_has_adapter(wp_engine* e, int32_t adapter_id) { return (e && e->adapters.count(adapter_id)) ? 1 : 0; }
+
+int wp_build_segments(wp_engine* e, const int32_t* ids, int32_t K, const int32_t* offsets, int32_t n_offsets,
+                      void* stream_) {
+  if (!e) return fail(WP_ERR_INVALID, "build_segments: engine is NULL");
+  if (K < 0 || n_offsets != K + 1)
+    return fail(WP_ERR_INVALID, "build_segment_table: seg_offsets must have K+1 entries");
+  if (K > kRefMaxSegments) return fail(WP_ERR_CAPACITY, "build_segment_table: K exceeds WP_MAX_SEGMENTS");
+  DeviceGuard g(e->device);
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  if (stream_capturing(stream)) return fail(WP_ERR_STATE, "build_segments cannot run during graph capture");
+
+  // Entries (one per distinct adapter, first-appearance order) and groups.
+  std::vector<int32_t> entry_ids;
+  std::vector<int> entry_slot;
+  std::vector<Entry> entries;
+  std::unordered_map<int32_t, int> entry_of;
+  std::vector<std::vector<int>> group_segs;
+  std::vector<std::pair<int32_t, int32_t>> ranges;
+  int64_t max_end = 0;
+  for (int k = 0; k < K; ++k) {
+    const int32_t id = ids[k];
+    const int32_t st = offsets[k];
+    const int32_t cnt = offsets[k + 1] - offsets[k];
+    auto it = e->adapters.find(id);
+    if (it == e->adapters.end()) return fail(WP_ERR_UNKNOWN_ADAPTER, "AdapterStore::lookup: unknown adapter_id %d", id);
+    if (st < 0 || cnt < 0) return fail(WP_ERR_INVALID, "build_segments: segment %d has a negative start or count", k);
+    auto ei = entry_of.find(id);
+    int ent;
+    if (ei == entry_of.end()) {
+      int su = -1;
+      Entry en = entry_for(e, id, it->second, &su);
+      if (en.a_ptr == 0)
+        return fail(WP_ERR_STATE, "build_segments: adapter %d is host-resident and not staged (prefetch it first)", id);
+      ent = static_cast<int>(entries.size());
+      entry_of[id] = ent;
+      entries.push_back(en);
+      entry_ids.push_back(id);
+      entry_slot.push_back(su);
+      group_segs.emplace_back();
+    } else {
+      ent = ei->second;
+    }
+    if (cnt > 0) {
+      group_segs[ent].push_back(k);
+      ranges.emplace_back(st, cnt);
+      max_end = std::max<int64_t>(max_end, static_cast<int64_t>(st) + cnt);
+    }
+  }
+  std::sort(ranges.begin(), ranges.end());
+  for (size_t i = 1; i < ranges.size(); ++i)
+    if (static_cast<int64_t>(ranges[i - 1].first) + ranges[i - 1].second > ranges[i].first)
+      return fail(WP_ERR_INVALID, "build_segments: segments overlap at token %d", ranges[i].first);
+  int64_t n_tok = 0;
+  for (auto& r : ranges) n_tok += r.second;
+  if (n_tok > e->tok_cap)
+    return fail(WP_ERR_CAPACITY, "build_segments: %lld tokens exceed max_tokens %d", (long long)n_tok, e->tok_cap);
+
+  // Wait until the previous upload left the pinned buffer.
+  int rc = wait_event_host(e->upload_done, &e->upload_pending);
+  if (rc != WP_OK) return rc;
+  char* p = e->pinned;
+  uint32_t* hdr = reinterpret_cast<uint32_t*>(p);
+  Segment* hsegs = reinterpret_cast<Segment*>(p + 256);
+  Block* hblocks = reinterpret_cast<Block*>(reinterpret_cast<char*>(hsegs) + sizeof(Segment) * std::max(K, 1));
+  int32_t* hperm = nullptr;
+  Entry* hent = nullptr;
+  for (int k = 0; k < K; ++k) {
+    hsegs[k].adapter_id = ids[k];
+    hsegs[k].token_start = offsets[k];
+    hsegs[k].token_count = offsets[k + 1] - offsets[k];
+    hsegs[k].pad = 0;
+  }
+  // perm: each adapter's segments concatenated; blocks of kBlockTokens.
+  std::vector<int32_t> perm_v;
+  perm_v.reserve(static_cast<size_t>(n_tok));
+  std::vector<Block> blocks_v;
+  for (size_t ent = 0; ent < group_segs.size(); ++ent) {
+    const int first = static_cast<int>(perm_v.size());
+    for (int k : group_segs[ent])
+      for (int32_t t = offsets[k]; t < offsets[k + 1]; ++t) perm_v.push_back(t);
+    const int n = static_cast<int>(perm_v.size()) - first;
+    for (int j = 0; j < n; j += kBlockTokens) {
+      Block b;
+      b.adapter_id = entry_ids[ent];
+      b.first = first + j;
+      b.count = std::min(kBlockTokens, n - j);
+      b.entry = static_cast<int>(ent);
+      blocks_v.push_back(b);
+    }
+  }
+  if (static_cast<int>(blocks_v.size()) > e->block_cap) return fail(WP_ERR_CAPACITY, "build_segments: too many blocks");
+  std::memcpy(hblocks, blocks_v.data(), sizeof(Block) * blocks_v.size());
+  hperm = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(hblocks) + sizeof(Block) * std::max<size_t>(blocks_v.size(), 1));
+  std::memcpy(hperm, perm_v.data(), sizeof(int32_t) * perm_v.size());
+  char* pe = reinterpret_cast<char*>(hperm) + sizeof(int32_t) * std::max<size_t>(perm_v.size(), 1);
+  pe = reinterpret_cast<char*>((reinterpret_cast<uintptr_t>(pe) + 63) & ~uintptr_t(63));
+  hent = reinterpret_cast<Entry*>(pe);
+  std::memcpy(hent, entries.data(), sizeof(Entry) * entries.size());
+  hdr[kHdrNumSegments] = static_cast<uint32_t>(K);
+  hdr[kHdrNumBlocks] = static_cast<uint32_t>(blocks_v.size());
+  hdr[kHdrNumGroups] = static_cast<uint32_t>(entries.size());
+  hdr[kHdrNumValid] = static_cast<uint32_t>(n_tok);
+  hdr[kHdrT] = static_cast<uint32_t>(max_end);
+
+  WP_HIP(hipMemcpyAsync(e->header, hdr, sizeof(uint32_t) * kHdrErrors, hipMemcpyHostToDevice, stream));
+  if (K > 0) WP_HIP(hipMemcpyAsync(e->segs, hsegs, sizeof(Segment) * K, hipMemcpyHostToDevice, stream));
+  if (!blocks_v.empty())
+    WP_HIP(hipMemcpyAsync(e->blocks, hblocks, sizeof(Block) * blocks_v.size(), hipMemcpyHostToDevice, stream));
+  if (!perm_v.empty())
+    WP_HIP(hipMemcpyAsync(e->perm, hperm, sizeof(int32_t) * perm_v.size(), hipMemcpyHostToDevice, stream));
+  if (!entries.empty())
+    WP_HIP(hipMemcpyAsync(e->plan_entries, hent, sizeof(Entry) * entries.size(), hipMemcpyHostToDevice, stream));
+  WP_HIP(hipEventRecord(e->upload_done, stream));
+  e->upload_pending = true;
+
+  e->plan_kind = 1;
+  e->plan_T = max_end;
+  e->plan_blocks = static_cast<int>(blocks_v.size());
+  e->plan_valid = static_cast<int>(n_tok);
+  e->plan_entry_ids = entry_ids;
+  e->plan_entry_slot = entry_slot;
+  return WP_OK;
+}
+
+int wp_build_seg_bounds(wp_engine* e, const void* idx, int32_t idx_is_int64, int64_t T, void* stream_) {
+  if (!e) return fail(WP_ERR_INVALID, "build_seg_bounds: engine is NULL");
+  if (T < 0) return fail(WP_ERR_INVALID, "build_seg_bounds: negative token count");
+  // Reference: returns False, and launches nothing, above its capacity (bindings:165-166).
+  if (T > e->cfg.max_tokens) return WP_NOT_HANDLED;
+  if (T > 0 && idx == nullptr) return fail(WP_ERR_INVALID, "build_seg_bounds: null indices");
+  DeviceGuard g(e->device);
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  WP_HIP(launch_plan(idx, idx_is_int64 ? 1 : 0, static_cast<int>(T), e->header, e->segs, e->blocks, e->perm,
+                     e->seg_cap, e->block_cap, stream));
+  e->plan_kind = 2;
+  e->plan_T = T;
+  e->plan_blocks = -1;
+  e->plan_valid = -1;
+  e->plan_entry_ids.clear();
+  e->plan_entry_slot.clear();
+  return WP_OK;
+}
+
+int wp_read_segments(wp_engine* e, int32_t* out, int64_t cap, int64_t* num_segments, void* stream_) {
+  if (!e || !num_segments) return fail(WP_ERR_INVALID, "read_segments: null argument");
+  DeviceGuard g(e->device);
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  uint32_t hdr[kHdrWords];
+  WP_HIP(hipMemcpyAsync(hdr, e->header, sizeof(hdr), hipMemcpyDeviceToHost, stream));
+  WP_HIP(hipStreamSynchronize(stream));
+  const int64_t n = e->plan_kind == 0 ? 0 : hdr[kHdrNumSegments];
+  *num_segments = n;
+  const int64_t m = std::min<int64_t>(std::min<int64_t>(n, cap), e->seg_cap);
+  if (m > 0 && out) {
+    std::vector<Segment> tmp(static_cast<size_t>(m));
+    WP_HIP(hipMemcpyAsync(tmp.data(), e->segs, sizeof(Segment) * m, hipMemcpyDeviceToHost, stream));
+    WP_HIP(hipStreamSynchronize(stream));
+    for (int64_t i = 0; i < m; ++i) {
+      out[3 * i + 0] = tmp[i].adapter_id;
+      out[3 * i + 1] = tmp[i].token_start;
+      out[3 * i + 2] = tmp[i].token_count;
+    }
+  }
+  return WP_OK;
+}
+
+int wp_read_plan(wp_engine* e, int32_t* perm, int64_t perm_cap, int32_t* blocks, int64_t block_cap, int64_t* n_valid,
+                 int64_t* n_blocks, void* stream_) {
+  if (!e || !n_valid || !n_blocks) return fail(WP_ERR_INVALID, "read_plan: null argument");
+  DeviceGuard g(e->device);
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  uint32_t hdr[kHdrWords];
+  WP_HIP(hipMemcpyAsync(hdr, e->header, sizeof(hdr), hipMemcpyDeviceToHost, stream));
+  WP_HIP(hipStreamSynchronize(stream));
+  *n_valid = hdr[kHdrNumValid];
+  *n_blocks = hdr[kHdrNumBlocks];
+  const int64_t np = std::min<int64_t>(*n_valid, perm_cap);
+  const int64_t nb = std::min<int64_t>(*n_blocks, block_cap);
+  if (np > 0 && perm) WP_HIP(hipMemcpyAsync(perm, e->perm, sizeof(int32_t) * np, hipMemcpyDeviceToHost, stream));
+  if (nb > 0 && blocks) WP_HIP(hipMemcpyAsync(blocks, e->blocks, sizeof(Block) * nb, hipMemcpyDeviceToHost, stream));
+  WP_HIP(hipStreamSynchronize(stream));
+  return WP_OK;
+}
+
+int wp_read_device_errors(wp_engine* e, uint32_t* flags, void* stream_) {
+  if (!e || !flags) return fail(WP_ERR_INVALID, "read_device_errors: null argument");
+  DeviceGuard g(e->device);
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  uint32_t v = 0;
+  WP_HIP(hipMemcpyAsync(&v, e->header + kHdrErrors, sizeof(v), hipMemcpyDeviceToHost, stream));
+  WP_HIP(hipMemcpyAsync(e->header + kHdrErrors, e->pinned_zero, sizeof(v), hipMemcpyHostToDevice, stream));
+  WP_HIP(hipStreamSynchronize(stream));
+  *flags = v;
+  return WP_OK;
+}
+
+namespace {
+
+int check_io(const char* who, int32_t dtype, const void* p16, const char* name) {
+  if (dtype != WP_DTYPE_F16 && dtype != WP_DTYPE_BF16) return fail(WP_ERR_INVALID, "%s: dtype must be fp16 or bf16", who);
+  if (p16 && !aligned(p16, 16)) return fail(WP_ERR_INVALID, "%s: %s must be 16-byte aligned", who, name);
+  return WP_OK;
+}
+
+// Table-mode weights for the current plan.
+int table_weights(wp_engine* e, hipStream_t stream, Weights* w, uint32_t* mask) {
+  *mask = 0;
+  w->mode = kTable;
+  if (e->plan_kind == 1) {
+    w->entries = e->plan_entries;
+    w->num_ids = static_cast<int32_t>(e->plan_entry_ids.size());
+    return WP_OK;
+  }
+  int rc = sync_table(e, stream, mask);
+  if (rc != WP_OK) return rc;
+  w->entries = e->dtable;
+  w->num_ids = e->dtable_cap;
+  return WP_OK;
+}
+
+}  // namespace
+
+int wp_shrink(wp_engine* e, const void* X, void* H, int32_t d_model, int32_t rank, int64_t T, int64_t h_row_stride,
+              int32_t dtype, void* stream_) {
+  if (!e) return fail(WP_ERR_INVALID, "shrink: engine is NULL");
+  if (rank != 0 && !rank_ok(rank)) return fail(WP_ERR_INVALID, "dispatch_bgmv_shrink: unsupported rank (only 8/16/32/64)");
+  int rc = check_io("shrink", dtype, X, "X");
+  if (rc != WP_OK) return rc;
+  if ((rc = check_io("shrink", dtype, H, "H")) != WP_OK) return rc;
+  if (d_model <= 0 || d_model % 8 != 0) return fail(WP_ERR_INVALID, "shrink: d_model must be a positive multiple of 8");
+  const int64_t need = rank == 0 ? kMaxRank : rank;
+  if (h_row_stride < need || h_row_stride % 8 != 0)
+    return fail(WP_ERR_INVALID, "shrink: H row stride %lld must be >= %lld and a multiple of 8", (long long)h_row_stride,
+                (long long)need);
+  if (e->plan_kind == 0) return fail(WP_ERR_STATE, "shrink: no segment table (call build_segments or build_seg_bounds)");
+  if (e->plan_T > T) return fail(WP_ERR_INVALID, "shrink: segments reach token %lld but X has %lld rows", (long long)e->plan_T, (long long)T);
+  if (e->plan_kind == 1) {
+    for (size_t i = 0; i < e->plan_entry_ids.size(); ++i) {
+      const Adapter& ad = e->adapters.at(e->plan_entry_ids[i]);
+      if (ad.d != d_model)
+        return fail(WP_ERR_INVALID, "shrink: adapter %d has d_model %d, call has %d", e->plan_entry_ids[i], ad.d, d_model);
+      if (rank != 0 && ad.rank != rank)
+        return fail(WP_ERR_INVALID, "shrink: adapter %d has rank %d, call has %d", e->plan_entry_ids[i], ad.rank, rank);
+      if (ad.dtype != dtype) return fail(WP_ERR_INVALID, "shrink: adapter %d dtype differs from X", e->plan_entry_ids[i]);
+    }
+  }
+  DeviceGuard g(e->device);
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  ApplyArgs a{};
+  a.x = X;
+  a.ldx = d_model;
+  a.h = H;
+  a.ldh = h_row_stride;
+  a.d_model = d_model;
+  a.rank = rank;
+  shrink_chunks(d_model, &a.dc, &a.n_chunks);
+  a.ptok = e->plan_kind == 1 ? std::max(1, e->plan_valid) : static_cast<int>(std::max<int64_t>(1, e->plan_T));
+  a.pstride = rank == 0 ? kMaxRank : rank;
+  a.partials = e->partials;
+  a.plan = plan_view(e);
+  uint32_t mask = 0;
+  if ((rc = table_weights(e, stream, &a.w, &mask)) != WP_OK) return rc;
+  a.w.n_slices = 1;
+  const int bound = block_bound(e, e->plan_T);
+  WP_HIP(launch_shrink(dtype == WP_DTYPE_BF16, a, grid_block_slots(bound, a.n_chunks), stream));
+  if (e->plan_kind == 1) record_slot_uses(e, e->plan_entry_slot, stream);
+  else record_mask_uses(e, mask, stream);
+  return WP_OK;
+}
+
+int wp_expand(wp_engine* e, const void* H, void* Y, int32_t out_features, int32_t rank, int64_t T, int64_t h_row_stride,
+              int64_t y_row_stride, int32_t y_col_offset, int32_t dtype, void* stream_) {
+  if (!e) return fail(WP_ERR_INVALID, "expand: engine is NULL");
+  if (rank != 0 && !rank_ok(rank)) return fail(WP_ERR_INVALID, "dispatch_bgmv_expand: unsupported rank (only 8/16/32/64)");
+  int rc = check_io("expand", dtype, H, "H");
+  if (rc != WP_OK) return rc;
+  if (dtype != WP_DTYPE_F16 && dtype != WP_DTYPE_BF16) return fail(WP_ERR_INVALID, "expand: bad dtype");
+  if (!aligned(Y, 8)) return fail(WP_ERR_INVALID, "expand: Y must be 8-byte aligned");
+  if (out_features <= 0 || out_features % 4 != 0)
+    return fail(WP_ERR_INVALID, "expand: out_features must be a positive multiple of 4");
+  if (y_col_offset < 0 || y_col_offset % 4 != 0 || y_row_stride % 4 != 0 || y_row_stride < y_col_offset + out_features)
+    return fail(WP_ERR_INVALID, "expand: Y window [%d, %d) does not fit row stride %lld with 4-element alignment",
+                y_col_offset, y_col_offset + out_features, (long long)y_row_stride);
+  const int64_t need = rank == 0 ? kMaxRank : rank;
+  if (h_row_stride < need || h_row_stride % 8 != 0) return fail(WP_ERR_INVALID, "expand: bad H row stride");
+  if (e->plan_kind == 0) return fail(WP_ERR_STATE, "expand: no segment table (call build_segments or build_seg_bounds)");
+  if (e->plan_T > T) return fail(WP_ERR_INVALID, "expand: segments reach token %lld but Y has %lld rows", (long long)e->plan_T, (long long)T);
+  if (e->plan_kind == 1) {
+    for (size_t i = 0; i < e->plan_entry_ids.size(); ++i) {
+      const Adapter& ad = e->adapters.at(e->plan_entry_ids[i]);
+      if (ad.o != out_features)
+        return fail(WP_ERR_INVALID, "expand: adapter %d has out_features %d, call has %d", e->plan_entry_ids[i], ad.o,
+                    out_features);
+      if (rank != 0 && ad.rank != rank)
+        return fail(WP_ERR_INVALID, "expand: adapter %d has rank %d, call has %d", e->plan_entry_ids[i], ad.rank, rank);
+      if (ad.dtype != dtype) return fail(WP_ERR_INVALID, "expand: adapter %d dtype differs from Y", e->plan_entry_ids[i]);
+    }
+  }
+  DeviceGuard g(e->device);
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  ApplyArgs a{};
+  a.h = const_cast<void*>(H);
+  a.ldh = h_row_stride;
+  a.y = Y;
+  a.ldy = y_row_stride;
+  a.rank = rank;
+  a.plan = plan_view(e);
+  uint32_t mask = 0;
+  if ((rc = table_weights(e, stream, &a.w, &mask)) != WP_OK) return rc;
+  const int cols = expand_cols_per_workgroup();
+  a.w.n_slices = 1;
+  a.w.o_size[0] = out_features;
+  a.w.y_off[0] = y_col_offset;
+  a.w.oc_start[0] = 0;
+  a.w.oc_start[1] = static_cast<int32_t>(ceil_div(out_features, cols));
+  a.n_ochunks = a.w.oc_start[1];
+  const int bound = block_bound(e, e->plan_T);
+  WP_HIP(launch_expand(dtype == WP_DTYPE_BF16, a, grid_block_slots(bound, a.n_ochunks), stream));
+  if (e->plan_kind == 1) record_slot_uses(e, e->plan_entry_slot, stream);
+  else record_mask_uses(e, mask, stream);
+  return WP_OK;
+}
+
+int wp_add_lora(wp_engine* e, void* y, const void* x, const void* wa, int64_t wa_stride0, int32_t num_loras,
+                int32_t n_slices, const void* const* wb, const int64_t* wb_stride0, const int32_t* out_features,
+                const int32_t* y_col_offsets, float scale, int32_t rank, int32_t d_model, int64_t T,
+                int64_t y_row_stride, int32_t dtype, void* stream_) {
+  if (!e) return fail(WP_ERR_INVALID, "add_lora: engine is NULL");
+  // Reference: add_lora_packed returns False for ranks its kernels lack (bindings:197-198).
+  if (!rank_ok(rank)) return WP_NOT_HANDLED;
+  int rc = check_io("add_lora", dtype, x, "x");
+  if (rc != WP_OK) return rc;
+  if ((rc = check_io("add_lora", dtype, wa, "wa_t_all")) != WP_OK) return rc;
+  if (!aligned(y, 8)) return fail(WP_ERR_INVALID, "add_lora: y must be 8-byte aligned");
+  if (d_model <= 0 || d_model % 8 != 0) return fail(WP_ERR_INVALID, "add_lora: d_model must be a positive multiple of 8");
+  if (num_loras <= 0) return fail(WP_ERR_INVALID, "add_lora: num_loras must be positive");
+  if (n_slices < 1 || n_slices > kMaxSlices) return fail(WP_ERR_INVALID, "add_lora: 1..%d output slices", kMaxSlices);
+  if (wa_stride0 % 8 != 0) return fail(WP_ERR_INVALID, "add_lora: wa_t_all stride must be a multiple of 8");
+  for (int s = 0; s < n_slices; ++s) {
+    if ((rc = check_io("add_lora", dtype, wb[s], "wb_t_all")) != WP_OK) return rc;
+    if (wb_stride0[s] % 8 != 0) return fail(WP_ERR_INVALID, "add_lora: wb_t_all stride must be a multiple of 8");
+    if (out_features[s] <= 0 || out_features[s] % 4 != 0 || y_col_offsets[s] < 0 || y_col_offsets[s] % 4 != 0 ||
+        y_col_offsets[s] + out_features[s] > y_row_stride)
+      return fail(WP_ERR_INVALID, "add_lora: slice %d window [%d, %d) does not fit y (row stride %lld, 4-aligned)", s,
+                  y_col_offsets[s], y_col_offsets[s] + out_features[s], (long long)y_row_stride);
+  }
+  if (y_row_stride % 4 != 0) return fail(WP_ERR_INVALID, "add_lora: y row stride must be a multiple of 4");
+  if (e->plan_kind == 0) return fail(WP_ERR_STATE, "add_lora: no segment table (call build_seg_bounds first)");
+  if (e->plan_T > T) return fail(WP_ERR_INVALID, "add_lora: segments reach token %lld but x has %lld rows", (long long)e->plan_T, (long long)T);
+  if (e->plan_T > e->tok_cap)
+    return fail(WP_ERR_CAPACITY, "add_lora: segments reach token %lld, beyond max_tokens %d", (long long)e->plan_T, e->tok_cap);
+  DeviceGuard g(e->device);
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+
+  ApplyArgs a{};
+  a.x = x;
+  a.ldx = d_model;
+  a.h = e->hscratch;
+  a.ldh = rank;
+  a.y = y;
+  a.ldy = y_row_stride;
+  a.d_model = d_model;
+  a.rank = rank;
+  shrink_chunks(d_model, &a.dc, &a.n_chunks);
+  a.ptok = e->plan_kind == 1 ? std::max(1, e->plan_valid) : static_cast<int>(std::max<int64_t>(1, e->plan_T));
+  a.pstride = rank;
+  a.partials = e->partials;
+  a.plan = plan_view(e);
+  a.w.mode = kStacked;
+  a.w.num_ids = num_loras;
+  a.w.a_base = wa;
+  a.w.a_stride = wa_stride0;
+  a.w.scale = scale;
+  a.w.n_slices = n_slices;
+  const int cols = expand_cols_per_workgroup();
+  int oc = 0;
+  for (int s = 0; s < n_slices; ++s) {
+    a.w.b_base[s] = wb[s];
+    a.w.b_stride[s] = wb_stride0[s];
+    a.w.o_size[s] = out_features[s];
+    a.w.y_off[s] = y_col_offsets[s];
+    a.w.oc_start[s] = oc;
+    oc += static_cast<int>(ceil_div(out_features[s], cols));
+  }
+  a.w.oc_start[n_slices] = oc;
+  a.n_ochunks = oc;
+  const int bound = block_bound(e, num_loras);
+  WP_HIP(launch_shrink(dtype == WP_DTYPE_BF16, a, grid_block_slots(bound, a.n_chunks), stream));
+  WP_HIP(launch_expand(dtype == WP_DTYPE_BF16, a, grid_block_slots(bound, a.n_ochunks), stream));
+  return WP_OK;
+}
+
+int wp_prefetch_adapter(wp_engine* e, int32_t adapter_id, int32_t* slot_out) {
+  if (!e || !slot_out) return fail(WP_ERR_INVALID, "prefetch_adapter: null argument");
+  *slot_out = -1;
+  auto it = e->adapters.find(adapter_id);
+  if (it == e->adapters.end()) return WP_OK;
+  // Existing slot for the id, else the first free one, else none
+  // (reference: StagingBufferPool::acquire_slot, staging_buffer.h:62-73).
+  int s = find_slot(e, adapter_id);
+  if (s < 0) {
+    for (size_t i = 0; i < e->slots.size(); ++i)
+      if (e->slots[i].adapter < 0) {
+        s = static_cast<int>(i);
+        break;
+      }
+  }
+  if (s < 0) return WP_OK;
+  DeviceGuard g(e->device);
+  Slot& sl = e->slots[s];
+  const Adapter& ad = it->second;
+  // Never overwrite buffers that queued kernels may still read.
+  if (sl.used) WP_HIP(hipStreamWaitEvent(e->pstream, sl.last_use, 0));
+  if (ad.copied) WP_HIP(hipStreamWaitEvent(e->pstream, ad.copied, 0));
+  if (sl.cap_a < ad.a_bytes) {
+    if (sl.A) WP_HIP(hipFreeAsync(sl.A, e->pstream));
+    sl.A = nullptr;
+    WP_HIP(hipMallocFromPoolAsync(&sl.A, ad.a_bytes, e->pool, e->pstream));
+    sl.cap_a = ad.a_bytes;
+  }
+  if (sl.cap_b < ad.b_bytes) {
+    if (sl.B) WP_HIP(hipFreeAsync(sl.B, e->pstream));
+    sl.B = nullptr;
+    WP_HIP(hipMallocFromPoolAsync(&sl.B, ad.b_bytes, e->pool, e->pstream));
+    sl.cap_b = ad.b_bytes;
+  }
+  const void* srcA = ad.hA ? ad.hA : ad.dA;
+  const void* srcB = ad.hB ? ad.hB : ad.dB;
+  const hipMemcpyKind kind = ad.hA ? hipMemcpyHostToDevice : hipMemcpyDeviceToDevice;
+  WP_HIP(hipMemcpyAsync(sl.A, srcA, ad.a_bytes, kind, e->pstream));
+  WP_HIP(hipMemcpyAsync(sl.B, srcB, ad.b_bytes, kind, e->pstream));
+  WP_HIP(hipEventRecord(sl.ready, e->pstream));
+  sl.adapter = adapter_id;
+  sl.issued = true;
+  e->table_dirty = true;
+  *slot_out = s;
+  return WP_OK;
+}
+
+int wp_is_prefetch_ready(wp_engine* e, int32_t adapter_id, int32_t* ready) {
+  if (!e || !ready) return fail(WP_ERR_INVALID, "is_prefetch_ready: null argument");
+  const int s = find_slot(e, adapter_id);
+  *ready = (s >= 0 && slot_ready(e->slots[s])) ? 1 : 0;
+  return WP_OK;
+}
+
+int wp_release_prefetch(wp_engine* e, int32_t adapter_id) {
+  if (!e) return fail(WP_ERR_INVALID, "release_prefetch: engine is NULL");
+  return release_slot(e, find_slot(e, adapter_id));
+}
+
+}  // extern "C"

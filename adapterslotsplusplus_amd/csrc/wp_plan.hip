@@ -1,0 +1,326 @@
+// wp_plan.hip -- once-per-step segment plan, built on the GPU (gfx950).
+//
+// Input: token_lora_indices[T] (int64 or int32) in HBM.  One workgroup builds,
+// with every intermediate held in LDS (gfx950: 160 KB per workgroup):
+//
+//   1. the exported segment table, bit-exact with the reference's
+//      build_seg_bounds_kernel (csrc/kernels/warp_pipe_r32.cu:461-512):
+//      maximal runs of equal ids in token order, ids < 0 skipped, every run
+//      split into pieces of 32 tokens (the last one takes the remainder),
+//      slots assigned in token-start order by an exclusive scan;
+//   2. the grouping the apply kernels run on (no reference counterpart): the
+//      runs are sorted by adapter id (bitonic sort of 64-bit (id, run) keys, so
+//      token order is kept inside an adapter), concatenated into `perm`, and
+//      each adapter's tokens are cut into blocks of kBlockTokens.  Every touched
+//      adapter's weights are then streamed once per block instead of once per
+//      run (about 232 runs vs 49 adapters for 256 Zipf-routed decode tokens).
+//
+// The reference uses one 256-thread block with a serial per-run scan and a
+// Hillis-Steele scan over shared memory, writing over PCIe into mapped host
+// memory.  Here: wave64 shuffle scans, LDS-resident arrays, HBM outputs written
+// by all threads in parallel (each output slot finds its run by binary search
+// over the scanned offsets), and capacities of 256 / 2048 / 8192 tokens.
+#include <hip/hip_runtime.h>
+
+#include "wp_types.h"
+
+namespace wp {
+namespace {
+
+// Exclusive scan of one int per thread across the workgroup.  `scratch` holds
+// NT/64 ints.  Returns the thread's exclusive prefix; *total gets the sum.
+// Begins and ends with a workgroup barrier.
+template <int NT>
+__device__ __forceinline__ int block_exclusive_scan(int v, int* scratch, int* total) {
+  constexpr int kWaves = NT / 64;
+  const int lane = threadIdx.x & 63;
+  const int wid = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off, 64);
+    if (lane >= off) x += y;
+  }
+  __syncthreads();
+  if (lane == 63) scratch[wid] = x;
+  __syncthreads();
+  if (wid == 0) {
+    int w = lane < kWaves ? scratch[lane] : 0;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(w, off, 64);
+      if (lane >= off) w += y;
+    }
+    if (lane < kWaves) scratch[lane] = w;
+  }
+  __syncthreads();
+  const int base = wid > 0 ? scratch[wid - 1] : 0;
+  *total = scratch[kWaves - 1];
+  __syncthreads();
+  return base + x - v;
+}
+
+// Largest i in [0, n) with a[i] <= q, for non-decreasing a and a[0] <= q.
+__device__ __forceinline__ int upper_index(const int* a, int n, int q) {
+  int lo = 0;
+  int hi = n - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (a[mid] <= q) {
+      lo = mid;
+    } else {
+      hi = mid - 1;
+    }
+  }
+  return lo;
+}
+
+template <int NT, int E>
+__global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, int idx_is_int64, int T,
+                                                  uint32_t* __restrict__ header, Segment* __restrict__ segments,
+                                                  Block* __restrict__ blocks, int32_t* __restrict__ perm, int seg_cap,
+                                                  int block_cap) {
+  constexpr int CAP = NT * E;
+  // s_big: the ids (int64) first, then the sort keys, then per-run offsets.
+  __shared__ unsigned long long s_big[CAP];
+  __shared__ int s_a[CAP + 1];  // run starts, later group adapter ids
+  __shared__ int s_b[CAP + 1];  // per-run segment bases, later group offsets
+  __shared__ int s_scan[NT / 64];
+  long long* s_id = reinterpret_cast<long long*>(s_big);
+
+  const int tid = threadIdx.x;
+  const int e0 = tid * E;
+
+  // 1. ids -> LDS.
+  for (int i = tid; i < CAP; i += NT) {
+    long long v = 0;
+    if (i < T) {
+      v = idx_is_int64 ? static_cast<const long long*>(idx)[i]
+                       : static_cast<long long>(static_cast<const int*>(idx)[i]);
+    }
+    s_id[i] = v;
+  }
+  __syncthreads();
+
+  // 2. Run starts in token order (reference :484): s_a[r] = first token of run r.
+  bool is_start[E];
+  int nstart = 0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int i = e0 + e;
+    is_start[e] = i < T && (i == 0 || s_id[i - 1] != s_id[i]);
+    nstart += is_start[e] ? 1 : 0;
+  }
+  int n_runs = 0;
+  int rb = block_exclusive_scan<NT>(nstart, s_scan, &n_runs);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    if (is_start[e]) s_a[rb++] = e0 + e;
+  }
+  if (tid == 0) s_a[n_runs] = T;
+  __syncthreads();
+
+  // 3. Exported table.  Pieces per run: ceil(len/32) when id >= 0 (reference
+  //    :485-489); slot bases by exclusive scan in token-start order (:494-503).
+  int pieces[E];
+  int psum = 0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int r = e0 + e;
+    pieces[e] = 0;
+    if (r < n_runs) {
+      const int st = s_a[r];
+      if (s_id[st] >= 0) pieces[e] = (s_a[r + 1] - st + kMaxSegmentTokens - 1) / kMaxSegmentTokens;
+    }
+    psum += pieces[e];
+  }
+  int n_segs = 0;
+  int sb = block_exclusive_scan<NT>(psum, s_scan, &n_segs);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int r = e0 + e;
+    if (r < n_runs) s_b[r] = sb;
+    sb += pieces[e];
+  }
+  if (tid == 0) s_b[n_runs] = n_segs;
+  __syncthreads();
+  const int seg_out = n_segs < seg_cap ? n_segs : seg_cap;
+  for (int q = tid; q < seg_out; q += NT) {
+    const int r = upper_index(s_b, n_runs, q);
+    const int st = s_a[r];
+    const int len = s_a[r + 1] - st;
+    const int p = q - s_b[r];
+    const int rem = len - p * kMaxSegmentTokens;
+    Segment s;
+    s.adapter_id = static_cast<int>(s_id[st]);
+    s.token_start = st + p * kMaxSegmentTokens;
+    s.token_count = rem < kMaxSegmentTokens ? rem : kMaxSegmentTokens;
+    s.pad = 0;
+    segments[q] = s;
+  }
+
+  // 4. Sort the runs with id >= 0 by (adapter id, run index).
+  unsigned long long key[E];
+  int nvalid = 0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int r = e0 + e;
+    key[e] = ~0ull;
+    if (r < n_runs) {
+      const long long id = s_id[s_a[r]];
+      if (id >= 0) {
+        key[e] = (static_cast<unsigned long long>(static_cast<unsigned>(static_cast<int>(id))) << 32) |
+                 static_cast<unsigned>(r);
+        ++nvalid;
+      }
+    }
+  }
+  int n_vruns = 0;
+  int vb = block_exclusive_scan<NT>(nvalid, s_scan, &n_vruns);  // ends every read of s_id
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    if (key[e] != ~0ull) s_big[vb++] = key[e];
+  }
+  int P = 1;
+  while (P < n_vruns) P <<= 1;
+  for (int i = n_vruns + tid; i < P; i += NT) s_big[i] = ~0ull;
+  __syncthreads();
+  for (int k = 2; k <= P; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = tid; i < P; i += NT) {
+        const int ixj = i ^ j;
+        if (ixj > i) {
+          const unsigned long long a = s_big[i];
+          const unsigned long long b = s_big[ixj];
+          const bool ascending = (i & k) == 0;
+          if ((a > b) == ascending) {
+            s_big[i] = b;
+            s_big[ixj] = a;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+
+  // 5. perm: the tokens of the sorted runs, concatenated.
+  int len_e[E];
+  int start_e[E];
+  int gid_e[E];
+  bool gstart[E];
+  int lsum = 0;
+  int gcount = 0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int p = e0 + e;
+    len_e[e] = 0;
+    start_e[e] = 0;
+    gid_e[e] = 0;
+    gstart[e] = false;
+    if (p < n_vruns) {
+      const unsigned long long kk = s_big[p];
+      const int r = static_cast<int>(kk & 0xffffffffull);
+      start_e[e] = s_a[r];
+      len_e[e] = s_a[r + 1] - s_a[r];
+      gid_e[e] = static_cast<int>(kk >> 32);
+      gstart[e] = p == 0 || (s_big[p - 1] >> 32) != (kk >> 32);
+    }
+    lsum += len_e[e];
+    gcount += gstart[e] ? 1 : 0;
+  }
+  int n_tok = 0;
+  int ob = block_exclusive_scan<NT>(lsum, s_scan, &n_tok);  // ends every read of s_big keys and s_a
+  int off_e[E];
+  int* s_roff = reinterpret_cast<int*>(s_big);           // [CAP] run offsets into perm
+  int* s_rstart = reinterpret_cast<int*>(s_big) + CAP;   // [CAP] run first tokens
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int p = e0 + e;
+    off_e[e] = ob;
+    if (p < n_vruns) {
+      s_roff[p] = ob;
+      s_rstart[p] = start_e[e];
+    }
+    ob += len_e[e];
+  }
+  __syncthreads();
+  for (int q = tid; q < n_tok; q += NT) {
+    const int p = upper_index(s_roff, n_vruns, q);
+    perm[q] = s_rstart[p] + (q - s_roff[p]);
+  }
+
+  // 6. Groups (one per adapter) and their blocks of kBlockTokens.
+  int n_groups = 0;
+  int gb = block_exclusive_scan<NT>(gcount, s_scan, &n_groups);  // ends every read of s_roff / s_rstart
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    if (gstart[e]) {
+      s_b[gb] = off_e[e];
+      s_a[gb] = gid_e[e];
+      ++gb;
+    }
+  }
+  if (tid == 0) s_b[n_groups] = n_tok;
+  __syncthreads();
+  int nb[E];
+  int bsum = 0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int g = e0 + e;
+    nb[e] = g < n_groups ? (s_b[g + 1] - s_b[g] + kBlockTokens - 1) / kBlockTokens : 0;
+    bsum += nb[e];
+  }
+  int n_blocks = 0;
+  int bb = block_exclusive_scan<NT>(bsum, s_scan, &n_blocks);
+  int* s_bbase = reinterpret_cast<int*>(s_big);  // [CAP] first block of each group
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int g = e0 + e;
+    if (g < n_groups) s_bbase[g] = bb;
+    bb += nb[e];
+  }
+  __syncthreads();
+  const int blk_out = n_blocks < block_cap ? n_blocks : block_cap;
+  for (int q = tid; q < blk_out; q += NT) {
+    const int g = upper_index(s_bbase, n_groups, q);
+    const int j = q - s_bbase[g];
+    const int n = s_b[g + 1] - s_b[g];
+    Block b;
+    b.adapter_id = s_a[g];
+    b.first = s_b[g] + j * kBlockTokens;
+    b.count = n - j * kBlockTokens < kBlockTokens ? n - j * kBlockTokens : kBlockTokens;
+    b.entry = s_a[g];
+    blocks[q] = b;
+  }
+
+  if (tid == 0) {
+    header[kHdrNumSegments] = static_cast<uint32_t>(n_segs);
+    header[kHdrNumBlocks] = static_cast<uint32_t>(blk_out);
+    header[kHdrNumGroups] = static_cast<uint32_t>(n_groups);
+    header[kHdrNumValid] = static_cast<uint32_t>(n_tok);
+    header[kHdrT] = static_cast<uint32_t>(T);
+  }
+}
+
+}  // namespace
+
+// Host launcher: the smallest capacity variant that holds T.
+hipError_t launch_plan(const void* idx, int idx_is_int64, int T, uint32_t* header, Segment* segments, Block* blocks,
+                       int32_t* perm, int seg_cap, int block_cap, hipStream_t stream) {
+  if (T < 0) return hipErrorInvalidValue;
+  if (T <= 256) {
+    plan_kernel<256, 1><<<1, 256, 0, stream>>>(idx, idx_is_int64, T, header, segments, blocks, perm, seg_cap,
+                                               block_cap);
+  } else if (T <= 2048) {
+    plan_kernel<1024, 2><<<1, 1024, 0, stream>>>(idx, idx_is_int64, T, header, segments, blocks, perm, seg_cap,
+                                                 block_cap);
+  } else if (T <= kPlanMaxTokens) {
+    plan_kernel<1024, 8><<<1, 1024, 0, stream>>>(idx, idx_is_int64, T, header, segments, blocks, perm, seg_cap,
+                                                 block_cap);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace wp

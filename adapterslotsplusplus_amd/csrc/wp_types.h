@@ -1,0 +1,109 @@
+// wp_types.h -- layouts shared by the host engine and the gfx950 kernels.
+//
+// Device-resident plan of one decode step (all in one engine-owned allocation):
+//
+//   header[16]    u32  num_segments, num_blocks, num_groups, num_valid_tokens, T, errors
+//   segments[]    Segment  the exported run-length table, bit-exact with the
+//                          reference's build_seg_bounds (warp_pipe_r32.cu:461-512)
+//   blocks[]      Block    work units: <= kBlockTokens tokens of ONE adapter
+//   perm[]        i32      token indices grouped by adapter (blocks index into it)
+//   counters[]    u32      per-block arrival counters of the split-K shrink
+//
+// The reference keeps its table in mapped pinned host memory that every kernel
+// block reads over PCIe (warp_pipe_bindings.cpp:21-27).  Here it lives in HBM
+// and is written either by the plan kernel or by a stream-ordered upload.
+#pragma once
+
+#include <stdint.h>
+
+namespace wp {
+
+// Longest segment of the exported table: WP_MAX_SEGMENT_TOKENS,
+// csrc/bridge/warp_pipe_metadata.h:22.
+constexpr int kMaxSegmentTokens = 32;
+// The reference's table capacity WP_MAX_SEGMENTS (warp_pipe_metadata.h:10);
+// build_segments keeps it as its K limit (segment_builder.cpp:12-14).
+constexpr int kRefMaxSegments = 256;
+// Tokens per work block: one adapter's weights are streamed once per block.
+constexpr int kBlockTokens = 64;
+// Largest T the on-device plan builder takes in one workgroup (LDS-resident).
+constexpr int kPlanMaxTokens = 8192;
+// Output slices one add_lora call may expand into (q/k/v/...).
+constexpr int kMaxSlices = 4;
+// Largest rank.
+constexpr int kMaxRank = 64;
+
+enum HeaderWord : int {
+  kHdrNumSegments = 0,
+  kHdrNumBlocks = 1,
+  kHdrNumGroups = 2,
+  kHdrNumValid = 3,
+  kHdrT = 4,
+  kHdrErrors = 5,
+  kHdrWords = 16
+};
+
+// Bits of header[kHdrErrors], set by kernels that had to skip work.
+enum DeviceError : uint32_t {
+  kErrIdRange = 1u,       // stacked weights: adapter id >= num_loras
+  kErrUnregistered = 2u,  // adapter table: id not registered / not resident
+  kErrShape = 4u          // adapter rank / d / o differs from the call's
+};
+
+struct Segment {  // 16 B; the reference descriptor's first three fields
+  int32_t adapter_id;
+  int32_t token_start;
+  int32_t token_count;
+  int32_t pad;
+};
+
+struct Block {  // 16 B
+  int32_t adapter_id;
+  int32_t first;  // offset into perm
+  int32_t count;  // 1..kBlockTokens
+  int32_t entry;  // index into the call's adapter-entry table
+};
+
+struct Entry {  // 32 B: one registered adapter as the kernels see it
+  uint64_t a_ptr;  // [rank, d] (0: not usable)
+  uint64_t b_ptr;  // [o, rank]
+  float alpha;
+  int32_t rank;
+  int32_t d_model;
+  int32_t out_features;
+};
+
+static_assert(sizeof(Segment) == 16, "Segment layout");
+static_assert(sizeof(Block) == 16, "Block layout");
+static_assert(sizeof(Entry) == 32, "Entry layout");
+
+// How a block finds its adapter's weights.
+enum WeightsMode : int32_t {
+  kStacked = 0,  // A = a_base + id * a_stride (vLLM wa_t_all / wb_t_all)
+  kTable = 1     // entries[block.entry]
+};
+
+struct Weights {
+  int32_t mode;
+  int32_t num_ids;  // stacked: L; table: number of entries
+  const void* a_base;
+  int64_t a_stride;  // elements
+  float scale;       // stacked: the call's scale
+  const Entry* entries;
+  int32_t n_slices;
+  int32_t oc_start[kMaxSlices + 1];  // prefix of o-chunks per slice
+  const void* b_base[kMaxSlices];
+  int64_t b_stride[kMaxSlices];
+  int32_t o_size[kMaxSlices];
+  int32_t y_off[kMaxSlices];
+};
+
+struct PlanView {
+  uint32_t* header;
+  const Segment* segments;
+  const Block* blocks;
+  const int32_t* perm;
+  uint32_t* counters;
+};
+
+}  // namespace wp

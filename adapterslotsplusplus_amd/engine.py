@@ -1,0 +1,295 @@
+"""WarpPipeEngine -- the drop-in Python surface of the grouped multi-LoRA apply.
+
+Mirrors lora_warp_pipe/engine.py:7-69 of the reference (same method names,
+argument order, return conventions and errors) on top of the MI355X C ABI
+(include/warppipe_mi355x.h, libwarppipe_mi355x.so).  PyTorch provides device
+memory and the current stream; all compute is in the library's HIP kernels.
+
+Conventions kept from the reference:
+  * errors raise RuntimeError (TORCH_CHECK / std::runtime_error there);
+  * "cannot handle" returns False (build_seg_bounds above capacity,
+    add_lora_packed for a rank without kernels) or -1 (prefetch_adapter);
+  * compute is enqueued on torch's current stream, prefetch on a private stream;
+  * shrink() returns a new zero-initialised H [T, rank]; expand() updates Y in place.
+
+Additions (each a superset of the reference behaviour):
+  * fp16 and bf16, ranks 8/16/32/64 on every path (the reference: fp16 only;
+    add_lora_packed and build_seg_bounds rank 32 only);
+  * shrink/expand also run on a build_seg_bounds table, through the adapter
+    store (the reference reads stale pointers there);
+  * rank=0 in shrink/expand selects mixed ranks (each adapter's own rank);
+  * add_lora_packed takes y_offset / y_slice_size, and add_lora_slices
+    expands one shared H into several output slices (packed q/k/v);
+  * register_adapter with CPU tensors puts the adapter in the pinned host
+    store; prefetch_adapter then stages it in HBM.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import List, Optional, Sequence, Tuple
+
+import torch
+
+from . import _lib
+from .config import WarpPipeConfig
+
+_DTYPES = {torch.float16: _lib.WP_DTYPE_F16, torch.bfloat16: _lib.WP_DTYPE_BF16}
+
+
+def _dtype_code(t: torch.Tensor, what: str) -> int:
+    code = _DTYPES.get(t.dtype)
+    if code is None:
+        raise RuntimeError(f"{what} must be fp16 or bf16, got {t.dtype}")
+    return code
+
+
+def _ptr(t: torch.Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(t.data_ptr())
+
+
+class _Ext:
+    """Stand-in for the reference's `engine._ext` extension object: exposes the
+    free functions tests call on it (test_rank_variants.py:97-103)."""
+
+    def __init__(self, lib):
+        self._lib = lib
+
+    def rank_supported(self, rank: int) -> bool:
+        return bool(self._lib.wp_rank_supported(int(rank)))
+
+
+class WarpPipeEngine:
+    def __init__(self, config: Optional[WarpPipeConfig] = None):
+        self.config = config or WarpPipeConfig()
+        self._lib = _lib.load()
+        self._ext = _Ext(self._lib)
+        self._handle = ctypes.c_void_p(None)
+        dev = self.config.device
+        if dev is None:
+            if not torch.cuda.is_available():
+                raise RuntimeError("WarpPipeEngine: no GPU available (the apply runs only on the GPU)")
+            dev = torch.cuda.current_device()
+        self.device = torch.device("cuda", int(dev))
+        cfg = _lib.WpConfig(int(dev), int(self.config.num_staging_slots), int(self.config.max_tokens), 64)
+        _lib.check(self._lib.wp_create(ctypes.byref(cfg), ctypes.byref(self._handle)), "WarpPipeEngine")
+        self._held = {}
+
+    # ------------------------------------------------------------ lifetime --
+    def close(self) -> None:
+        h = getattr(self, "_handle", None)
+        if h is not None and h.value:
+            self._lib.wp_destroy(h)
+            self._handle = ctypes.c_void_p(None)
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _stream(self) -> ctypes.c_void_p:
+        return ctypes.c_void_p(torch.cuda.current_stream(self.device).cuda_stream)
+
+    def _on_device(self, t: torch.Tensor, what: str) -> None:
+        if not t.is_cuda:
+            raise RuntimeError(f"{what} must be a CUDA tensor")
+        if t.device != self.device:
+            raise RuntimeError(f"{what} is on {t.device}, the engine on {self.device}")
+
+    # ------------------------------------------------------- adapter store --
+    def register_adapter(self, adapter_id, A, B, alpha_scale, rank=None):
+        """A [rank, d], B [o, rank], contiguous fp16/bf16 (reference engine.py:12-14,
+        bindings:110-119).  CUDA tensors: the adapter is device-resident.  CPU
+        tensors: it goes to the pinned host store and is usable once prefetched."""
+        rank = int(rank or self.config.rank)
+        if A.is_cuda != B.is_cuda:
+            raise RuntimeError("A/B must both be CUDA tensors or both CPU tensors")
+        if A.is_cuda:
+            self._on_device(A, "A")
+            self._on_device(B, "B")
+        if A.dtype != B.dtype:
+            raise RuntimeError("A/B must have the same dtype")
+        dt = _dtype_code(A, "A/B")
+        if not (A.is_contiguous() and B.is_contiguous()):
+            raise RuntimeError("A/B must be contiguous")
+        d_model = int(A.size(-1))
+        out_features = int(B.size(-2)) if B.dim() >= 2 else 0
+        if A.numel() != rank * d_model or B.numel() != out_features * rank or int(B.size(-1)) != rank:
+            raise RuntimeError(
+                f"A must be [rank={rank}, d] and B [o, rank={rank}]; got {tuple(A.shape)} and {tuple(B.shape)}")
+        host = 0 if A.is_cuda else 1
+        _lib.check(self._lib.wp_register_adapter(self._handle, int(adapter_id), _ptr(A), _ptr(B), rank, d_model,
+                                                 out_features, float(alpha_scale), dt, host, self._stream()),
+                   "register_adapter")
+        # Keeps the source alive until the stream-ordered copy has run (the
+        # reference holds the tensors until eviction as well, bindings:118).
+        self._held[int(adapter_id)] = (A, B) if host == 0 else None
+
+    def evict_adapter(self, adapter_id):
+        _lib.check(self._lib.wp_evict_adapter(self._handle, int(adapter_id), self._stream()), "evict_adapter")
+        self._held.pop(int(adapter_id), None)
+
+    # ------------------------------------------------------ segment tables --
+    def build_segments(self, sorted_adapter_ids, seg_offsets):
+        ids = [int(v) for v in sorted_adapter_ids]
+        offs = [int(v) for v in seg_offsets]
+        ids_c = (ctypes.c_int32 * max(len(ids), 1))(*ids)
+        offs_c = (ctypes.c_int32 * max(len(offs), 1))(*offs)
+        _lib.check(self._lib.wp_build_segments(self._handle, ids_c, len(ids), offs_c, len(offs), self._stream()),
+                   "build_segments")
+
+    def build_seg_bounds(self, token_lora_indices) -> bool:
+        """Builds the step's segment table on the GPU; False iff the token count
+        exceeds config.max_tokens (reference: engine.py:28-32, bindings:162-170)."""
+        idx = token_lora_indices
+        if not isinstance(idx, torch.Tensor) or not idx.is_cuda:
+            raise RuntimeError("build_seg_bounds: token_lora_indices must be a CUDA tensor")
+        self._on_device(idx, "token_lora_indices")
+        if idx.dtype not in (torch.int64, torch.int32):
+            idx = idx.to(torch.int64)
+        idx = idx.reshape(-1)
+        if not idx.is_contiguous():
+            idx = idx.contiguous()
+        T = int(idx.numel())
+        rc = _lib.check(self._lib.wp_build_seg_bounds(self._handle, _ptr(idx), 1 if idx.dtype == torch.int64 else 0,
+                                                      T, self._stream()), "build_seg_bounds")
+        return rc == _lib.WP_OK
+
+    def read_segments(self) -> List[Tuple[int, int, int]]:
+        """The current segment table as (adapter_id, token_start, token_count)
+        tuples (synchronises the current stream; for tests and debugging)."""
+        cap = max(int(self.config.max_tokens), 256)
+        buf = (ctypes.c_int32 * (3 * cap))()
+        n = ctypes.c_int64(0)
+        _lib.check(self._lib.wp_read_segments(self._handle, buf, cap, ctypes.byref(n), self._stream()),
+                   "read_segments")
+        m = min(n.value, cap)
+        return [(buf[3 * i], buf[3 * i + 1], buf[3 * i + 2]) for i in range(m)]
+
+    def read_plan(self):
+        """(perm, blocks) of the current plan: the token order grouped by
+        adapter and the (adapter_id, first, count, entry) work blocks."""
+        cap = int(self.config.max_tokens)
+        bcap = cap + 256
+        perm = (ctypes.c_int32 * cap)()
+        blocks = (ctypes.c_int32 * (4 * bcap))()
+        nv = ctypes.c_int64(0)
+        nb = ctypes.c_int64(0)
+        _lib.check(self._lib.wp_read_plan(self._handle, perm, cap, blocks, bcap, ctypes.byref(nv), ctypes.byref(nb),
+                                          self._stream()), "read_plan")
+        return (list(perm[: min(nv.value, cap)]),
+                [tuple(blocks[4 * i: 4 * i + 4]) for i in range(min(nb.value, bcap))])
+
+    def device_errors(self) -> int:
+        """Reads and clears the device error word (adapters the kernels had to
+        skip: id out of range / unregistered / shape mismatch)."""
+        v = ctypes.c_uint32(0)
+        _lib.check(self._lib.wp_read_device_errors(self._handle, ctypes.byref(v), self._stream()), "device_errors")
+        return int(v.value)
+
+    # --------------------------------------------------------------- apply --
+    def shrink(self, X, d_model, rank, total_tokens):
+        """H = rn(alpha * X . A^T) per segment; returns a new zero-initialised
+        [total_tokens, rank] tensor (reference bindings:132-139).  rank=0 or
+        None: mixed ranks, H is [T, 64] with each row's first r_a columns set."""
+        rank = int(rank or 0)
+        self._on_device(X, "X")
+        dt = _dtype_code(X, "X")
+        if not X.is_contiguous():
+            raise RuntimeError("X must be contiguous")
+        T = int(total_tokens)
+        if X.numel() < T * int(d_model):
+            raise RuntimeError(f"X has {X.numel()} elements, fewer than total_tokens x d_model")
+        width = rank if rank else 64
+        H = torch.zeros(T, width, dtype=X.dtype, device=X.device)
+        _lib.check(self._lib.wp_shrink(self._handle, _ptr(X), _ptr(H), int(d_model), rank, T, width, dt,
+                                       self._stream()), "shrink")
+        return H
+
+    def expand(self, H, Y, out_features, rank, y_offset: int = 0):
+        """Y[:, y_offset:y_offset+o] += H . B^T per segment, in place
+        (reference bindings:141-148)."""
+        rank = int(rank or 0)
+        self._on_device(H, "H")
+        self._on_device(Y, "Y")
+        if H.dtype != Y.dtype:
+            raise RuntimeError("H/Y must have the same dtype")
+        dt = _dtype_code(Y, "Y")
+        if not (H.is_contiguous() and Y.is_contiguous()):
+            raise RuntimeError("H/Y must be contiguous")
+        T = int(Y.size(0))
+        _lib.check(self._lib.wp_expand(self._handle, _ptr(H), _ptr(Y), int(out_features), rank, T, int(H.size(-1)),
+                                       int(Y.size(-1)), int(y_offset), dt, self._stream()), "expand")
+
+    def add_lora_packed(self, y, x, wa_t_all, wb_t_all, scale, y_offset=None, y_slice_size=None) -> bool:
+        """y += (scale * x . A[idx]^T) . B[idx]^T for the tokens of the last
+        build_seg_bounds table (reference engine.py:56-62, bindings:195-234).
+        Returns False (caller falls back) only for a rank without kernels."""
+        off = int(y_offset or 0)
+        return self.add_lora_slices(y, x, wa_t_all, [wb_t_all], scale, [off],
+                                    [y_slice_size] if y_slice_size is not None else None)
+
+    def add_lora_slices(self, y, x, wa_t_all, wb_t_alls: Sequence[torch.Tensor], scale,
+                        y_offsets: Sequence[int], y_slice_sizes: Optional[Sequence[int]] = None) -> bool:
+        """One shrink, several expands: each wb_t_alls[i] ([L, 1, o_i, r]) writes
+        columns [y_offsets[i], y_offsets[i] + o_i) of y (packed q/k/v)."""
+        rank = int(wb_t_alls[0].size(-1))
+        if not self._ext.rank_supported(rank):
+            return False
+        self._on_device(x, "x")
+        self._on_device(y, "y")
+        dt = _dtype_code(x, "x")
+        if y.dtype != x.dtype or wa_t_all.dtype != x.dtype or any(w.dtype != x.dtype for w in wb_t_alls):
+            raise RuntimeError("add_lora_packed: x, y and the LoRA weights must share one dtype")
+        x2 = x.reshape(-1, x.size(-1))
+        y2 = y.reshape(-1, y.size(-1))
+        if not (x2.is_contiguous() and y2.is_contiguous()):
+            raise RuntimeError("add_lora_packed: x/y must be contiguous")
+        if y2.data_ptr() != y.data_ptr():
+            raise RuntimeError("add_lora_packed: y must be viewable as 2-D in place")
+        if not wa_t_all.is_contiguous() or not all(w.is_contiguous() for w in wb_t_alls):
+            raise RuntimeError("add_lora_packed: wa_t_all/wb_t_all must be contiguous")
+        self._on_device(wa_t_all, "wa_t_all")
+        T = int(x2.size(0))
+        d_model = int(x2.size(1))
+        L = int(wa_t_all.size(0))
+        if int(wa_t_all.size(-1)) != d_model or int(wa_t_all.size(-2)) != rank:
+            raise RuntimeError(f"add_lora_packed: wa_t_all {tuple(wa_t_all.shape)} does not match x and rank {rank}")
+        n = len(wb_t_alls)
+        outs = []
+        for i, w in enumerate(wb_t_alls):
+            self._on_device(w, "wb_t_all")
+            if int(w.size(0)) != L or int(w.size(-1)) != rank:
+                raise RuntimeError(f"add_lora_packed: wb_t_all {tuple(w.shape)} does not match wa_t_all")
+            o = int(w.size(-2))
+            if y_slice_sizes is not None and y_slice_sizes[i] is not None and int(y_slice_sizes[i]) != o:
+                raise RuntimeError(f"add_lora_packed: y_slice_size {y_slice_sizes[i]} != wb_t_all rows {o}")
+            outs.append(o)
+        if int(y2.size(0)) != T:
+            raise RuntimeError("add_lora_packed: x and y have different token counts")
+        wb_ptrs = (ctypes.c_void_p * n)(*[w.data_ptr() for w in wb_t_alls])
+        wb_strides = (ctypes.c_int64 * n)(*[int(w.stride(0)) for w in wb_t_alls])
+        o_arr = (ctypes.c_int32 * n)(*outs)
+        off_arr = (ctypes.c_int32 * n)(*[int(v) for v in y_offsets])
+        rc = _lib.check(self._lib.wp_add_lora(self._handle, _ptr(y2), _ptr(x2), _ptr(wa_t_all),
+                                              int(wa_t_all.stride(0)), L, n, wb_ptrs, wb_strides, o_arr, off_arr,
+                                              float(scale), rank, d_model, T, int(y2.size(1)), dt, self._stream()),
+                        "add_lora_packed")
+        return rc == _lib.WP_OK
+
+    # ------------------------------------------------------------- staging --
+    def prefetch_adapter(self, adapter_id) -> int:
+        """Stages the adapter's A/B in a slot on the prefetch stream; returns the
+        slot index or -1 (unknown id / pool exhausted) (reference bindings:46-57)."""
+        slot = ctypes.c_int32(-1)
+        _lib.check(self._lib.wp_prefetch_adapter(self._handle, int(adapter_id), ctypes.byref(slot)),
+                   "prefetch_adapter")
+        return int(slot.value)
+
+    def is_prefetch_ready(self, adapter_id) -> bool:
+        r = ctypes.c_int32(0)
+        _lib.check(self._lib.wp_is_prefetch_ready(self._handle, int(adapter_id), ctypes.byref(r)), "is_prefetch_ready")
+        return bool(r.value)
+
+    def release_prefetch(self, adapter_id):
+        _lib.check(self._lib.wp_release_prefetch(self._handle, int(adapter_id)), "release_prefetch")

@@ -1,0 +1,176 @@
+/*
+ * warppipe_mi355x.h -- C ABI of the MI355X (gfx950) grouped multi-LoRA apply.
+ *
+ * This is the drop-in boundary that replaces the reference's pybind11 class
+ * `warp_pipe_ext.WarpPipeExtension` (csrc/pybind/warp_pipe_bindings.cpp:18-300).
+ * Everything is plain C: opaque handle, raw device pointers, sizes, and a
+ * hipStream_t passed as void*.  No torch types cross this boundary; the Python
+ * engine (adapterslotsplusplus_amd/engine.py) binds it with ctypes.
+ *
+ * Conventions (reference: warp_pipe_bindings.cpp, engine.py):
+ *   - Every call returns an int status.  WP_OK = 0.  WP_NOT_HANDLED = 1 is the
+ *     reference's "return False / -1, caller falls back" convention.  Negative
+ *     values are errors; the reference raises RuntimeError for these
+ *     (TORCH_CHECK / std::runtime_error), and wp_last_error() returns the
+ *     message of the last failing call on the calling thread.
+ *   - Compute is enqueued on the caller's stream (the reference uses torch's
+ *     current stream, bindings:135,145,167,211).  Nothing on the compute path
+ *     synchronises the host.
+ *   - Tensors are row-major.  X [T, d], H [T, rank], Y rows of `y_row_stride`
+ *     elements.  A_seg is [rank, d] and B_seg is [o, rank] (bindings:114-115).
+ *   - dtype: WP_DTYPE_F16 or WP_DTYPE_BF16 for X, A, B, H, Y alike; all
+ *     accumulation is fp32.
+ */
+#ifndef WARPPIPE_MI355X_H
+#define WARPPIPE_MI355X_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WP_ABI_VERSION 1
+
+enum wp_status {
+  WP_OK = 0,
+  WP_NOT_HANDLED = 1,
+  WP_ERR_INVALID = -1,          /* bad argument (shape, dtype, alignment, rank) */
+  WP_ERR_HIP = -2,              /* a HIP runtime call failed */
+  WP_ERR_UNKNOWN_ADAPTER = -3,  /* adapter id not registered */
+  WP_ERR_CAPACITY = -4,         /* a table or pool limit was exceeded */
+  WP_ERR_NO_DEVICE = -5,        /* no usable GPU */
+  WP_ERR_STATE = -6             /* call not valid in the engine's current state */
+};
+
+enum wp_dtype { WP_DTYPE_F16 = 0, WP_DTYPE_BF16 = 1 };
+
+typedef struct wp_engine wp_engine;
+
+typedef struct wp_config {
+  int32_t device;             /* HIP device ordinal */
+  int32_t num_staging_slots;  /* reference: WP_MAX_STAGING = 8 (warp_pipe_metadata.h:11) */
+  int32_t max_tokens;         /* largest T accepted by build_seg_bounds (reference: 256) */
+  int32_t max_rank;           /* largest adapter rank (64) */
+} wp_config;
+
+/* ---- library ---------------------------------------------------------- */
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* wp_last_error(void);
+
+/* ABI version (WP_ABI_VERSION). */
+int wp_abi_version(void);
+
+/* 1 if rank has a compiled kernel specialisation (8, 16, 32, 64), else 0.
+ * Replaces WarpPipeExtension::rank_supported (bindings:126) /
+ * warp_pipe_rank_supported (csrc/dispatch/warp_pipe_dispatcher.cpp:18). */
+int wp_rank_supported(int32_t rank);
+
+/* ---- engine lifetime ---------------------------------------------------- */
+
+/* Replaces WarpPipeExtension::WarpPipeExtension (bindings:20-34): creates the
+ * per-engine segment table, staging slots and prefetch stream.  cfg may be
+ * NULL for the defaults.  Fails with WP_ERR_NO_DEVICE when no GPU is usable. */
+int wp_create(const wp_config* cfg, wp_engine** out);
+
+/* Replaces ~WarpPipeExtension (bindings:36-39). Synchronises the device. */
+int wp_destroy(wp_engine* e);
+
+/* ---- adapter store ------------------------------------------------------ */
+
+/* Replaces WarpPipeExtension::register_adapter (bindings:110-119) and
+ * AdapterStore::register_adapter (csrc/memory/adapter_store.h:21-27).
+ * A is [rank, d], B is [o, rank], both contiguous.  The weights are copied into
+ * engine-owned memory: device-resident (a stream-ordered pool allocation) when
+ * `host_resident` is 0 and A/B are device pointers, or into the pinned host
+ * store when `host_resident` is 1 and A/B are host pointers (such an adapter
+ * is usable once prefetched).  Re-registering an id replaces it. */
+int wp_register_adapter(wp_engine* e, int32_t adapter_id, const void* A, const void* B, int32_t rank,
+                        int32_t d_model, int32_t out_features, float alpha_scale, int32_t dtype,
+                        int32_t host_resident, void* stream);
+
+/* Replaces WarpPipeExtension::evict_adapter (bindings:121-124).  Silent for an
+ * unknown id (adapter_store.h:29).  Also releases a staging slot held by the id. */
+int wp_evict_adapter(wp_engine* e, int32_t adapter_id, void* stream);
+
+/* 1 if the id is registered, 0 otherwise. */
+int wp_has_adapter(wp_engine* e, int32_t adapter_id);
+
+/* ---- segment tables ----------------------------------------------------- */
+
+/* Replaces WarpPipeExtension::build_segments (bindings:128-130) /
+ * build_segment_table (csrc/dispatch/segment_builder.cpp:5-50).  One segment
+ * per (ids[k], offsets[k], offsets[k+1]-offsets[k]); n_offsets must be K+1 and
+ * K at most max_segments.  The table is uploaded stream-ordered on `stream`. */
+int wp_build_segments(wp_engine* e, const int32_t* sorted_adapter_ids, int32_t K, const int32_t* seg_offsets,
+                      int32_t n_offsets, void* stream);
+
+/* Replaces WarpPipeExtension::build_seg_bounds (bindings:162-170) and
+ * build_seg_bounds_kernel (csrc/kernels/warp_pipe_r32.cu:461-512).  idx is a
+ * device array of T token->adapter ids (int64 if idx_is_int64, else int32).
+ * Builds, on the device, the run-length segment table (bit-exact with the
+ * reference) and the by-adapter token grouping the apply kernels use.
+ * Returns WP_NOT_HANDLED (reference: False, no launch) when T > max_tokens. */
+int wp_build_seg_bounds(wp_engine* e, const void* idx, int32_t idx_is_int64, int64_t T, void* stream);
+
+/* Test/debug readback (synchronous on `stream`): copies the current segment
+ * table as int32 triples (adapter_id, token_start, token_count) into host
+ * memory `out` (capacity cap triples) and the count into *num_segments. */
+int wp_read_segments(wp_engine* e, int32_t* out, int64_t cap, int64_t* num_segments, void* stream);
+
+/* Test/debug readback of the grouped plan (synchronous): perm[n_valid],
+ * blocks as int32 quads (adapter_id, first, count, entry) and the counts. */
+int wp_read_plan(wp_engine* e, int32_t* perm, int64_t perm_cap, int32_t* blocks, int64_t block_cap,
+                 int64_t* n_valid, int64_t* n_blocks, void* stream);
+
+/* Reads and clears the device error word (bit flags, see wp_types.h). */
+int wp_read_device_errors(wp_engine* e, uint32_t* flags, void* stream);
+
+/* ---- apply ---------------------------------------------------------------- */
+
+/* Replaces WarpPipeExtension::shrink (bindings:132-139) and
+ * dispatch_bgmv_shrink (warp_pipe_dispatcher.cpp:33-42):
+ *   H[t, :rank_a] = rn(alpha_a * X[t, :] . A_a^T) for every segment token.
+ * H must be zero-initialised by the caller ([T, h_row_stride]).  rank = 0
+ * selects mixed-rank mode (each adapter's own rank, h_row_stride >= 64). */
+int wp_shrink(wp_engine* e, const void* X, void* H, int32_t d_model, int32_t rank, int64_t T,
+              int64_t h_row_stride, int32_t dtype, void* stream);
+
+/* Replaces WarpPipeExtension::expand (bindings:141-148):
+ *   Y[t, off + o] = rn(Y[t, off + o] + H[t, :] . B_a[o, :]) for every segment token. */
+int wp_expand(wp_engine* e, const void* H, void* Y, int32_t out_features, int32_t rank, int64_t T,
+              int64_t h_row_stride, int64_t y_row_stride, int32_t y_col_offset, int32_t dtype, void* stream);
+
+/* Replaces WarpPipeExtension::add_lora_packed (bindings:195-234) and the DSAK
+ * kernels (warp_pipe_r32.cu:280-423), generalised to ranks 8/16/32/64, bf16,
+ * and n_slices (1..4) output slices sharing one H:
+ *   h = rn(scale * x[t] . wa[id]^T);  y[t, y_off[s] + o] = rn(y[...] + h . wb_s[id][o, :])
+ * for every token t of the last build_seg_bounds table (ids < 0 untouched).
+ * wa: [L, rank, d] with element stride wa_stride0 between adapters;
+ * wb[s]: [L, o[s], rank] with element stride wb_stride0[s]. */
+int wp_add_lora(wp_engine* e, void* y, const void* x, const void* wa, int64_t wa_stride0, int32_t num_loras,
+                int32_t n_slices, const void* const* wb, const int64_t* wb_stride0, const int32_t* out_features,
+                const int32_t* y_col_offsets, float scale, int32_t rank, int32_t d_model, int64_t T,
+                int64_t y_row_stride, int32_t dtype, void* stream);
+
+/* ---- staging / prefetch ---------------------------------------------------- */
+
+/* Replaces WarpPipeExtension::prefetch_adapter (bindings:46-57): copies the
+ * adapter's A and B into a staging slot on the engine's prefetch stream (H2D
+ * from the pinned host store, or D2D).  Writes the slot index, or -1 when the
+ * id is unknown or every slot is taken (*slot_out). */
+int wp_prefetch_adapter(wp_engine* e, int32_t adapter_id, int32_t* slot_out);
+
+/* Replaces is_prefetch_ready (bindings:59-62): *ready = 1 once the copy completed. */
+int wp_is_prefetch_ready(wp_engine* e, int32_t adapter_id, int32_t* ready);
+
+/* Replaces release_prefetch (bindings:64): frees the id's slot (no-op without one).
+ * The slot's buffers are not overwritten before kernels that read them finished. */
+int wp_release_prefetch(wp_engine* e, int32_t adapter_id);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WARPPIPE_MI355X_H */

@@ -1,0 +1,357 @@
+"""GPU parity of shrink / expand / add_lora against the CPU oracle.
+
+Each test mirrors a reference test (cited) on identical seeded inputs drawn on
+the CPU, at the north-star tolerance |dev - ref| <= 1e-3 + 1e-2 |ref|
+(bf16 / fp16 I/O, fp32 accumulation)."""
+import numpy as np
+import pytest
+import torch
+
+from adapterslotsplusplus_amd import WarpPipeEngine
+from oracle import bgmv
+from oracle import segments as so
+from tests.helpers import announce, assert_close, randn
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.float16, torch.bfloat16]
+
+
+def register(engine, K, rank, d, o, dtype, seed, alpha, ids=None):
+    A = randn((K, rank, d), seed, dtype, 0.02)
+    B = randn((K, o, rank), seed + 1, dtype, 0.02)
+    ids = list(range(K)) if ids is None else ids
+    adapters = {}
+    for i, aid in enumerate(ids):
+        engine.register_adapter(aid, A[i].cuda().contiguous(), B[i].cuda().contiguous(), alpha, rank=rank)
+        adapters[aid] = (A[i], B[i], alpha)
+    return adapters
+
+
+def run_host_path(engine, adapters, ids, offsets, X, Y0, d, o, rank):
+    engine.build_segments(ids, offsets)
+    T = X.shape[0]
+    H = engine.shrink(X.cuda(), d, rank, T)
+    Y = Y0.cuda().clone()
+    engine.expand(H, Y, o, rank)
+    torch.cuda.synchronize()
+    segs = so.segment_table(ids, offsets).tolist()
+    H_ref = bgmv.shrink(X, segs, adapters, rank if rank else 64, T)
+    Y_ref = bgmv.expand(H_ref, Y0, segs, adapters)
+    return H, Y, H_ref, Y_ref
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_bgmv_correctness_grid(dtype):
+    """tests/correctness/test_bgmv_correctness.py:17-60: K x T grid, r=32, d=o=4096."""
+    for K in [1, 2, 4, 8]:
+        for T in [1, 4, 8, 16]:
+            announce(f"bgmv grid K={K} T={T} {dtype}")
+            engine = WarpPipeEngine()
+            adapters = register(engine, K, 32, 4096, 4096, dtype, K * 1000 + T, 16.0 / 32)
+            X = randn((K * T, 4096), K * 7 + T, dtype, 0.1)
+            Y0 = randn((K * T, 4096), K * 11 + T, dtype, 0.1)
+            H, Y, H_ref, Y_ref = run_host_path(engine, adapters, list(range(K)), [i * T for i in range(K + 1)],
+                                               X, Y0, 4096, 4096, 32)
+            assert_close(H, H_ref, f"H K={K} T={T}")
+            assert_close(Y, Y_ref, f"Y K={K} T={T}")
+            assert engine.device_errors() == 0
+
+
+@pytest.mark.parametrize("rank", [8, 16, 32, 64])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_rank_variants(rank, dtype):
+    """tests/unit/test_rank_variants.py:30-95: d=o=512, K=3, 17 tokens each (tails)."""
+    announce(f"rank variants r={rank} {dtype}")
+    engine = WarpPipeEngine()
+    K, n = 3, 17
+    adapters = register(engine, K, rank, 512, 512, dtype, 5, 16.0 / rank)
+    X = randn((K * n, 512), 6, dtype, 0.1)
+    Y0 = randn((K * n, 512), 7, dtype, 0.1)
+    H, Y, H_ref, Y_ref = run_host_path(engine, adapters, list(range(K)), [i * n for i in range(K + 1)],
+                                       X, Y0, 512, 512, rank)
+    assert_close(H, H_ref, "H")
+    assert_close(Y, Y_ref, "Y")
+
+
+@pytest.mark.parametrize("rank", [8, 16, 32, 64])
+def test_pipeline_full_size(rank):
+    """tests/unit/test_pipeline_output.py:36-82: d=o=4096, K=4 x 32 tokens, per-chunk check."""
+    announce(f"pipeline full size r={rank}")
+    dtype = torch.float16
+    engine = WarpPipeEngine()
+    K, n = 4, 32
+    adapters = register(engine, K, rank, 4096, 4096, dtype, 100 + rank, 16.0 / rank)
+    X = randn((K * n, 4096), 8, dtype, 0.1)
+    Y0 = randn((K * n, 4096), 9, dtype, 0.1)
+    H, Y, H_ref, Y_ref = run_host_path(engine, adapters, list(range(K)), [i * n for i in range(K + 1)],
+                                       X, Y0, 4096, 4096, rank)
+    assert_close(H, H_ref, "H")
+    for lo in range(0, K * n, 4):
+        assert_close(Y[lo:lo + 4], Y_ref[lo:lo + 4], f"Y chunk {lo}")
+
+
+def test_segment_builder_shapes():
+    """tests/unit/test_segment_builder.py:35-75: 1/31/2 tokens; K=256 one token each."""
+    announce("segment builder shapes")
+    dtype = torch.float16
+    engine = WarpPipeEngine()
+    adapters = register(engine, 256, 32, 4096, 4096, dtype, 21, 0.5)
+    X = randn((34, 4096), 22, dtype, 0.1)
+    Y0 = randn((34, 4096), 23, dtype, 0.1)
+    H, Y, H_ref, Y_ref = run_host_path(engine, adapters, [0, 1, 2], [0, 1, 32, 34], X, Y0, 4096, 4096, 32)
+    assert_close(H, H_ref, "H 1/31/2")
+    assert_close(Y, Y_ref, "Y 1/31/2")
+    X = randn((256, 4096), 24, dtype, 0.1)
+    Y0 = randn((256, 4096), 25, dtype, 0.1)
+    H, Y, H_ref, Y_ref = run_host_path(engine, adapters, list(range(256)), list(range(257)), X, Y0, 4096, 4096, 32)
+    assert_close(H, H_ref, "H K=256")
+    assert_close(Y, Y_ref, "Y K=256")
+
+
+def test_long_host_segment_is_fully_applied():
+    """A 100-token host segment: all tokens are applied (the reference's grid
+    drops tokens past 32, Appendix-B defect)."""
+    announce("long host segment")
+    dtype = torch.bfloat16
+    engine = WarpPipeEngine()
+    adapters = register(engine, 2, 16, 1024, 768, dtype, 31, 1.0)
+    X = randn((140, 1024), 32, dtype)
+    Y0 = randn((140, 768), 33, dtype)
+    H, Y, H_ref, Y_ref = run_host_path(engine, adapters, [1, 0], [0, 100, 140], X, Y0, 1024, 768, 16)
+    assert_close(H, H_ref, "H")
+    assert_close(Y, Y_ref, "Y")
+
+
+ADD_LORA_CASES = [
+    [0, 0, 0, 0, -1, -1, 2, 2, 2, 1, 1, 1, 1, 1, 1, 1],   # test_add_lora_packed.py:78
+    [3] * 32,                                             # :81
+    [-1] * 8,                                             # :84
+    [5] * 33,                                             # :93
+    list(range(8)) * 4,                                   # :102
+    [4] * 8,                                              # :108
+    [4] * 9,                                              # :109
+]
+
+
+def add_lora_case(engine, idx_list, rank, dtype, seed, L=8, d=4096, o=4096, scale=16.0 / 32):
+    T = len(idx_list)
+    wa = randn((L, 1, rank, d), seed, dtype, 0.02)
+    wb = randn((L, 1, o, rank), seed + 1, dtype, 0.02)
+    x = randn((T, d), seed + 2, dtype, 0.1)
+    y0 = randn((T, o), seed + 3, dtype, 0.1)
+    idx = torch.tensor(idx_list, dtype=torch.int64)
+    y = y0.cuda()
+    assert engine.build_seg_bounds(idx.cuda())
+    assert engine.add_lora_packed(y, x.cuda(), wa.cuda(), wb.cuda(), scale)
+    torch.cuda.synchronize()
+    y_ref = bgmv.add_lora(y0, x, wa, wb, scale, so.seg_bounds(idx_list).tolist())
+    return y, y_ref
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_add_lora_packed_cases(dtype):
+    """tests/correctness/test_add_lora_packed.py:48-112, all seven index lists."""
+    engine = WarpPipeEngine()
+    for n, lst in enumerate(ADD_LORA_CASES):
+        announce(f"add_lora case {n} {dtype}")
+        y, y_ref = add_lora_case(engine, lst, 32, dtype, 40 + n)
+        assert_close(y, y_ref, f"case {n}")
+    assert engine.device_errors() == 0
+
+
+@pytest.mark.parametrize("rank", [8, 16, 64])
+def test_add_lora_other_ranks(rank):
+    """add_lora at the ranks the reference's DSAK path rejects (bindings:197-198)."""
+    engine = WarpPipeEngine()
+    for n, lst in enumerate(ADD_LORA_CASES[:2] + ADD_LORA_CASES[4:5]):
+        announce(f"add_lora r={rank} case {n}")
+        y, y_ref = add_lora_case(engine, lst, rank, torch.bfloat16, 60 + n, scale=16.0 / rank)
+        assert_close(y, y_ref, f"r={rank} case {n}")
+
+
+def test_add_lora_unsupported_rank_returns_false():
+    engine = WarpPipeEngine()
+    idx = torch.zeros(4, dtype=torch.int64, device="cuda")
+    assert engine.build_seg_bounds(idx)
+    y = torch.zeros(4, 64, dtype=torch.float16, device="cuda")
+    x = torch.zeros(4, 64, dtype=torch.float16, device="cuda")
+    wa = torch.zeros(1, 1, 24, 64, dtype=torch.float16, device="cuda")
+    wb = torch.zeros(1, 1, 64, 24, dtype=torch.float16, device="cuda")
+    assert engine.add_lora_packed(y, x, wa, wb, 1.0) is False
+
+
+def test_segment_reuse_across_layers():
+    """test_add_lora_packed.py:116-146: one table, four layers with their own weights."""
+    engine = WarpPipeEngine()
+    idx_list = [0, 0, 0, -1, 1, 1, 1, 1, 1, 2, 2]
+    T = len(idx_list)
+    x = randn((T, 4096), 70, torch.float16, 0.1)
+    assert engine.build_seg_bounds(torch.tensor(idx_list, device="cuda"))
+    segs = so.seg_bounds(idx_list).tolist()
+    for layer in range(4):
+        announce(f"reuse across layers layer={layer}")
+        wa = randn((8, 1, 32, 4096), 71 + layer, torch.float16, 0.02)
+        wb = randn((8, 1, 4096, 32), 81 + layer, torch.float16, 0.02)
+        y0 = randn((T, 4096), 91 + layer, torch.float16, 0.1)
+        y = y0.cuda()
+        assert engine.add_lora_packed(y, x.cuda(), wa.cuda(), wb.cuda(), 0.5)
+        torch.cuda.synchronize()
+        assert_close(y, bgmv.add_lora(y0, x, wa, wb, 0.5, segs), f"layer {layer}")
+
+
+def test_graph_capture_replay_uses_replay_time_indices():
+    """tests/correctness/test_warp_pipe_graph_capture.py:39-129: capture with one
+    routing, rebuild the table outside the graph, replay with another; several
+    replays with eager work and synchronisation in between, each checked."""
+    dtype = torch.float16
+    T = 16
+    wa = randn((8, 1, 32, 4096), 100, dtype, 0.02)
+    wb = randn((8, 1, 4096, 32), 101, dtype, 0.02)
+    x = randn((T, 4096), 102, dtype, 0.1)
+    y0 = randn((T, 4096), 103, dtype, 0.1)
+    cap = [0, 0, 0, 0, 1, 1, 1, 1, -1, -1, 2, 2, 2, 2, 2, 2]
+    rep = [3, 3, 5, 5, 5, 5, 5, 5, 5, 5, 5, 5, 5, 5, -1, 6]
+    engine = WarpPipeEngine()
+    wa_d, wb_d, x_d, y0_d = wa.cuda(), wb.cuda(), x.cuda(), y0.cuda()
+    idx_buf = torch.zeros(T, dtype=torch.int64, device="cuda")
+    y_buf = torch.zeros(T, 4096, dtype=dtype, device="cuda")
+    idx_buf.copy_(torch.tensor(cap))
+    assert engine.build_seg_bounds(idx_buf)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            y_buf.copy_(y0_d)
+            engine.add_lora_packed(y_buf, x_d, wa_d, wb_d, 0.5)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    y_buf.copy_(y0_d)
+    announce("graph capture")
+    with torch.cuda.graph(g):
+        assert engine.add_lora_packed(y_buf, x_d, wa_d, wb_d, 0.5)
+    torch.cuda.synchronize()
+    ref_cap = bgmv.add_lora(y0, x, wa, wb, 0.5, so.seg_bounds(cap).tolist())
+    ref_rep = bgmv.add_lora(y0, x, wa, wb, 0.5, so.seg_bounds(rep).tolist())
+    for it, (lst, ref) in enumerate([(cap, ref_cap), (rep, ref_rep), (cap, ref_cap), (rep, ref_rep)]):
+        announce(f"graph replay {it}")
+        idx_buf.copy_(torch.tensor(lst))
+        assert engine.build_seg_bounds(idx_buf)
+        y_buf.copy_(y0_d)
+        _ = (x_d.float() * 2).sum()  # eager work between replays
+        g.replay()
+        torch.cuda.synchronize()
+        assert_close(y_buf, ref, f"replay {it}")
+    # Negative control: the replay-routing result differs from the capture-routing one.
+    assert not torch.allclose(ref_rep.float(), ref_cap.float(), rtol=1e-2, atol=1e-3)
+
+
+def test_seg_bounds_with_registered_adapters():
+    """build_seg_bounds + shrink/expand through the adapter store (the reference
+    reads stale descriptor pointers on this pairing)."""
+    announce("seg_bounds + store shrink/expand")
+    dtype = torch.bfloat16
+    engine = WarpPipeEngine()
+    adapters = register(engine, 6, 32, 2048, 1536, dtype, 110, 0.25, ids=[3, 7, 11, 2, 5, 0])
+    rng = np.random.default_rng(3)
+    idx = rng.choice([3, 7, 11, 2, 5, 0, -1], size=200)
+    X = randn((200, 2048), 111, dtype)
+    Y0 = randn((200, 1536), 112, dtype)
+    assert engine.build_seg_bounds(torch.from_numpy(idx).cuda())
+    H = engine.shrink(X.cuda(), 2048, 32, 200)
+    Y = Y0.cuda()
+    engine.expand(H, Y, 1536, 32)
+    torch.cuda.synchronize()
+    segs = so.seg_bounds(idx).tolist()
+    H_ref = bgmv.shrink(X, segs, adapters, 32, 200)
+    assert_close(H, H_ref, "H")
+    assert_close(Y, bgmv.expand(H_ref, Y0, segs, adapters), "Y")
+    assert engine.device_errors() == 0
+
+
+def test_mixed_rank_store():
+    """Mixed ranks in one grouped call (configuration 3's shape, reduced)."""
+    announce("mixed rank")
+    dtype = torch.bfloat16
+    engine = WarpPipeEngine()
+    ranks = [8, 16, 32, 64] * 3
+    adapters = {}
+    for i, r in enumerate(ranks):
+        A = randn((r, 1280), 120 + i, dtype, 0.02)
+        B = randn((2048, r), 140 + i, dtype, 0.02)
+        engine.register_adapter(i, A.cuda(), B.cuda(), 16.0 / r, rank=r)
+        adapters[i] = (A, B, 16.0 / r)
+    rng = np.random.default_rng(5)
+    idx = rng.integers(-1, 12, size=300)
+    X = randn((300, 1280), 160, dtype)
+    Y0 = randn((300, 2048), 161, dtype)
+    assert engine.build_seg_bounds(torch.from_numpy(idx).cuda())
+    H = engine.shrink(X.cuda(), 1280, 0, 300)
+    Y = Y0.cuda()
+    engine.expand(H, Y, 2048, 0)
+    torch.cuda.synchronize()
+    segs = so.seg_bounds(idx).tolist()
+    H_ref = bgmv.shrink(X, segs, adapters, 64, 300)
+    assert_close(H, H_ref, "H")
+    assert_close(Y, bgmv.expand(H_ref, Y0, segs, adapters), "Y")
+    assert engine.device_errors() == 0
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_packed_slices_and_offsets(dtype):
+    """One shared H expanded into q/k/v slices of a wider y, and a single
+    y_offset slice (the reference hook falls back for these)."""
+    announce(f"slices {dtype}")
+    engine = WarpPipeEngine()
+    T, d, L, r = 96, 1024, 6, 32
+    rng = np.random.default_rng(7)
+    idx = rng.integers(-1, L, size=T)
+    wa = randn((L, 1, r, d), 170, dtype, 0.02)
+    wbs = [randn((L, 1, o, r), 171 + i, dtype, 0.02) for i, o in enumerate([1024, 256, 256])]
+    x = randn((T, d), 175, dtype)
+    y0 = randn((T, 1536 + 8), 176, dtype)
+    offs = [0, 1024, 1280]
+    assert engine.build_seg_bounds(torch.from_numpy(idx).cuda())
+    y = y0.cuda()
+    assert engine.add_lora_slices(y, x.cuda(), wa.cuda(), [w.cuda() for w in wbs], 0.5, offs)
+    torch.cuda.synchronize()
+    segs = so.seg_bounds(idx).tolist()
+    assert_close(y, bgmv.add_lora(y0, x, wa, wbs, 0.5, segs, offs), "q/k/v slices")
+    y = y0.cuda()
+    assert engine.add_lora_packed(y, x.cuda(), wa.cuda(), wbs[1].cuda(), 0.5, y_offset=1288, y_slice_size=256)
+    torch.cuda.synchronize()
+    assert_close(y, bgmv.add_lora(y0, x, wa, [wbs[1]], 0.5, segs, [1288]), "y_offset slice")
+
+
+def test_out_of_range_ids_are_skipped_and_flagged():
+    """Ids >= L are not read (the reference indexes past wa_t_all, Appendix B
+    item 4): those rows stay untouched and the device error word says so."""
+    announce("out of range ids")
+    dtype = torch.float16
+    engine = WarpPipeEngine()
+    idx_list = [0, 0, 9, 9, 1, -1, 12, 1]
+    assert engine.device_errors() == 0
+    T = len(idx_list)
+    wa = randn((4, 1, 32, 512), 191, dtype, 0.02)
+    wb = randn((4, 1, 512, 32), 192, dtype, 0.02)
+    x = randn((T, 512), 193, dtype)
+    y0 = randn((T, 512), 194, dtype)
+    assert engine.build_seg_bounds(torch.tensor(idx_list, device="cuda"))
+    y = y0.cuda()
+    assert engine.add_lora_packed(y, x.cuda(), wa.cuda(), wb.cuda(), 1.0)
+    torch.cuda.synchronize()
+    segs = [s for s in so.seg_bounds(idx_list).tolist() if s[0] < 4]
+    assert_close(y, bgmv.add_lora(y0, x, wa, wb, 1.0, segs), "valid rows")
+    assert engine.device_errors() & 1
+
+
+def test_plan_token_count_must_fit_call():
+    engine = WarpPipeEngine()
+    assert engine.build_seg_bounds(torch.zeros(32, dtype=torch.int64, device="cuda"))
+    x = torch.zeros(16, 256, dtype=torch.float16, device="cuda")
+    y = torch.zeros(16, 256, dtype=torch.float16, device="cuda")
+    wa = torch.zeros(1, 1, 32, 256, dtype=torch.float16, device="cuda")
+    wb = torch.zeros(1, 1, 256, 32, dtype=torch.float16, device="cuda")
+    with pytest.raises(RuntimeError, match="segments reach token"):
+        engine.add_lora_packed(y, x, wa, wb, 1.0)

@@ -1,0 +1,154 @@
+"""GPU parity at the full sizes of the five benchmark configurations
+(BASELINE.json configs[0..4]) against the CPU oracle, on identical inputs
+drawn with seeded CPU generators (adapterslotsplusplus_amd.workloads)."""
+import numpy as np
+import pytest
+import torch
+
+from adapterslotsplusplus_amd import WarpPipeEngine
+from adapterslotsplusplus_amd import workloads as wl
+from oracle import bgmv
+from oracle import segments as so
+from tests.helpers import announce, assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def add_lora_check(engine, idx, x, y0, wa, wbs, offs, scale, what):
+    y = y0.cuda()
+    assert engine.add_lora_slices(y, x.cuda(), wa.cuda(), [w.cuda() for w in wbs], scale, offs)
+    torch.cuda.synchronize()
+    segs = so.seg_bounds(idx.numpy()).tolist()
+    assert_close(y, bgmv.add_lora(y0, x, wa, wbs, scale, segs, offs), what)
+
+
+def test_cfg1_reference_cpu_case():
+    """h=4096, r=16, 4 adapters, 64 uniformly routed tokens, fp16, scale 1, y0 = 0."""
+    announce("cfg1")
+    dt = torch.float16
+    idx = wl.uniform_indices(64, 4, seed=0)
+    x = wl.normal((64, 4096), 1.0, dt, 10)
+    wa = wl.normal((4, 1, 16, 4096), 0.02, dt, 11)
+    wb = wl.normal((4, 1, 4096, 16), 0.02, dt, 12)
+    y0 = torch.zeros(64, 4096, dtype=dt)
+    engine = WarpPipeEngine()
+    assert engine.build_seg_bounds(idx.cuda())
+    add_lora_check(engine, idx, x, y0, wa, [wb], [0], 1.0, "cfg1")
+
+
+def test_cfg2_llama7b_decode_calls():
+    """256 Zipf(1.1)-routed tokens, 64 adapters, r=32, bf16;
+    the o_proj call and the packed-qkv call (3 slices at offsets 0/4096/8192)."""
+    c = wl.CFG2
+    idx = wl.zipf_indices(c["T"], c["n_adapters"], c["zipf_s"], c["routing_seed"])
+    qkv, o = wl.llama7b_decode_layer_pair(c["T"], c["n_adapters"], c["rank"], c["dtype"], seed=20)
+    x = wl.normal((c["T"], 4096), 1.0, c["dtype"], 30)
+    engine = WarpPipeEngine()
+    assert engine.build_seg_bounds(idx.cuda())
+    announce("cfg2 o_proj")
+    add_lora_check(engine, idx, x, wl.normal((c["T"], 4096), 1.0, c["dtype"], 31), o.wa, o.wbs, o.y_offsets,
+                   0.5, "cfg2 o_proj")
+    announce("cfg2 qkv")
+    add_lora_check(engine, idx, x, wl.normal((c["T"], 3 * 4096), 1.0, c["dtype"], 32), qkv.wa, qkv.wbs,
+                   qkv.y_offsets, 0.5, "cfg2 qkv")
+    assert engine.device_errors() == 0
+
+
+@pytest.mark.parametrize("layer", ["gate", "down"])
+def test_cfg3_mixed_rank_13b(layer):
+    """h=5120, I=13824, 128 adapters with ranks uniform in
+    {8,16,32,64} (seed 2), 512 Zipf(1.1)-routed tokens (seed 3), bf16."""
+    announce(f"cfg3 {layer}")
+    dt = torch.bfloat16
+    d_in, d_out = (5120, 13824) if layer == "gate" else (13824, 5120)
+    g = torch.Generator().manual_seed(2)
+    ranks = [int(v) for v in torch.tensor([8, 16, 32, 64])[torch.randint(0, 4, (128,), generator=g)]]
+    idx = wl.zipf_indices(512, 128, 1.1, seed=3)
+    engine = WarpPipeEngine()
+    adapters = {}
+    touched = set(idx.tolist())
+    for i, r in enumerate(ranks):
+        if i not in touched:
+            continue
+        A = wl.normal((r, d_in), 0.02, dt, 1000 + i)
+        B = wl.normal((d_out, r), 0.02, dt, 2000 + i)
+        engine.register_adapter(i, A.cuda(), B.cuda(), 16.0 / r, rank=r)
+        adapters[i] = (A, B, 16.0 / r)
+    X = wl.normal((512, d_in), 1.0, dt, 40)
+    Y0 = wl.normal((512, d_out), 1.0, dt, 41)
+    assert engine.build_seg_bounds(idx.cuda())
+    H = engine.shrink(X.cuda(), d_in, 0, 512)
+    Y = Y0.cuda()
+    engine.expand(H, Y, d_out, 0)
+    torch.cuda.synchronize()
+    segs = so.seg_bounds(idx.numpy()).tolist()
+    H_ref = bgmv.shrink(X, segs, adapters, 64, 512)
+    assert_close(H, H_ref, f"cfg3 {layer} H")
+    assert_close(Y, bgmv.expand(H_ref, Y0, segs, adapters), f"cfg3 {layer} Y")
+    assert engine.device_errors() == 0
+
+
+def test_cfg4_prefill_chunk():
+    """8192 tokens over 16 adapters, segment lengths lognormal(6, 1)
+    (seed 4), r=64, h=4096, fp16; q and o targets."""
+    dt = torch.float16
+    lens = wl.lognormal_segments(8192, 16, 6.0, 1.0, seed=4)
+    idx = torch.repeat_interleave(torch.arange(16), torch.tensor(lens))
+    x = wl.normal((8192, 4096), 1.0, dt, 50)
+    engine = WarpPipeEngine()
+    assert engine.build_seg_bounds(idx.cuda())
+    for t, name in enumerate(["q", "o"]):
+        announce(f"cfg4 {name}")
+        wa = wl.normal((16, 1, 64, 4096), 0.02, dt, 51 + 2 * t)
+        wb = wl.normal((16, 1, 4096, 64), 0.02, dt, 52 + 2 * t)
+        y0 = wl.normal((8192, 4096), 1.0, dt, 60 + t)
+        add_lora_check(engine, idx, x, y0, wa, [wb], [0], 0.25, f"cfg4 {name}")
+
+
+def test_cfg5_draft_step_graph():
+    """draft model h=2048, 22 layers x {q,k,v,o} = 88 calls, 32
+    tenants x 4 draft tokens (tenant-contiguous), r=32, bf16; build_seg_bounds
+    and all 88 calls captured in one graph, replayed with a new routing."""
+    dt = torch.bfloat16
+    T, L, h = 128, 32, 2048
+    n_calls = 88
+    engine = WarpPipeEngine()
+    was = [wl.normal((L, 1, 32, h), 0.02, dt, 3000 + i) for i in range(n_calls)]
+    wbs = [wl.normal((L, 1, h, 32), 0.02, dt, 4000 + i) for i in range(n_calls)]
+    xs = [wl.normal((T, h), 1.0, dt, 5000 + i) for i in range(n_calls)]
+    y0s = [wl.normal((T, h), 1.0, dt, 6000 + i) for i in range(n_calls)]
+    d_was = [w.cuda() for w in was]
+    d_wbs = [w.cuda() for w in wbs]
+    d_xs = [v.cuda() for v in xs]
+    d_y0s = [v.cuda() for v in y0s]
+    d_ys = [v.clone() for v in d_y0s]
+    idx_a = torch.repeat_interleave(torch.arange(L), 4)
+    idx_b = torch.repeat_interleave(torch.randperm(L, generator=torch.Generator().manual_seed(7)), 4)
+    idx_buf = idx_a.cuda()
+
+    def step():
+        assert engine.build_seg_bounds(idx_buf)
+        for i in range(n_calls):
+            assert engine.add_lora_packed(d_ys[i], d_xs[i], d_was[i], d_wbs[i], 0.5)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    announce("cfg5 capture")
+    with torch.cuda.graph(g):
+        step()
+    torch.cuda.synchronize()
+    for rep, idx in enumerate([idx_b, idx_a]):
+        announce(f"cfg5 replay {rep}")
+        idx_buf.copy_(idx.cuda())
+        for i in range(n_calls):
+            d_ys[i].copy_(d_y0s[i])
+        g.replay()
+        torch.cuda.synchronize()
+        segs = so.seg_bounds(idx.numpy()).tolist()
+        for i in range(0, n_calls, 11):
+            assert_close(d_ys[i], bgmv.add_lora(y0s[i], xs[i], was[i], wbs[i], 0.5, segs), f"cfg5 call {i} rep {rep}")
