@@ -28,10 +28,11 @@ WP_DTYPE_BF16 = 1
 DEVICE_ERR_ID_RANGE = 1
 DEVICE_ERR_UNREGISTERED = 2
 DEVICE_ERR_SHAPE = 4
+DEVICE_ERR_SPIN = 8
 
 # Every entry point include/warppipe_mi355x.h declares.
 EXPORTED = (
-    "wp_last_error", "wp_abi_version", "wp_rank_supported", "wp_create", "wp_destroy",
+    "wp_last_error", "wp_abi_version", "wp_rank_supported", "wp_block_tokens", "wp_create", "wp_destroy",
     "wp_register_adapter", "wp_evict_adapter", "wp_has_adapter", "wp_build_segments",
     "wp_build_seg_bounds", "wp_read_segments", "wp_read_plan", "wp_read_device_errors",
     "wp_shrink", "wp_expand", "wp_add_lora", "wp_prefetch_adapter", "wp_is_prefetch_ready",
@@ -70,6 +71,7 @@ def load():
         "wp_last_error": ([], ctypes.c_char_p),
         "wp_abi_version": ([], ctypes.c_int),
         "wp_rank_supported": ([i32], ctypes.c_int),
+        "wp_block_tokens": ([i64], ctypes.c_int),
         "wp_create": ([P(WpConfig), P(p)], ctypes.c_int),
         "wp_destroy": ([p], ctypes.c_int),
         "wp_register_adapter": ([p, i32, p, p, i32, i32, i32, f32, i32, i32, p], ctypes.c_int),

@@ -16,23 +16,31 @@ struct ApplyArgs {
   void* y;         // Y [T, ldy]
   int64_t ldy;
   int32_t d_model;
-  int32_t rank;      // 8/16/32/64, or 0 for mixed ranks (per adapter)
-  int32_t dc;        // shrink d-range per workgroup, multiple of 128
-  int32_t n_chunks;  // ceil(d_model / dc)
-  int32_t n_ochunks; // expand workgroups per block (all slices)
-  int32_t ptok;      // rows per chunk in `partials` (>= tokens in the plan)
-  int32_t pstride;   // floats per partial row (rank, or 64 when mixed)
-  float* partials;   // fp32 [n_chunks][ptok][pstride]
+  int32_t rank;       // 8/16/32/64, or 0 for mixed ranks (per adapter)
+  int32_t dc;         // shrink d-range per workgroup, multiple of 128
+  int32_t n_chunks;   // ceil(d_model / dc): shrink workgroups per block
+  int32_t n_ochunks;  // expand workgroups per block (all slices)
+  int32_t n_slots;    // block slots of the grid (>= the plan's block count)
+  int32_t hs;         // elements per H row: rank, or 64 for mixed ranks
+  int32_t ptok;       // rows per chunk of `part` (plan positions)
+  float* part;        // fp32 partial H by plan position: [n_chunks][ptok][hs]
+  uint32_t* done;     // per block (stride kCounterStride): shrink workgroups published, zero between calls
+  uint32_t* consumed; // per block (stride kCounterStride): expand workgroups finished, zero between calls
   PlanView plan;
   Weights w;
 };
 
 // Builds the step plan from token_lora_indices (wp_plan.hip).
+// Blocks hold at most bt (<= kBlockTokens) tokens.
 hipError_t launch_plan(const void* idx, int idx_is_int64, int T, uint32_t* header, Segment* segments, Block* blocks,
-                       int32_t* perm, int seg_cap, int block_cap, hipStream_t stream);
+                       int32_t* perm, int32_t* bperm, int seg_cap, int block_cap, int bt, hipStream_t stream);
 
-hipError_t launch_shrink(int dtype_bf16, const ApplyArgs& a, int max_blocks, hipStream_t stream);
-hipError_t launch_expand(int dtype_bf16, const ApplyArgs& a, int max_blocks, hipStream_t stream);
+// One launch: shrink + expand of a whole add_lora call (partials, counters).
+hipError_t launch_fused(int dtype_bf16, const ApplyArgs& a, hipStream_t stream);
+// shrink(): split-K shrink; one finishing workgroup per block writes H[token].
+hipError_t launch_shrink(int dtype_bf16, const ApplyArgs& a, hipStream_t stream);
+// expand(): expand from a caller-provided token-indexed H.
+hipError_t launch_expand(int dtype_bf16, const ApplyArgs& a, hipStream_t stream);
 
 // Output columns one expand workgroup produces.
 int expand_cols_per_workgroup();

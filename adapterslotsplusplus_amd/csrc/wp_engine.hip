@@ -18,8 +18,9 @@
 //   * Staging slots are sized per adapter (the reference's fixed 512 KiB slots
 //     overflow for rank 64 x 13824), eviction releases the id's slot, and a slot
 //     is never overwritten before the kernels that read it have finished.
-//   * Every scratch buffer (fp32 partials, H) is allocated at engine creation,
-//     so calls allocate nothing and graph replays keep valid pointers.
+//   * Every scratch buffer (fp32 partials, published H, counters, plan arrays) is
+//     allocated at engine creation, so calls allocate nothing and graph
+//     replays keep valid pointers.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -94,16 +95,14 @@ struct Slot {
   bool used = false;
 };
 
-// d-range per shrink workgroup: at most 16 chunks, each a multiple of 128.
+// d-range per shrink workgroup: at most kMaxChunks chunks, each a multiple of 128.
+constexpr int kMaxChunks = 16;
 inline void shrink_chunks(int d, int* dc, int* n_chunks) {
-  const int nc = static_cast<int>(std::min<int64_t>(16, ceil_div(d, 128)));
+  const int nc = static_cast<int>(std::min<int64_t>(kMaxChunks, ceil_div(d, 128)));
   const int c = static_cast<int>(ceil_div(ceil_div(d, nc), 128) * 128);
   *dc = c;
   *n_chunks = static_cast<int>(ceil_div(d, c));
 }
-
-constexpr int kMaxChunks = 16;
-constexpr int kGridCapWorkgroups = 4096;
 
 }  // namespace
 
@@ -121,11 +120,12 @@ struct wp_engine {
   Segment* segs = nullptr;
   Block* blocks = nullptr;
   int32_t* perm = nullptr;
-  uint32_t* counters = nullptr;
+  int32_t* bperm = nullptr;     // [block_cap][kBlockTokens]
+  uint32_t* done = nullptr;     // [block_cap]
+  uint32_t* consumed = nullptr; // [block_cap]
   Entry* plan_entries = nullptr;
-  void* hscratch = nullptr;
+  float* part = nullptr;        // [kMaxChunks][tok_cap][kMaxRank] fp32 partial H
   int seg_cap = 0, block_cap = 0, tok_cap = 0, entry_cap = 0;
-  float* partials = nullptr;
 
   // Id-indexed adapter table for table-mode kernels on device-built plans.
   Entry* dtable = nullptr;
@@ -148,6 +148,7 @@ struct wp_engine {
   // Host view of the current plan.
   int plan_kind = 0;          // 0 none, 1 host-built (build_segments), 2 device-built (build_seg_bounds)
   int64_t plan_T = 0;         // device: T of build_seg_bounds; host: max token end
+  int plan_bt = kBlockTokens; // most tokens per block of the current plan
   int plan_blocks = 0;        // host: exact block count
   int plan_valid = 0;         // host: exact token count in perm
   std::vector<int32_t> plan_entry_ids;  // host: adapter id per entry
@@ -317,8 +318,21 @@ PlanView plan_view(const wp_engine* e) {
   v.segments = e->segs;
   v.blocks = e->blocks;
   v.perm = e->perm;
-  v.counters = e->counters;
+  v.bperm = e->bperm;
   return v;
+}
+
+// Fields every apply launch shares.
+ApplyArgs base_args(const wp_engine* e, int rank) {
+  ApplyArgs a{};
+  a.rank = rank;
+  a.hs = rank == 0 ? kMaxRank : rank;
+  a.ptok = e->tok_cap;
+  a.part = e->part;
+  a.done = e->done;
+  a.consumed = e->consumed;
+  a.plan = plan_view(e);
+  return a;
 }
 
 // Upper bound on the block count of the current plan, given at most `groups`
@@ -327,13 +341,9 @@ int block_bound(const wp_engine* e, int64_t groups) {
   if (e->plan_kind == 1) return e->plan_blocks;
   const int64_t T = e->plan_T;
   const int64_t g = std::min<int64_t>(T, std::max<int64_t>(groups, 0));
-  return static_cast<int>(std::min<int64_t>(T, T / kBlockTokens + g));
+  return static_cast<int>(std::min<int64_t>(T, T / e->plan_bt + g));
 }
 
-int grid_block_slots(int bound, int per_block) {
-  const int cap = std::max(1, kGridCapWorkgroups / std::max(1, per_block));
-  return std::min(bound, cap);
-}
 
 }  // namespace
 
@@ -348,6 +358,8 @@ const char* wp_last_error(void) { return g_last_error.c_str(); }
 int wp_abi_version(void) { return WP_ABI_VERSION; }
 
 int wp_rank_supported(int32_t rank) { return rank_ok(rank) ? 1 : 0; }
+
+int wp_block_tokens(int64_t T) { return plan_block_tokens(T); }
 
 int wp_create(const wp_config* cfg_in, wp_engine** out) {
   if (out == nullptr) return fail(WP_ERR_INVALID, "wp_create: out is NULL");
@@ -400,9 +412,11 @@ int wp_create(const wp_config* cfg_in, wp_engine** out) {
   const size_t o_seg = carve(sizeof(Segment) * e->seg_cap);
   const size_t o_blk = carve(sizeof(Block) * e->block_cap);
   const size_t o_perm = carve(sizeof(int32_t) * e->tok_cap);
-  const size_t o_cnt = carve(sizeof(uint32_t) * e->block_cap);
+  const size_t o_bperm = carve(sizeof(int32_t) * static_cast<size_t>(e->block_cap) * kBlockTokens);
+  const size_t o_done = carve(sizeof(uint32_t) * e->block_cap * kCounterStride);
+  const size_t o_cons = carve(sizeof(uint32_t) * e->block_cap * kCounterStride);
   const size_t o_ent = carve(sizeof(Entry) * e->entry_cap);
-  const size_t o_h = carve(sizeof(uint16_t) * static_cast<size_t>(e->tok_cap) * kMaxRank);
+  const size_t o_part = carve(sizeof(float) * kMaxChunks * static_cast<size_t>(e->tok_cap) * kMaxRank);
   if (hipMalloc(reinterpret_cast<void**>(&e->ws), off) != hipSuccess)
     return bail(fail(WP_ERR_HIP, "wp_create: workspace allocation (%zu bytes) failed", off));
   if (hipMemset(e->ws, 0, off) != hipSuccess) return bail(fail(WP_ERR_HIP, "wp_create: workspace clear failed"));
@@ -410,15 +424,15 @@ int wp_create(const wp_config* cfg_in, wp_engine** out) {
   e->segs = reinterpret_cast<Segment*>(e->ws + o_seg);
   e->blocks = reinterpret_cast<Block*>(e->ws + o_blk);
   e->perm = reinterpret_cast<int32_t*>(e->ws + o_perm);
-  e->counters = reinterpret_cast<uint32_t*>(e->ws + o_cnt);
+  e->bperm = reinterpret_cast<int32_t*>(e->ws + o_bperm);
+  e->done = reinterpret_cast<uint32_t*>(e->ws + o_done);
+  e->consumed = reinterpret_cast<uint32_t*>(e->ws + o_cons);
   e->plan_entries = reinterpret_cast<Entry*>(e->ws + o_ent);
-  e->hscratch = e->ws + o_h;
-  const size_t pbytes = sizeof(float) * kMaxChunks * static_cast<size_t>(e->tok_cap) * kMaxRank;
-  if (hipMalloc(reinterpret_cast<void**>(&e->partials), pbytes) != hipSuccess)
-    return bail(fail(WP_ERR_HIP, "wp_create: partials allocation failed"));
+  e->part = reinterpret_cast<float*>(e->ws + o_part);
 
   e->pinned_bytes = sizeof(uint32_t) * kHdrWords + sizeof(Segment) * e->seg_cap + sizeof(Block) * e->block_cap +
-                    sizeof(int32_t) * e->tok_cap + sizeof(Entry) * e->entry_cap + 1024;
+                    sizeof(int32_t) * e->tok_cap + sizeof(int32_t) * static_cast<size_t>(e->block_cap) * kBlockTokens +
+                    sizeof(Entry) * e->entry_cap + 1024;
   if (hipHostMalloc(reinterpret_cast<void**>(&e->pinned), e->pinned_bytes, hipHostMallocDefault) != hipSuccess)
     return bail(fail(WP_ERR_HIP, "wp_create: pinned upload buffer failed"));
   if (hipHostMalloc(reinterpret_cast<void**>(&e->pinned_zero), 64, hipHostMallocDefault) != hipSuccess)
@@ -461,7 +475,6 @@ int wp_destroy(wp_engine* e) {
   }
   if (e->dtable) (void)hipFree(e->dtable);
   if (e->ws) (void)hipFree(e->ws);
-  if (e->partials) (void)hipFree(e->partials);
   if (e->pinned) (void)hipHostFree(e->pinned);
   if (e->pinned_zero) (void)hipHostFree(e->pinned_zero);
   if (e->pinned_table) (void)hipHostFree(e->pinned_table);
@@ -597,7 +610,8 @@ int wp_build_segments(wp_engine* e, const int32_t* ids, int32_t K, const int32_t
     hsegs[k].token_count = offsets[k + 1] - offsets[k];
     hsegs[k].pad = 0;
   }
-  // perm: each adapter's segments concatenated; blocks of kBlockTokens.
+  // perm: each adapter's segments concatenated; blocks of bt tokens.
+  const int bt = plan_block_tokens(max_end);
   std::vector<int32_t> perm_v;
   perm_v.reserve(static_cast<size_t>(n_tok));
   std::vector<Block> blocks_v;
@@ -606,11 +620,11 @@ int wp_build_segments(wp_engine* e, const int32_t* ids, int32_t K, const int32_t
     for (int k : group_segs[ent])
       for (int32_t t = offsets[k]; t < offsets[k + 1]; ++t) perm_v.push_back(t);
     const int n = static_cast<int>(perm_v.size()) - first;
-    for (int j = 0; j < n; j += kBlockTokens) {
+    for (int j = 0; j < n; j += bt) {
       Block b;
       b.adapter_id = entry_ids[ent];
       b.first = first + j;
-      b.count = std::min(kBlockTokens, n - j);
+      b.count = std::min(bt, n - j);
       b.entry = static_cast<int>(ent);
       blocks_v.push_back(b);
     }
@@ -619,7 +633,11 @@ int wp_build_segments(wp_engine* e, const int32_t* ids, int32_t K, const int32_t
   std::memcpy(hblocks, blocks_v.data(), sizeof(Block) * blocks_v.size());
   hperm = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(hblocks) + sizeof(Block) * std::max<size_t>(blocks_v.size(), 1));
   std::memcpy(hperm, perm_v.data(), sizeof(int32_t) * perm_v.size());
-  char* pe = reinterpret_cast<char*>(hperm) + sizeof(int32_t) * std::max<size_t>(perm_v.size(), 1);
+  int32_t* hbperm = hperm + std::max<size_t>(perm_v.size(), 1);
+  for (size_t q = 0; q < blocks_v.size(); ++q)
+    for (int j = 0; j < kBlockTokens; ++j)
+      hbperm[q * kBlockTokens + j] = j < blocks_v[q].count ? perm_v[blocks_v[q].first + j] : -1;
+  char* pe = reinterpret_cast<char*>(hbperm + std::max<size_t>(blocks_v.size(), 1) * kBlockTokens);
   pe = reinterpret_cast<char*>((reinterpret_cast<uintptr_t>(pe) + 63) & ~uintptr_t(63));
   hent = reinterpret_cast<Entry*>(pe);
   std::memcpy(hent, entries.data(), sizeof(Entry) * entries.size());
@@ -635,6 +653,9 @@ int wp_build_segments(wp_engine* e, const int32_t* ids, int32_t K, const int32_t
     WP_HIP(hipMemcpyAsync(e->blocks, hblocks, sizeof(Block) * blocks_v.size(), hipMemcpyHostToDevice, stream));
   if (!perm_v.empty())
     WP_HIP(hipMemcpyAsync(e->perm, hperm, sizeof(int32_t) * perm_v.size(), hipMemcpyHostToDevice, stream));
+  if (!blocks_v.empty())
+    WP_HIP(hipMemcpyAsync(e->bperm, hbperm, sizeof(int32_t) * blocks_v.size() * kBlockTokens, hipMemcpyHostToDevice,
+                          stream));
   if (!entries.empty())
     WP_HIP(hipMemcpyAsync(e->plan_entries, hent, sizeof(Entry) * entries.size(), hipMemcpyHostToDevice, stream));
   WP_HIP(hipEventRecord(e->upload_done, stream));
@@ -642,6 +663,7 @@ int wp_build_segments(wp_engine* e, const int32_t* ids, int32_t K, const int32_t
 
   e->plan_kind = 1;
   e->plan_T = max_end;
+  e->plan_bt = bt;
   e->plan_blocks = static_cast<int>(blocks_v.size());
   e->plan_valid = static_cast<int>(n_tok);
   e->plan_entry_ids = entry_ids;
@@ -657,10 +679,12 @@ int wp_build_seg_bounds(wp_engine* e, const void* idx, int32_t idx_is_int64, int
   if (T > 0 && idx == nullptr) return fail(WP_ERR_INVALID, "build_seg_bounds: null indices");
   DeviceGuard g(e->device);
   hipStream_t stream = static_cast<hipStream_t>(stream_);
+  const int bt = plan_block_tokens(T);
   WP_HIP(launch_plan(idx, idx_is_int64 ? 1 : 0, static_cast<int>(T), e->header, e->segs, e->blocks, e->perm,
-                     e->seg_cap, e->block_cap, stream));
+                     e->bperm, e->seg_cap, e->block_cap, bt, stream));
   e->plan_kind = 2;
   e->plan_T = T;
+  e->plan_bt = bt;
   e->plan_blocks = -1;
   e->plan_valid = -1;
   e->plan_entry_ids.clear();
@@ -717,6 +741,12 @@ int wp_read_device_errors(wp_engine* e, uint32_t* flags, void* stream_) {
   WP_HIP(hipMemcpyAsync(&v, e->header + kHdrErrors, sizeof(v), hipMemcpyDeviceToHost, stream));
   WP_HIP(hipMemcpyAsync(e->header + kHdrErrors, e->pinned_zero, sizeof(v), hipMemcpyHostToDevice, stream));
   WP_HIP(hipStreamSynchronize(stream));
+  if (v & kErrSpin) {
+    // A wait that gave up leaves the per-block counters undefined: clear them.
+    WP_HIP(hipMemsetAsync(e->done, 0, sizeof(uint32_t) * e->block_cap * kCounterStride, stream));
+    WP_HIP(hipMemsetAsync(e->consumed, 0, sizeof(uint32_t) * e->block_cap * kCounterStride, stream));
+    WP_HIP(hipStreamSynchronize(stream));
+  }
   *flags = v;
   return WP_OK;
 }
@@ -773,23 +803,18 @@ int wp_shrink(wp_engine* e, const void* X, void* H, int32_t d_model, int32_t ran
   }
   DeviceGuard g(e->device);
   hipStream_t stream = static_cast<hipStream_t>(stream_);
-  ApplyArgs a{};
+  ApplyArgs a = base_args(e, rank);
   a.x = X;
   a.ldx = d_model;
   a.h = H;
   a.ldh = h_row_stride;
   a.d_model = d_model;
-  a.rank = rank;
   shrink_chunks(d_model, &a.dc, &a.n_chunks);
-  a.ptok = e->plan_kind == 1 ? std::max(1, e->plan_valid) : static_cast<int>(std::max<int64_t>(1, e->plan_T));
-  a.pstride = rank == 0 ? kMaxRank : rank;
-  a.partials = e->partials;
-  a.plan = plan_view(e);
   uint32_t mask = 0;
   if ((rc = table_weights(e, stream, &a.w, &mask)) != WP_OK) return rc;
   a.w.n_slices = 1;
-  const int bound = block_bound(e, e->plan_T);
-  WP_HIP(launch_shrink(dtype == WP_DTYPE_BF16, a, grid_block_slots(bound, a.n_chunks), stream));
+  a.n_slots = block_bound(e, e->plan_T);
+  WP_HIP(launch_shrink(dtype == WP_DTYPE_BF16, a, stream));
   if (e->plan_kind == 1) record_slot_uses(e, e->plan_entry_slot, stream);
   else record_mask_uses(e, mask, stream);
   return WP_OK;
@@ -825,13 +850,11 @@ int wp_expand(wp_engine* e, const void* H, void* Y, int32_t out_features, int32_
   }
   DeviceGuard g(e->device);
   hipStream_t stream = static_cast<hipStream_t>(stream_);
-  ApplyArgs a{};
+  ApplyArgs a = base_args(e, rank);
   a.h = const_cast<void*>(H);
   a.ldh = h_row_stride;
   a.y = Y;
   a.ldy = y_row_stride;
-  a.rank = rank;
-  a.plan = plan_view(e);
   uint32_t mask = 0;
   if ((rc = table_weights(e, stream, &a.w, &mask)) != WP_OK) return rc;
   const int cols = expand_cols_per_workgroup();
@@ -841,8 +864,8 @@ int wp_expand(wp_engine* e, const void* H, void* Y, int32_t out_features, int32_
   a.w.oc_start[0] = 0;
   a.w.oc_start[1] = static_cast<int32_t>(ceil_div(out_features, cols));
   a.n_ochunks = a.w.oc_start[1];
-  const int bound = block_bound(e, e->plan_T);
-  WP_HIP(launch_expand(dtype == WP_DTYPE_BF16, a, grid_block_slots(bound, a.n_ochunks), stream));
+  a.n_slots = block_bound(e, e->plan_T);
+  WP_HIP(launch_expand(dtype == WP_DTYPE_BF16, a, stream));
   if (e->plan_kind == 1) record_slot_uses(e, e->plan_entry_slot, stream);
   else record_mask_uses(e, mask, stream);
   return WP_OK;
@@ -874,25 +897,16 @@ int wp_add_lora(wp_engine* e, void* y, const void* x, const void* wa, int64_t wa
   if (y_row_stride % 4 != 0) return fail(WP_ERR_INVALID, "add_lora: y row stride must be a multiple of 4");
   if (e->plan_kind == 0) return fail(WP_ERR_STATE, "add_lora: no segment table (call build_seg_bounds first)");
   if (e->plan_T > T) return fail(WP_ERR_INVALID, "add_lora: segments reach token %lld but x has %lld rows", (long long)e->plan_T, (long long)T);
-  if (e->plan_T > e->tok_cap)
-    return fail(WP_ERR_CAPACITY, "add_lora: segments reach token %lld, beyond max_tokens %d", (long long)e->plan_T, e->tok_cap);
   DeviceGuard g(e->device);
   hipStream_t stream = static_cast<hipStream_t>(stream_);
 
-  ApplyArgs a{};
+  ApplyArgs a = base_args(e, rank);
   a.x = x;
   a.ldx = d_model;
-  a.h = e->hscratch;
-  a.ldh = rank;
   a.y = y;
   a.ldy = y_row_stride;
   a.d_model = d_model;
-  a.rank = rank;
   shrink_chunks(d_model, &a.dc, &a.n_chunks);
-  a.ptok = e->plan_kind == 1 ? std::max(1, e->plan_valid) : static_cast<int>(std::max<int64_t>(1, e->plan_T));
-  a.pstride = rank;
-  a.partials = e->partials;
-  a.plan = plan_view(e);
   a.w.mode = kStacked;
   a.w.num_ids = num_loras;
   a.w.a_base = wa;
@@ -911,9 +925,8 @@ int wp_add_lora(wp_engine* e, void* y, const void* x, const void* wa, int64_t wa
   }
   a.w.oc_start[n_slices] = oc;
   a.n_ochunks = oc;
-  const int bound = block_bound(e, num_loras);
-  WP_HIP(launch_shrink(dtype == WP_DTYPE_BF16, a, grid_block_slots(bound, a.n_chunks), stream));
-  WP_HIP(launch_expand(dtype == WP_DTYPE_BF16, a, grid_block_slots(bound, a.n_ochunks), stream));
+  a.n_slots = block_bound(e, num_loras);
+  WP_HIP(launch_fused(dtype == WP_DTYPE_BF16, a, stream));
   return WP_OK;
 }
 

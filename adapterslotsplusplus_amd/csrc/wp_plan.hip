@@ -11,7 +11,7 @@
 //   2. the grouping the apply kernels run on (no reference counterpart): the
 //      runs are sorted by adapter id (bitonic sort of 64-bit (id, run) keys, so
 //      token order is kept inside an adapter), concatenated into `perm`, and
-//      each adapter's tokens are cut into blocks of kBlockTokens.  Every touched
+//      each adapter's tokens are cut into blocks of `bt` tokens.  Every touched
 //      adapter's weights are then streamed once per block instead of once per
 //      run (about 232 runs vs 49 adapters for 256 Zipf-routed decode tokens).
 //
@@ -78,8 +78,8 @@ __device__ __forceinline__ int upper_index(const int* a, int n, int q) {
 template <int NT, int E>
 __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, int idx_is_int64, int T,
                                                   uint32_t* __restrict__ header, Segment* __restrict__ segments,
-                                                  Block* __restrict__ blocks, int32_t* __restrict__ perm, int seg_cap,
-                                                  int block_cap) {
+                                                  Block* __restrict__ blocks, int32_t* __restrict__ perm,
+                                                  int32_t* __restrict__ bperm, int seg_cap, int block_cap, int bt) {
   constexpr int CAP = NT * E;
   // s_big: the ids (int64) first, then the sort keys, then per-run offsets.
   __shared__ unsigned long long s_big[CAP];
@@ -249,7 +249,7 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
     perm[q] = s_rstart[p] + (q - s_roff[p]);
   }
 
-  // 6. Groups (one per adapter) and their blocks of kBlockTokens.
+  // 6. Groups (one per adapter) and their blocks of bt tokens.
   int n_groups = 0;
   int gb = block_exclusive_scan<NT>(gcount, s_scan, &n_groups);  // ends every read of s_roff / s_rstart
 #pragma unroll
@@ -267,7 +267,7 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const int g = e0 + e;
-    nb[e] = g < n_groups ? (s_b[g + 1] - s_b[g] + kBlockTokens - 1) / kBlockTokens : 0;
+    nb[e] = g < n_groups ? (s_b[g + 1] - s_b[g] + bt - 1) / bt : 0;
     bsum += nb[e];
   }
   int n_blocks = 0;
@@ -287,10 +287,21 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
     const int n = s_b[g + 1] - s_b[g];
     Block b;
     b.adapter_id = s_a[g];
-    b.first = s_b[g] + j * kBlockTokens;
-    b.count = n - j * kBlockTokens < kBlockTokens ? n - j * kBlockTokens : kBlockTokens;
+    b.first = s_b[g] + j * bt;
+    b.count = n - j * bt < bt ? n - j * bt : bt;
     b.entry = s_a[g];
     blocks[q] = b;
+  }
+  // Block-padded token lists, read back from perm (written above by this
+  // workgroup; the barrier makes those global writes visible to it).
+  __syncthreads();
+  for (int u = tid; u < blk_out * bt; u += NT) {
+    const int q = u / bt;
+    const int j = u - q * bt;
+    const int g = upper_index(s_bbase, n_groups, q);
+    const int n = s_b[g + 1] - s_b[g];
+    const int jj = (q - s_bbase[g]) * bt + j;  // position inside the group
+    if (jj < n) bperm[static_cast<int64_t>(q) * kBlockTokens + j] = perm[s_b[g] + jj];
   }
 
   if (tid == 0) {
@@ -299,6 +310,7 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
     header[kHdrNumGroups] = static_cast<uint32_t>(n_groups);
     header[kHdrNumValid] = static_cast<uint32_t>(n_tok);
     header[kHdrT] = static_cast<uint32_t>(T);
+    header[kHdrBlockTokens] = static_cast<uint32_t>(bt);
   }
 }
 
@@ -306,17 +318,17 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
 
 // Host launcher: the smallest capacity variant that holds T.
 hipError_t launch_plan(const void* idx, int idx_is_int64, int T, uint32_t* header, Segment* segments, Block* blocks,
-                       int32_t* perm, int seg_cap, int block_cap, hipStream_t stream) {
-  if (T < 0) return hipErrorInvalidValue;
+                       int32_t* perm, int32_t* bperm, int seg_cap, int block_cap, int bt, hipStream_t stream) {
+  if (T < 0 || bt < 1 || bt > kBlockTokens) return hipErrorInvalidValue;
   if (T <= 256) {
-    plan_kernel<256, 1><<<1, 256, 0, stream>>>(idx, idx_is_int64, T, header, segments, blocks, perm, seg_cap,
-                                               block_cap);
+    plan_kernel<256, 1><<<1, 256, 0, stream>>>(idx, idx_is_int64, T, header, segments, blocks, perm, bperm,
+                                               seg_cap, block_cap, bt);
   } else if (T <= 2048) {
-    plan_kernel<1024, 2><<<1, 1024, 0, stream>>>(idx, idx_is_int64, T, header, segments, blocks, perm, seg_cap,
-                                                 block_cap);
+    plan_kernel<1024, 2><<<1, 1024, 0, stream>>>(idx, idx_is_int64, T, header, segments, blocks, perm, bperm,
+                                                 seg_cap, block_cap, bt);
   } else if (T <= kPlanMaxTokens) {
-    plan_kernel<1024, 8><<<1, 1024, 0, stream>>>(idx, idx_is_int64, T, header, segments, blocks, perm, seg_cap,
-                                                 block_cap);
+    plan_kernel<1024, 8><<<1, 1024, 0, stream>>>(idx, idx_is_int64, T, header, segments, blocks, perm, bperm,
+                                                 seg_cap, block_cap, bt);
   } else {
     return hipErrorInvalidValue;
   }

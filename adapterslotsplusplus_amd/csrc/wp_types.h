@@ -7,7 +7,9 @@
 //                          reference's build_seg_bounds (warp_pipe_r32.cu:461-512)
 //   blocks[]      Block    work units: <= kBlockTokens tokens of ONE adapter
 //   perm[]        i32      token indices grouped by adapter (blocks index into it)
-//   counters[]    u32      per-block arrival counters of the split-K shrink
+//   bperm[]       i32      the same tokens, kBlockTokens slots per block, so a
+//                          workgroup loads its tokens without first reading
+//                          its block descriptor
 //
 // The reference keeps its table in mapped pinned host memory that every kernel
 // block reads over PCIe (warp_pipe_bindings.cpp:21-27).  Here it lives in HBM
@@ -24,8 +26,19 @@ constexpr int kMaxSegmentTokens = 32;
 // The reference's table capacity WP_MAX_SEGMENTS (warp_pipe_metadata.h:10);
 // build_segments keeps it as its K limit (segment_builder.cpp:12-14).
 constexpr int kRefMaxSegments = 256;
-// Tokens per work block: one adapter's weights are streamed once per block.
+// Most tokens per work block, and the slot stride of bperm: one adapter's
+// weights are streamed once per block.
 constexpr int kBlockTokens = 64;
+// Plans over at most this many tokens (decode-sized steps) cut blocks at 16
+// tokens instead, one MFMA token tile: more, shorter blocks spread a hot
+// adapter over more workgroups, and its repeated weight reads are served by
+// the caches while the blocks run side by side.
+constexpr int kSmallPlanTokens = 512;
+inline constexpr int plan_block_tokens(int64_t T) { return T <= kSmallPlanTokens ? 16 : kBlockTokens; }
+// Stride (in 32-bit words) between two blocks' cross-workgroup counters: one
+// 256-byte line each, so polls and increments of different blocks never share
+// a line.
+constexpr int kCounterStride = 64;
 // Largest T the on-device plan builder takes in one workgroup (LDS-resident).
 constexpr int kPlanMaxTokens = 8192;
 // Output slices one add_lora call may expand into (q/k/v/...).
@@ -40,6 +53,7 @@ enum HeaderWord : int {
   kHdrNumValid = 3,
   kHdrT = 4,
   kHdrErrors = 5,
+  kHdrBlockTokens = 6,
   kHdrWords = 16
 };
 
@@ -47,7 +61,8 @@ enum HeaderWord : int {
 enum DeviceError : uint32_t {
   kErrIdRange = 1u,       // stacked weights: adapter id >= num_loras
   kErrUnregistered = 2u,  // adapter table: id not registered / not resident
-  kErrShape = 4u          // adapter rank / d / o differs from the call's
+  kErrShape = 4u,         // adapter rank / d / o differs from the call's
+  kErrSpin = 8u           // a fused call's expand side gave up waiting
 };
 
 struct Segment {  // 16 B; the reference descriptor's first three fields
@@ -103,7 +118,7 @@ struct PlanView {
   const Segment* segments;
   const Block* blocks;
   const int32_t* perm;
-  uint32_t* counters;
+  const int32_t* bperm;
 };
 
 }  // namespace wp

@@ -67,6 +67,11 @@ int wp_abi_version(void);
  * warp_pipe_rank_supported (csrc/dispatch/warp_pipe_dispatcher.cpp:18). */
 int wp_rank_supported(int32_t rank);
 
+/* Most tokens per work block in a plan over T tokens (16 for T <= 512, else
+ * 64), as wp_read_plan reports the blocks.  No reference counterpart: the
+ * by-adapter blocking is this library's own. */
+int wp_block_tokens(int64_t T);
+
 /* ---- engine lifetime ---------------------------------------------------- */
 
 /* Replaces WarpPipeExtension::WarpPipeExtension (bindings:20-34): creates the

@@ -12,14 +12,11 @@ import numpy as np
 import pytest
 import torch
 
-from adapterslotsplusplus_amd import WarpPipeConfig, WarpPipeEngine
+from adapterslotsplusplus_amd import WarpPipeConfig, WarpPipeEngine, _lib
 from oracle import segments as so
 from tests.helpers import announce
 
 pytestmark = pytest.mark.gpu
-
-BLOCK_TOKENS = 64
-
 
 @pytest.fixture(scope="module")
 def engine():
@@ -32,12 +29,14 @@ def kat(golden_dir, name):
 
 
 def oracle_blocks(idx):
+    """Blocks of at most wp_block_tokens(T) tokens cut from each adapter's group."""
+    bt = _lib.load().wp_block_tokens(len(idx))
     perm, gid, goff = so.group_tokens(idx)
     blocks = []
     for g in range(gid.size):
         n = int(goff[g + 1] - goff[g])
-        for j in range(0, n, BLOCK_TOKENS):
-            blocks.append((int(gid[g]), int(goff[g]) + j, min(BLOCK_TOKENS, n - j), int(gid[g])))
+        for j in range(0, n, bt):
+            blocks.append((int(gid[g]), int(goff[g]) + j, min(bt, n - j), int(gid[g])))
     return perm.tolist(), blocks
 
 

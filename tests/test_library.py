@@ -39,6 +39,12 @@ def test_abi_version_and_rank_table():
         assert lib.wp_rank_supported(r) == 0
 
 
+def test_block_size_rule():
+    lib = _lib.load()
+    for T, bt in ((0, 16), (1, 16), (256, 16), (512, 16), (513, 64), (2048, 64), (8192, 64)):
+        assert lib.wp_block_tokens(T) == bt, T
+
+
 def test_library_contains_gfx950_code():
     data = open(_lib.LIB_PATH, "rb").read()
     assert b"gfx950" in data
