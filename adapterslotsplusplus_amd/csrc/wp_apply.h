@@ -18,8 +18,10 @@ struct ApplyArgs {
   int32_t d_model;
   int32_t rank;       // 8/16/32/64, or 0 for mixed ranks (per adapter)
   int32_t dc;         // shrink d-range per workgroup, multiple of 128
-  int32_t n_chunks;   // ceil(d_model / dc): shrink workgroups per block
-  int32_t n_ochunks;  // expand workgroups per block (all slices)
+  int32_t n_chunks;   // ceil(d_model / dc): d-ranges, i.e. partials per H value
+  int32_t n_rgroups;  // rank groups of kShrinkRows rows; n_chunks * n_rgroups shrink workgroups per block
+  int32_t n_ochunks;  // 256-column output chunks per block (all slices)
+  int32_t n_sub;      // output chunks per expand workgroup (fused), else 1
   int32_t n_slots;    // block slots of the grid (>= the plan's block count)
   int32_t hs;         // elements per H row: rank, or 64 for mixed ranks
   int32_t ptok;       // rows per chunk of `part` (plan positions)

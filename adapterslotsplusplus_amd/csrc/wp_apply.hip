@@ -12,9 +12,10 @@
 // csrc/kernels/warp_pipe_r32.cu:280-423) runs both halves of a call in ONE
 // launch, which saves a ~1.7 us graph launch per call:
 //
-//   shrink workgroups   block b, d-range c (split-K).  The four waves split the
-//                       d-range and reduce through LDS; the workgroup stores
-//                       its fp32 partial H coherently and counts done[b].
+//   shrink workgroups   block b, d-range c, 16 rank rows.  The four waves
+//                       split the d-range and reduce through LDS; the
+//                       workgroup stores its fp32 partial H coherently and
+//                       counts done[b].
 //   expand workgroups   block b, 256 output columns.  They load their B rows
 //                       and current Y, wait until done[b] counts every shrink
 //                       workgroup of the block, sum the partials in a fixed
@@ -72,11 +73,12 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kOT = 4;                  // output tiles per wave in expand
 constexpr int kOC = kWaves * kOT * 16;  // output columns per expand workgroup (256)
-constexpr int kShrinkKSteps = 2;        // 32-wide K-steps per wave per load batch
+constexpr int kShrinkKSteps = 4;        // 32-wide K-steps per wave per load batch
 // Bound of the partials wait: polls of ~1 us each, so about 0.1 s.
 constexpr unsigned kSpinLimit = 1u << 17;
 
-enum Role : int { kFused = 0, kShrinkOnly = 1, kExpandOnly = 2 };
+// kFusedMulti: fused, with several output chunks per expand workgroup.
+enum Role : int { kFused = 0, kShrinkOnly = 1, kExpandOnly = 2, kFusedMulti = 3 };
 
 __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -226,71 +228,59 @@ __device__ __forceinline__ int32_t block_token(const ApplyArgs& a, int b, int tl
 
 // ---------------------------------------------------------------- shrink ----
 
-// Partial H of block b over d-range c, stored coherently to part[c].  Token
-// tiles are processed one after another (the wave's A rows are re-read from
-// L1 for tiles after the first); within a tile the loads of each batch of
+// Partial H of block b over d-range c for rank rows [r_begin, r_begin + 16),
+// stored coherently to part[c].  The rows are the MFMA tile's M side (rows
+// past the adapter's rank load zeros and are not stored).  Token tiles are
+// processed one after another; within a tile the loads of each batch of
 // K-steps are issued before the MFMAs that consume them.  Every shrink
-// workgroup then counts done[b], whether or not the block was computable.
-template <typename T, int RANK>
-__device__ __forceinline__ void shrink_body(const ApplyArgs& a, int b, int c, const Block& blk, int32_t tok0,
-                                            const Resolved<T>& res, f32x4* s_red) {
+// workgroup then counts done[b], whether or not it had rows to compute.
+template <typename T>
+__device__ __forceinline__ void shrink_body(const ApplyArgs& a, int b, int c, int r_begin, const Block& blk,
+                                            int32_t tok0, const Resolved<T>& res, f32x4* s_red) {
   using V8 = typename VecOf<T>::v8;
-  constexpr int RT = (RANK + 15) / 16;
   constexpr int KB = kShrinkKSteps;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int row = lane & 15;
   const int kq = (lane >> 4) * 8;
-  if (res.ptr != nullptr) {
+  const int n_rows = min(kShrinkRows, res.rank - r_begin);
+  if (res.ptr != nullptr && n_rows > 0) {
     const int d = a.d_model;
     const int kw_len = a.dc / kWaves;
     const int k_begin = c * a.dc + wave * kw_len;
     const int k_end = min(k_begin + kw_len, d);
     const int ntt = (blk.count + 15) >> 4;
     const T* X = static_cast<const T*>(a.x);
-    const T* ar[RT];
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-      const int r = rt * 16 + row;
-      ar[rt] = r < RANK ? res.ptr + static_cast<int64_t>(r) * d : nullptr;
-    }
-    float* prow = a.part + (static_cast<int64_t>(c) * a.ptok + blk.first) * a.hs;
+    const T* ar = row < n_rows ? res.ptr + static_cast<int64_t>(r_begin + row) * d : nullptr;
+    float* prow = a.part + (static_cast<int64_t>(c) * a.ptok + blk.first) * a.hs + r_begin;
     for (int tt = 0; tt < ntt; ++tt) {
       const int32_t tok = tt == 0 ? tok0 : block_token(a, b, tt * 16 + row, blk.count);
       const T* xr = tok >= 0 ? X + static_cast<int64_t>(tok) * a.ldx : nullptr;
-      f32x4 acc[RT];
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      f32x4 acc{0.f, 0.f, 0.f, 0.f};
       for (int k = k_begin; k < k_end; k += 32 * KB) {
-        V8 af[KB][RT];
+        V8 af[KB];
         V8 xf[KB];
 #pragma unroll
         for (int st = 0; st < KB; ++st) {
           const int kk = k + st * 32 + kq;
           const bool in = kk < k_end;
-#pragma unroll
-          for (int rt = 0; rt < RT; ++rt) af[st][rt] = (ar[rt] != nullptr && in) ? load8(ar[rt] + kk) : zero8<T>();
+          af[st] = (ar != nullptr && in) ? load8(ar + kk) : zero8<T>();
           xf[st] = (xr != nullptr && in) ? load8(xr + kk) : zero8<T>();
         }
 #pragma unroll
-        for (int st = 0; st < KB; ++st)
-#pragma unroll
-          for (int rt = 0; rt < RT; ++rt) acc[rt] = mfma16(af[st][rt], xf[st], acc[rt]);
+        for (int st = 0; st < KB; ++st) acc = mfma16(af[st], xf[st], acc);
       }
       // Reduce the four waves' d-slices through LDS (fixed order) and store
       // this tile's partial, coherently.
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt) s_red[(wave * RT + rt) * 64 + lane] = acc[rt];
+      s_red[wave * 64 + lane] = acc;
       __syncthreads();
-      if (threadIdx.x < RT * 64) {
-        const int ln = threadIdx.x & 63;
-        const int rt = threadIdx.x >> 6;
-        const int tl = tt * 16 + (ln & 15);
-        const int r0 = rt * 16 + (ln >> 4) * 4;
-        if (tl < blk.count && r0 < RANK) {
-          f32x4 sum = s_red[(0 * RT + rt) * 64 + ln];
+      if (threadIdx.x < 64) {
+        const int tl = tt * 16 + (lane & 15);
+        const int r0 = (lane >> 4) * 4;
+        if (tl < blk.count && r0 < n_rows) {
+          f32x4 sum = s_red[lane];
 #pragma unroll
-          for (int w = 1; w < kWaves; ++w) sum += s_red[(w * RT + rt) * 64 + ln];
+          for (int w = 1; w < kWaves; ++w) sum += s_red[w * 64 + lane];
           coherent_store_f4(prow + static_cast<int64_t>(tl) * a.hs + r0, sum);
         }
       }
@@ -311,7 +301,7 @@ __device__ __forceinline__ bool wait_partials(const ApplyArgs& a, int b, int* s_
   if (threadIdx.x == 0) {
     int ok = 1;
     unsigned spins = 0;
-    const unsigned need = static_cast<unsigned>(a.n_chunks);
+    const unsigned need = static_cast<unsigned>(a.n_chunks * a.n_rgroups);
     while (atomic_load_u(&a.done[b * kCounterStride]) < need) {
       __builtin_amdgcn_s_sleep(8);
       if (++spins > kSpinLimit) {
@@ -327,19 +317,21 @@ __device__ __forceinline__ bool wait_partials(const ApplyArgs& a, int b, int* s_
 }
 
 // H of block b: rn(alpha * sum_c part[c]) for its count x RANK values.  P
-// threads share one 4-wide unit (P = 2 when there are more than 8 chunks):
-// sub-sum s takes chunks s, s+P, ... in order, and the sub-sums are added in
+// threads share one 4-wide unit (as many as the 256 threads allow): sub-sum s
+// takes chunks s, s+P, ... in increasing order, and the sub-sums are added in
 // order s = 0..P-1, so every workgroup that reduces the block gets the same
-// bits.  Each thread issues its (at most 8) loads back to back, unpredicated:
-// a load past the last chunk re-reads the last chunk and is discarded.
-// emit(j, r0, v4) receives each unit.
+// bits.  Loads go out in unpredicated batches of four (a load past the last
+// chunk re-reads the last chunk and is discarded).  emit(j, r0, v4) receives
+// each unit.
 template <int RANK, typename Emit>
 __device__ __forceinline__ void reduce_partials(const ApplyArgs& a, const Block& blk, float alpha, f32x4* s_tmp,
                                                 Emit emit) {
   constexpr int R4 = RANK / 4;
   const int n_units = blk.count * R4;
   const int nch = a.n_chunks;
-  const int P = nch > 8 ? 2 : 1;
+  int P = 1;
+  while (P < nch && n_units * P * 2 <= kThreads) P *= 2;
+  const int nper = (nch + P - 1) / P;
   // Byte offsets from a uniform base: the workspace keeps them below 2^32.
   const uint32_t cstride = static_cast<uint32_t>(a.ptok) * static_cast<uint32_t>(a.hs) * 4u;
   const char* pbase = reinterpret_cast<const char*>(a.part + static_cast<int64_t>(blk.first) * a.hs);
@@ -353,20 +345,24 @@ __device__ __forceinline__ void reduce_partials(const ApplyArgs& a, const Block&
     f32x4 sum{0.f, 0.f, 0.f, 0.f};
     if (t < total) {
       const uint32_t o0 = static_cast<uint32_t>(j * a.hs + r0) * 4u;
-      f32x4 v[8];
+      for (int i0 = 0; i0 < nper; i0 += 4) {
+        f32x4 v[4];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int cc = min(s + i * P, nch - 1);
-        v[i] = coherent_load_f4(reinterpret_cast<const float*>(pbase + (o0 + static_cast<uint32_t>(cc) * cstride)));
+        for (int i = 0; i < 4; ++i) {
+          const int cc = min(s + (i0 + i) * P, nch - 1);
+          v[i] = coherent_load_f4(reinterpret_cast<const float*>(pbase + (o0 + static_cast<uint32_t>(cc) * cstride)));
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (s + (i0 + i) * P < nch) sum += v[i];
       }
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        if (s + i * P < nch) sum += v[i];
     }
     if (P > 1) {
       s_tmp[threadIdx.x] = sum;
       __syncthreads();
-      if (t < total && s == 0) sum += s_tmp[threadIdx.x + 1];
+      if (t < total && s == 0) {
+        for (int q = 1; q < P; ++q) sum += s_tmp[threadIdx.x + q];
+      }
       __syncthreads();
     }
     if (t < total && s == 0) emit(j, r0, sum * alpha);
@@ -379,101 +375,170 @@ __device__ __forceinline__ void reduce_partials(const ApplyArgs& a, const Block&
 template <int RANK>
 constexpr int lds_h_stride() { return RANK + 8; }
 
-template <typename T, int RANK, int ROLE>
-__device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, const Block& blk, int32_t tok0,
-                                            const Resolved<T>& res, int o_first, int o_size, int y_off,
-                                            T* s_h, f32x4* s_tmp, int* s_flag) {
-  using V8 = typename VecOf<T>::v8;
+// One 256-column output chunk of an expand workgroup: its slice's B rows and
+// where its columns land in Y.
+template <typename T>
+struct OutChunk {
+  Resolved<T> res;
+  int o_first = 0;  // first output column inside the slice
+  int o_size = 0;   // the slice's output columns
+  int y_off = 0;    // the slice's first column in Y
+};
+
+template <typename T>
+__device__ __forceinline__ OutChunk<T> out_chunk(const ApplyArgs& a, const Block& blk, int oc) {
+  int s = 0;
+  while (s + 1 < a.w.n_slices && oc >= a.w.oc_start[s + 1]) ++s;
+  OutChunk<T> c;
+  c.res = resolve_b<T>(a, blk, s);
+  c.o_first = (oc - a.w.oc_start[s]) * kOC;
+  c.o_size = a.w.o_size[s];
+  c.y_off = a.w.y_off[s];
+  return c;
+}
+
+// This wave's 64 rows of the chunk's B and token tile 0 of its Y columns (Y
+// kept packed until the MFMAs, to spare registers).
+template <typename T, int RANK>
+__device__ __forceinline__ void load_chunk(const ApplyArgs& a, const OutChunk<T>& c, int32_t tok0,
+                                           typename VecOf<T>::v8 (&bf)[kOT][(RANK + 31) / 32], u32x2 (&yq)[kOT]) {
   constexpr int KS = (RANK + 31) / 32;
-  constexpr bool kFused_ = ROLE == kFused;
-  constexpr int HS = lds_h_stride<RANK>();
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int row = lane & 15;
   const int kq = (lane >> 4) * 8;
   const int oq = (lane >> 4) * 4;
-  const int ob = o_first + wave * (kOT * 16);
-  const int ntt = (blk.count + 15) >> 4;
-  T* Y = static_cast<T*>(a.y);
-  const bool ok = res.ptr != nullptr;
-
-  // Issued before the wait: this wave's 64 rows of B and token tile 0 of Y
-  // (kept packed until the MFMAs, to spare registers during the reduction).
-  V8 bf[kOT][KS];
-  u32x2 yq[kOT];
-  f32x4 acc[kOT];
+  const int ob = c.o_first + wave * (kOT * 16);
+  const bool ok = c.res.ptr != nullptr;
 #pragma unroll
   for (int ot = 0; ot < kOT; ++ot) {
     const int o = ob + ot * 16 + row;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int k = ks * 32 + kq;
-      bf[ot][ks] = (ok && o < o_size && k < RANK) ? load8(res.ptr + static_cast<int64_t>(o) * RANK + k) : zero8<T>();
+      bf[ot][ks] = (ok && o < c.o_size && k < RANK) ? load8(c.res.ptr + static_cast<int64_t>(o) * RANK + k)
+                                                      : zero8<T>();
     }
   }
-  T* yrow0 = (ok && tok0 >= 0) ? Y + static_cast<int64_t>(tok0) * a.ldy + y_off : nullptr;
+  const T* yrow0 = (ok && tok0 >= 0) ? static_cast<const T*>(a.y) + static_cast<int64_t>(tok0) * a.ldy + c.y_off
+                                     : nullptr;
 #pragma unroll
   for (int ot = 0; ot < kOT; ++ot) {
     const int o = ob + ot * 16 + oq;
-    yq[ot] = (yrow0 != nullptr && o < o_size) ? *reinterpret_cast<const u32x2*>(yrow0 + o) : u32x2{0u, 0u};
+    yq[ot] = (yrow0 != nullptr && o < c.o_size) ? *reinterpret_cast<const u32x2*>(yrow0 + o) : u32x2{0u, 0u};
   }
+}
 
-  bool go = ok;
-  if constexpr (kFused_) {
+// Y[tokens, chunk columns] = rn(Y + H.B^T) for every token tile of the block;
+// H comes from LDS (fused) or from the caller's token-indexed H (expand()).
+template <typename T, int RANK, bool kHFromLds>
+__device__ __forceinline__ void compute_chunk(const ApplyArgs& a, int b, const Block& blk, int32_t tok0,
+                                              const OutChunk<T>& c,
+                                              const typename VecOf<T>::v8 (&bf)[kOT][(RANK + 31) / 32],
+                                              u32x2 (&yq)[kOT], const T* s_h) {
+  using V8 = typename VecOf<T>::v8;
+  constexpr int KS = (RANK + 31) / 32;
+  constexpr int HS = RANK + 8;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int row = lane & 15;
+  const int kq = (lane >> 4) * 8;
+  const int oq = (lane >> 4) * 4;
+  const int ob = c.o_first + wave * (kOT * 16);
+  const int ntt = (blk.count + 15) >> 4;
+  T* Y = static_cast<T*>(a.y);
+  for (int tt = 0; tt < ntt; ++tt) {
+    const int32_t tok = tt == 0 ? tok0 : block_token(a, b, tt * 16 + row, blk.count);
+    T* yrow = (tok >= 0) ? Y + static_cast<int64_t>(tok) * a.ldy + c.y_off : nullptr;
+    if (tt > 0) {
+#pragma unroll
+      for (int ot = 0; ot < kOT; ++ot) {
+        const int o = ob + ot * 16 + oq;
+        yq[ot] = (yrow != nullptr && o < c.o_size) ? *reinterpret_cast<const u32x2*>(yrow + o) : u32x2{0u, 0u};
+      }
+    }
+    f32x4 acc[kOT];
+#pragma unroll
+    for (int ot = 0; ot < kOT; ++ot) acc[ot] = unpack4f<T>(yq[ot]);
+    V8 hf[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int k = ks * 32 + kq;
+      if (tok < 0 || k >= RANK) {
+        hf[ks] = zero8<T>();
+      } else if constexpr (kHFromLds) {
+        hf[ks] = __builtin_bit_cast(V8, *reinterpret_cast<const u32x4*>(s_h + (tt * 16 + row) * HS + k));
+      } else {
+        hf[ks] = load8(static_cast<const T*>(a.h) + static_cast<int64_t>(tok) * a.ldh + k);
+      }
+    }
+#pragma unroll
+    for (int ot = 0; ot < kOT; ++ot)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) acc[ot] = mfma16(bf[ot][ks], hf[ks], acc[ot]);
+#pragma unroll
+    for (int ot = 0; ot < kOT; ++ot) {
+      const int o = ob + ot * 16 + oq;
+      if (yrow != nullptr && o < c.o_size) store4(yrow + o, acc[ot]);
+    }
+  }
+}
+
+// Expand workgroup `p` of block b: output chunks p, p + n_owg, ... (at most
+// n_sub of them; with several slices of equal width, one chunk per slice).
+// Chunk 0's B and Y are loaded before the wait.
+template <typename T, int RANK, int ROLE>
+__device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, const Block& blk, int32_t tok0,
+                                            T* s_h, f32x4* s_tmp, int* s_flag) {
+  using V8 = typename VecOf<T>::v8;
+  constexpr int KS = (RANK + 31) / 32;
+  constexpr bool kFusedRole = ROLE == kFused || ROLE == kFusedMulti;
+  constexpr int HS = RANK + 8;
+  const int n_owg = (a.n_ochunks + a.n_sub - 1) / a.n_sub;
+  OutChunk<T> cur = out_chunk<T>(a, blk, p);
+  if (cur.res.err != 0 && p == 0 && threadIdx.x == 0) flag_error(a.plan.header, cur.res.err);
+  V8 bf[kOT][KS];
+  u32x2 yq[kOT];
+  load_chunk<T, RANK>(a, cur, tok0, bf, yq);
+
+  bool go = cur.res.ptr != nullptr;
+  if constexpr (kFusedRole) {
     // Every expand workgroup waits, even one that cannot compute, so that the
     // last one to finish may reset the block's counters.
     const bool arrived = wait_partials(a, b, s_flag);
     go = go && arrived;
     if (go) {
-      reduce_partials<RANK>(a, blk, res.alpha, s_tmp, [&](int j, int r0, f32x4 v) {
+      reduce_partials<RANK>(a, blk, cur.res.alpha, s_tmp, [&](int j, int r0, f32x4 v) {
         *reinterpret_cast<typename VecOf<T>::v4*>(s_h + j * HS + r0) = round4<T>(v);
       });
     }
     __syncthreads();
   }
   if (go) {
-    for (int tt = 0; tt < ntt; ++tt) {
-      const int32_t tok = tt == 0 ? tok0 : block_token(a, b, tt * 16 + row, blk.count);
-      T* yrow = (tok >= 0) ? Y + static_cast<int64_t>(tok) * a.ldy + y_off : nullptr;
-      if (tt > 0) {
-#pragma unroll
-        for (int ot = 0; ot < kOT; ++ot) {
-          const int o = ob + ot * 16 + oq;
-          yq[ot] = (yrow != nullptr && o < o_size) ? *reinterpret_cast<const u32x2*>(yrow + o) : u32x2{0u, 0u};
+    if constexpr (ROLE == kFusedMulti) {
+      // Chunks after the first load when they are reached: the registers a
+      // second set would take are worth more as occupancy.
+      for (int i = 0; i < a.n_sub; ++i) {
+        const int oc = p + i * n_owg;
+        if (oc >= a.n_ochunks) break;
+        if (i > 0) {
+          cur = out_chunk<T>(a, blk, oc);
+          if (cur.res.err != 0 && p == 0 && threadIdx.x == 0) flag_error(a.plan.header, cur.res.err);
+          load_chunk<T, RANK>(a, cur, tok0, bf, yq);
         }
+        if (cur.res.ptr != nullptr) compute_chunk<T, RANK, true>(a, b, blk, tok0, cur, bf, yq, s_h);
       }
-#pragma unroll
-      for (int ot = 0; ot < kOT; ++ot) acc[ot] = unpack4f<T>(yq[ot]);
-      V8 hf[KS];
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const int k = ks * 32 + kq;
-        if (tok < 0 || k >= RANK) {
-          hf[ks] = zero8<T>();
-        } else if constexpr (kFused_) {
-          hf[ks] = __builtin_bit_cast(V8, *reinterpret_cast<const u32x4*>(s_h + (tt * 16 + row) * HS + k));
-        } else {
-          hf[ks] = load8(static_cast<const T*>(a.h) + static_cast<int64_t>(tok) * a.ldh + k);
-        }
-      }
-#pragma unroll
-      for (int ot = 0; ot < kOT; ++ot)
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) acc[ot] = mfma16(bf[ot][ks], hf[ks], acc[ot]);
-#pragma unroll
-      for (int ot = 0; ot < kOT; ++ot) {
-        const int o = ob + ot * 16 + oq;
-        if (yrow != nullptr && o < o_size) store4(yrow + o, acc[ot]);
-      }
+    } else {
+      compute_chunk<T, RANK, kFusedRole>(a, b, blk, tok0, cur, bf, yq, s_h);
     }
   }
 
-  if constexpr (kFused_) {
+  if constexpr (kFusedRole) {
     // The last expand workgroup of the block resets its counters; every
     // expand workgroup has passed its wait by then, and every shrink
     // workgroup has counted.
     if (threadIdx.x == 0) {
-      if (atomic_add_u(&a.consumed[b * kCounterStride], 1u) == static_cast<unsigned>(a.n_ochunks - 1)) {
+      if (atomic_add_u(&a.consumed[b * kCounterStride], 1u) == static_cast<unsigned>(n_owg - 1)) {
         atomic_store_u(&a.consumed[b * kCounterStride], 0u);
         atomic_store_u(&a.done[b * kCounterStride], 0u);
       }
@@ -497,20 +562,23 @@ __device__ __forceinline__ void finish_body(const ApplyArgs& a, int b, const Blo
 
 // ---------------------------------------------------------------- kernels ----
 
-// Occupancy target: rank 64 and mixed ranks need the most registers and run
-// at 5 waves per SIMD; for ranks up to 32 the fused kernel (B and Y held
-// across the partials' reduction) runs at 6 (<= 80 VGPRs), shrink() and
-// expand() at 8 (<= 64 VGPRs).
+// Occupancy target (waves per SIMD), from the registers each variant needs
+// without spilling: the fused kernel holds B and Y across the partials'
+// reduction; rank 64 and mixed ranks hold twice the B fragments.
 template <int RANK, int ROLE>
-constexpr int waves_per_simd() { return (RANK == 0 || RANK == 64) ? 5 : (ROLE == kFused ? 6 : 8); }
+constexpr int waves_per_simd() {
+  constexpr bool wide = RANK == 0 || RANK == 64;
+  if (ROLE == kFusedMulti) return wide ? 5 : 7;
+  if (ROLE == kFused) return wide ? 5 : 7;
+  return wide ? 5 : 8;
+}
 
 // LDS of one workgroup: shrink's cross-wave tiles, or expand's block H plus
 // the reduction's exchange buffer.
 template <typename T, int RANK>
 struct alignas(16) SharedMem {
   static constexpr int RR = RANK == 0 ? kMaxRank : RANK;
-  static constexpr int RT = (RR + 15) / 16;
-  static constexpr int kRed = kWaves * RT * 64;                        // f32x4
+  static constexpr int kRed = kWaves * 64;                             // f32x4
   static constexpr int kH = (kBlockTokens * (RR + 8) * 2 + 15) / 16;   // f32x4 worth of T
   static constexpr int kExp = kH + kThreads;
   f32x4 buf[kRed > kExp ? kRed : kExp];
@@ -525,14 +593,15 @@ void apply_kernel(ApplyArgs a) {
   f32x4* s_red = smem.buf;
   T* s_h = reinterpret_cast<T*>(smem.buf);
   f32x4* s_tmp = smem.buf + SM::kH;
-  const int S = ROLE == kExpandOnly ? 0 : a.n_slots * a.n_chunks;
-  const int per_block = ROLE == kShrinkOnly ? 1 : a.n_ochunks;
+  const int per_shrink = a.n_chunks * a.n_rgroups;
+  const int S = ROLE == kExpandOnly ? 0 : a.n_slots * per_shrink;
+  const int per_block = ROLE == kShrinkOnly ? 1 : (a.n_ochunks + a.n_sub - 1) / a.n_sub;
   const int wg = static_cast<int>(blockIdx.x);
   const bool shrink_role = wg < S;
   int b, part;
   if (shrink_role) {
-    b = wg / a.n_chunks;
-    part = wg - b * a.n_chunks;
+    b = wg / per_shrink;
+    part = wg - b * per_shrink;
   } else {
     const int e = wg - S;
     b = e / per_block;
@@ -550,16 +619,8 @@ void apply_kernel(ApplyArgs a) {
     const Resolved<T> res = resolve_a<T>(a, blk);
     if (shrink_role) {
       if (res.err != 0 && part == 0 && threadIdx.x == 0) flag_error(a.plan.header, res.err);
-      if constexpr (RANK != 0) {
-        shrink_body<T, RANK>(a, b, part, blk, t0, res, s_red);
-      } else {
-        switch (res.rank) {
-          case 16: shrink_body<T, 16>(a, b, part, blk, t0, res, s_red); break;
-          case 32: shrink_body<T, 32>(a, b, part, blk, t0, res, s_red); break;
-          case 64: shrink_body<T, 64>(a, b, part, blk, t0, res, s_red); break;
-          default: shrink_body<T, 8>(a, b, part, blk, t0, res, s_red); break;
-        }
-      }
+      const int rg = part / a.n_chunks;
+      shrink_body<T>(a, b, part - rg * a.n_chunks, rg * kShrinkRows, blk, t0, res, s_red);
     } else if constexpr (ROLE == kShrinkOnly) {
       if constexpr (RANK != 0) {
         finish_body<T, RANK>(a, b, blk, res, s_tmp, &s_flag);
@@ -575,21 +636,16 @@ void apply_kernel(ApplyArgs a) {
     return;
   }
   if constexpr (ROLE != kShrinkOnly) {
-    int s = 0;
-    while (s + 1 < a.w.n_slices && part >= a.w.oc_start[s + 1]) ++s;
-    const int o_first = (part - a.w.oc_start[s]) * kOC;
-    const Resolved<T> res = resolve_b<T>(a, blk, s);
-    if (res.err != 0 && part == 0 && threadIdx.x == 0) flag_error(a.plan.header, res.err);
-    const int o_size = a.w.o_size[s];
-    const int y_off = a.w.y_off[s];
     if constexpr (RANK != 0) {
-      expand_body<T, RANK, ROLE>(a, b, blk, t0, res, o_first, o_size, y_off, s_h, s_tmp, &s_flag);
+      expand_body<T, RANK, ROLE>(a, b, part, blk, t0, s_h, s_tmp, &s_flag);
     } else {
-      switch (res.rank) {
-        case 16: expand_body<T, 16, ROLE>(a, b, blk, t0, res, o_first, o_size, y_off, s_h, s_tmp, &s_flag); break;
-        case 32: expand_body<T, 32, ROLE>(a, b, blk, t0, res, o_first, o_size, y_off, s_h, s_tmp, &s_flag); break;
-        case 64: expand_body<T, 64, ROLE>(a, b, blk, t0, res, o_first, o_size, y_off, s_h, s_tmp, &s_flag); break;
-        default: expand_body<T, 8, ROLE>(a, b, blk, t0, res, o_first, o_size, y_off, s_h, s_tmp, &s_flag); break;
+      // Mixed ranks: the block's adapter decides (resolved again inside).
+      const Resolved<T> r0 = resolve_b<T>(a, blk, 0);
+      switch (r0.rank) {
+        case 16: expand_body<T, 16, ROLE>(a, b, part, blk, t0, s_h, s_tmp, &s_flag); break;
+        case 32: expand_body<T, 32, ROLE>(a, b, part, blk, t0, s_h, s_tmp, &s_flag); break;
+        case 64: expand_body<T, 64, ROLE>(a, b, part, blk, t0, s_h, s_tmp, &s_flag); break;
+        default: expand_body<T, 8, ROLE>(a, b, part, blk, t0, s_h, s_tmp, &s_flag); break;
       }
     }
   }
@@ -597,8 +653,8 @@ void apply_kernel(ApplyArgs a) {
 
 template <typename T, int ROLE>
 hipError_t launch_rank(const ApplyArgs& a, hipStream_t stream) {
-  const int64_t S = ROLE == kExpandOnly ? 0 : static_cast<int64_t>(a.n_slots) * a.n_chunks;
-  const int64_t E = static_cast<int64_t>(a.n_slots) * (ROLE == kShrinkOnly ? 1 : a.n_ochunks);
+  const int64_t S = ROLE == kExpandOnly ? 0 : static_cast<int64_t>(a.n_slots) * a.n_chunks * a.n_rgroups;
+  const int64_t E = static_cast<int64_t>(a.n_slots) * (ROLE == kShrinkOnly ? 1 : (a.n_ochunks + a.n_sub - 1) / a.n_sub);
   const int64_t n = S + E;
   if (n <= 0) return hipSuccess;
   const dim3 grid(static_cast<unsigned>(n));
@@ -623,7 +679,7 @@ hipError_t launch_role(int dtype_bf16, const ApplyArgs& a, hipStream_t stream) {
 int expand_cols_per_workgroup() { return kOC; }
 
 hipError_t launch_fused(int dtype_bf16, const ApplyArgs& a, hipStream_t stream) {
-  return launch_role<kFused>(dtype_bf16, a, stream);
+  return a.n_sub > 1 ? launch_role<kFusedMulti>(dtype_bf16, a, stream) : launch_role<kFused>(dtype_bf16, a, stream);
 }
 hipError_t launch_shrink(int dtype_bf16, const ApplyArgs& a, hipStream_t stream) {
   return launch_role<kShrinkOnly>(dtype_bf16, a, stream);

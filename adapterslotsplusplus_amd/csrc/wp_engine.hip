@@ -95,13 +95,19 @@ struct Slot {
   bool used = false;
 };
 
-// d-range per shrink workgroup: at most kMaxChunks chunks, each a multiple of 128.
-constexpr int kMaxChunks = 16;
-inline void shrink_chunks(int d, int* dc, int* n_chunks) {
-  const int nc = static_cast<int>(std::min<int64_t>(kMaxChunks, ceil_div(d, 128)));
+// Expand workgroups per block a fused call aims for.
+constexpr int kExpandWorkgroups = 16;
+
+// Shrink split of a call: rank groups, then at most kShrinkWorkgroups /
+// groups d-ranges, each a multiple of 128 (four waves x 32).
+constexpr int kMaxChunks = kShrinkWorkgroups;
+inline void shrink_split(int d, int rank, int* dc, int* n_chunks, int* n_rgroups) {
+  const int g = shrink_rank_groups(rank);
+  const int nc = static_cast<int>(std::min<int64_t>(std::max(1, kShrinkWorkgroups / g), ceil_div(d, 128)));
   const int c = static_cast<int>(ceil_div(ceil_div(d, nc), 128) * 128);
   *dc = c;
   *n_chunks = static_cast<int>(ceil_div(d, c));
+  *n_rgroups = g;
 }
 
 }  // namespace
@@ -326,6 +332,7 @@ PlanView plan_view(const wp_engine* e) {
 ApplyArgs base_args(const wp_engine* e, int rank) {
   ApplyArgs a{};
   a.rank = rank;
+  a.n_sub = 1;
   a.hs = rank == 0 ? kMaxRank : rank;
   a.ptok = e->tok_cap;
   a.part = e->part;
@@ -809,7 +816,7 @@ int wp_shrink(wp_engine* e, const void* X, void* H, int32_t d_model, int32_t ran
   a.h = H;
   a.ldh = h_row_stride;
   a.d_model = d_model;
-  shrink_chunks(d_model, &a.dc, &a.n_chunks);
+  shrink_split(d_model, rank, &a.dc, &a.n_chunks, &a.n_rgroups);
   uint32_t mask = 0;
   if ((rc = table_weights(e, stream, &a.w, &mask)) != WP_OK) return rc;
   a.w.n_slices = 1;
@@ -906,7 +913,7 @@ int wp_add_lora(wp_engine* e, void* y, const void* x, const void* wa, int64_t wa
   a.y = y;
   a.ldy = y_row_stride;
   a.d_model = d_model;
-  shrink_chunks(d_model, &a.dc, &a.n_chunks);
+  shrink_split(d_model, rank, &a.dc, &a.n_chunks, &a.n_rgroups);
   a.w.mode = kStacked;
   a.w.num_ids = num_loras;
   a.w.a_base = wa;
@@ -925,6 +932,10 @@ int wp_add_lora(wp_engine* e, void* y, const void* x, const void* wa, int64_t wa
   }
   a.w.oc_start[n_slices] = oc;
   a.n_ochunks = oc;
+  // About kExpandWorkgroups expand workgroups per block; wider outputs (several
+  // slices) give each workgroup several chunks, so that the partials of the
+  // block are summed fewer times.
+  a.n_sub = static_cast<int>(ceil_div(oc, kExpandWorkgroups));
   a.n_slots = block_bound(e, num_loras);
   WP_HIP(launch_fused(dtype == WP_DTYPE_BF16, a, stream));
   return WP_OK;

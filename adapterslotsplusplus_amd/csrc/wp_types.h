@@ -45,6 +45,15 @@ constexpr int kPlanMaxTokens = 8192;
 constexpr int kMaxSlices = 4;
 // Largest rank.
 constexpr int kMaxRank = 64;
+// Shrink work split: each block's shrink runs on kShrinkWorkgroups
+// workgroups, each owning kShrinkRows rank rows (one MFMA tile) over one
+// d-range; the d-range count times the rank-group count is at most
+// kShrinkWorkgroups.  Mixed-rank calls use kMaxRank / kShrinkRows groups.
+constexpr int kShrinkRows = 16;
+constexpr int kShrinkWorkgroups = 16;
+inline constexpr int shrink_rank_groups(int rank) {
+  return rank == 0 ? kMaxRank / kShrinkRows : (rank + kShrinkRows - 1) / kShrinkRows;
+}
 
 enum HeaderWord : int {
   kHdrNumSegments = 0,
