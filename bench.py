@@ -14,6 +14,15 @@ value = algorithmic HBM bytes of the 80 calls / step time (GB/s); the bytes
 count X read once, Y read and written once and each touched adapter's A and B
 read once per call (H excluded).
 
+roofline: the dominant kernel is the fused apply kernel of the packed-qkv
+call (one launch per call, about 60% of the step).  Its average launch
+duration is measured with HIP events on the launch stream around replays of a
+graph holding only the 40 qkv launches (back to back, as in the step);
+achieved = the call's algorithmic bytes / that duration.  traffic (HBM bytes per launch) comes from the rocprofv3 --pmc
+FETCH_SIZE / WRITE_SIZE runs summarised in profiles/apply_qkv_cfg2_pmc.json,
+scaled by the same counters' reading for the plain copy this script launches
+once (COPY_BYTES read + written); null when that summary is absent.
+
 Prints one JSON line.  `--gpus N` with N > 1 exits: this build runs on one GPU.
 """
 import argparse
@@ -27,6 +36,8 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0
+COPY_BYTES = 256 << 20  # calibration copy: bytes read (and written) once
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "apply_qkv_cfg2_pmc.json")
 METRIC = "shrink+expand achieved HBM GB/s (% of peak); us per 80-call decode step"
 
 
@@ -85,6 +96,39 @@ def cpu_baseline(seconds):
                    f"{len(segs)} run-length segments), median {med * 1e6:.0f} us/call, torch fp32 per segment"),
         "us_per_call": round(med * 1e6, 1),
     }
+
+
+def launch_duration_us(calls, reps):
+    """Average duration (us) of the single kernel launch each call makes: the
+    calls are captured into one HIP graph (their launches then run back to
+    back), and HIP events on the launch stream time `reps` replays."""
+    import torch
+
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for fn in calls:
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (reps * len(calls))
+
+
+def pmc_traffic():
+    """HBM bytes per launch of the qkv apply kernel from the committed PMC
+    summary, or None."""
+    try:
+        with open(PMC_SUMMARY) as f:
+            p = json.load(f)
+        return int(p["hbm_bytes_per_launch"])
+    except (OSError, ValueError, KeyError):
+        return None
 
 
 def main():
@@ -165,28 +209,29 @@ def main():
     ms_step = ev0.elapsed_time(ev1) / args.steps
     value = bytes_step / (ms_step * 1e-3) / 1e9
 
-    # Per-call timing of the o_proj and qkv calls (eager, events on the
-    # launch stream), over the 40 distinct layers so no call hits in cache.
+    # Per-launch durations of the two fused kernels (one launch per call),
+    # over the 40 distinct layers so no call hits in cache.
     engine.build_seg_bounds(idx)
     torch.cuda.synchronize()
-    per = {}
-    for name in ("o_proj", "qkv"):
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        reps = 5
-        e0.record()
-        for _ in range(reps):
-            for ly in layers:
-                if name == "o_proj":
-                    engine.add_lora_packed(ly["y_o"], ly["x_o"], ly["wa_o"], ly["wb_o"], 0.5)
-                else:
-                    engine.add_lora_slices(ly["y_q"], ly["x_q"], ly["wa_q"], ly["wb_q"], 0.5, offs)
-        e1.record()
-        torch.cuda.synchronize()
-        per[name] = e0.elapsed_time(e1) * 1e3 / (reps * n_layers)
-    call_bytes_avg = (bytes_qkv + bytes_o) / 2
-    call_us_avg = (per["o_proj"] + per["qkv"]) / 2
-    achieved = call_bytes_avg / (call_us_avg * 1e-6) / 1e9
+
+    def qkv_call(ly):
+        return lambda: engine.add_lora_slices(ly["y_q"], ly["x_q"], ly["wa_q"], ly["wb_q"], 0.5, offs)
+
+    def o_call(ly):
+        return lambda: engine.add_lora_packed(ly["y_o"], ly["x_o"], ly["wa_o"], ly["wb_o"], 0.5)
+
+    reps = max(1, args.steps // 2)
+    qkv_us = launch_duration_us([qkv_call(ly) for ly in layers], reps)
+    o_us = launch_duration_us([o_call(ly) for ly in layers], reps)
+    achieved = bytes_qkv / (qkv_us * 1e-6) / 1e9
+
+    # Calibration copy for the PMC runs: reads and writes COPY_BYTES once.
+    src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
 
     out = {
         "metric": METRIC,
@@ -216,10 +261,15 @@ def main():
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": None,
-            "kernel": "add_lora call (shrink + expand launches), eager, per-call HIP events",
-            "us_per_call": {k: round(v, 3) for k, v in per.items()},
-            "bytes_per_call": {"o_proj": bytes_o, "qkv": bytes_qkv},
+            "traffic": pmc_traffic(),
+            "kernel": "wp::apply_kernel<__bf16, 32, kFusedMulti> (packed-qkv call: shrink + expand, one launch)",
+            "bytes_per_launch": bytes_qkv,
+            "us_per_launch": round(qkv_us, 3),
+            "other_kernels": {
+                "wp::apply_kernel<__bf16, 32, kFused> (o_proj call)": {
+                    "us_per_launch": round(o_us, 3), "bytes_per_launch": bytes_o,
+                    "achieved": round(bytes_o / (o_us * 1e-6) / 1e9, 2)},
+            },
         },
     }
     if not args.no_cpu_baseline:
