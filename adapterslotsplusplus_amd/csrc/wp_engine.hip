@@ -18,7 +18,7 @@
 //   * Staging slots are sized per adapter (the reference's fixed 512 KiB slots
 //     overflow for rank 64 x 13824), eviction releases the id's slot, and a slot
 //     is never overwritten before the kernels that read it have finished.
-//   * Every scratch buffer (fp32 partials, published H, counters, plan arrays) is
+//   * Every scratch buffer (fp32 partials, counters, plan arrays) is
 //     allocated at engine creation, so calls allocate nothing and graph
 //     replays keep valid pointers.
 #include <hip/hip_runtime.h>
