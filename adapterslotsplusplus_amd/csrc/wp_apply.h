@@ -25,8 +25,7 @@ struct ApplyArgs {
   int32_t n_slots;    // block slots of the grid (>= the plan's block count)
   int32_t hs;         // elements per H row: rank, or 64 for mixed ranks
   int32_t ptok;       // rows per chunk of `part` (plan positions)
-  float* part;        // fp32 partial H by plan position: [n_chunks][ptok][hs]
-  uint32_t* done;     // per block (stride kCounterStride): shrink workgroups published, zero between calls
+  float* part;        // fp32 partial H by plan position: [n_chunks][ptok][hs], kPartialEmpty between calls
   uint32_t* consumed; // per block (stride kCounterStride): expand workgroups finished, zero between calls
   PlanView plan;
   Weights w;

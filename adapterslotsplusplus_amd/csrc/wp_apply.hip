@@ -14,24 +14,26 @@
 //
 //   shrink workgroups   block b, d-range c, 16 rank rows.  The four waves
 //                       split the d-range and reduce through LDS; the
-//                       workgroup stores its fp32 partial H coherently and
-//                       counts done[b].
-//   expand workgroups   block b, 256 output columns.  They load their B rows
-//                       and current Y, wait until done[b] counts every shrink
-//                       workgroup of the block, sum the partials in a fixed
+//                       workgroup stores its fp32 partial H coherently.
+//   expand workgroups   block b, 256 output columns (of each slice).  They
+//                       load their B rows and current Y, wait until the
+//                       block's partials hold values (the buffer holds the
+//                       NaN pattern kPartialEmpty between calls, which no
+//                       bf16/fp16 computation produces), sum them in a fixed
 //                       order (so every workgroup, and every run, gets the
 //                       same bits), apply alpha once and round H to the I/O
 //                       dtype in LDS (reference :129, :360), then run the
 //                       MFMAs and store Y = rn(Y + H.B^T) (reference :194).
-//                       The last one of the block resets its counters.
+//                       The last one of the block empties its partials again.
 //
 // Summing the partials in every expand workgroup re-reads a few KB per
-// workgroup but keeps the cross-workgroup chain to one hop: partial stores,
-// their acknowledgement, one counter increment, the expand side's poll.
-// Data crosses workgroups only through device-scope atomic loads and stores
-// (sc1: coherent across the XCDs' L2s) ordered by s_waitcnt, and counters --
-// never through __threadfence, whose L2 writeback + invalidate costs
-// ~60-100 ns serialised over the device, nor through accumulation atomics.
+// workgroup but keeps the cross-workgroup chain to one hop: the partial
+// stores themselves are the publication (no acknowledgement wait, no
+// counter), and the readers validate every word they use.  Data crosses
+// workgroups only through device-scope atomic loads and stores (sc1:
+// coherent across the XCDs' L2s) -- never through __threadfence, whose L2
+// writeback + invalidate costs ~60-100 ns serialised over the device, nor
+// through accumulation atomics.
 //
 // Grid: the shrink workgroups of every block slot, then the expand (or, for
 // shrink(), one finishing) workgroups.  Those wait only on shrink workgroups,
@@ -232,8 +234,9 @@ __device__ __forceinline__ int32_t block_token(const ApplyArgs& a, int b, int tl
 // stored coherently to part[c].  The rows are the MFMA tile's M side (rows
 // past the adapter's rank load zeros and are not stored).  Token tiles are
 // processed one after another; within a tile the loads of each batch of
-// K-steps are issued before the MFMAs that consume them.  Every shrink
-// workgroup then counts done[b], whether or not it had rows to compute.
+// K-steps are issued before the MFMAs that consume them.  The stores are the
+// publication: the partial buffer holds kPartialEmpty between calls, and the
+// readers poll for real values (no acknowledgement wait, no counter).
 template <typename T>
 __device__ __forceinline__ void shrink_body(const ApplyArgs& a, int b, int c, int r_begin, const Block& blk,
                                             int32_t tok0, const Resolved<T>& res, f32x4* s_red) {
@@ -287,30 +290,40 @@ __device__ __forceinline__ void shrink_body(const ApplyArgs& a, int b, int c, in
       __syncthreads();
     }
   }
-  // Publish: every wave's stores are acknowledged before the count.
-  wait_vm();
-  __syncthreads();
-  if (threadIdx.x == 0) atomic_add_u(&a.done[b * kCounterStride], 1u);
 }
 
 // ---------------------------------------------------------------- reduce ----
 
-// Waits (thread 0 polls, bounded) until all shrink workgroups of block b
-// have published their partials.  Returns false after kErrSpin.
-__device__ __forceinline__ bool wait_partials(const ApplyArgs& a, int b, int* s_flag) {
-  if (threadIdx.x == 0) {
+__device__ __forceinline__ bool is_empty(float v) { return __builtin_bit_cast(uint32_t, v) == kPartialEmpty; }
+__device__ __forceinline__ bool any_empty(f32x4 v) { return is_empty(v[0]) || is_empty(v[1]) || is_empty(v[2]) || is_empty(v[3]); }
+
+// Waits (wave 0 polls, bounded) until one probe word of every shrink
+// workgroup's partial of block b holds a value: a cheap gate before the full
+// read, which validates every word itself.  Returns false after kErrSpin.
+__device__ __forceinline__ bool wait_partials(const ApplyArgs& a, const Block& blk, int rank, int* s_flag) {
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    const int n_rg = (rank + kShrinkRows - 1) / kShrinkRows;
+    const int n_probe = a.n_chunks * n_rg;
+    const float* probe = nullptr;
+    if (lane < n_probe) {
+      const int rg = lane / a.n_chunks;
+      const int kc = lane - rg * a.n_chunks;
+      probe = a.part + (static_cast<int64_t>(kc) * a.ptok + blk.first) * a.hs + rg * kShrinkRows;
+    }
     int ok = 1;
-    unsigned spins = 0;
-    const unsigned need = static_cast<unsigned>(a.n_chunks * a.n_rgroups);
-    while (atomic_load_u(&a.done[b * kCounterStride]) < need) {
-      __builtin_amdgcn_s_sleep(8);
-      if (++spins > kSpinLimit) {
+    for (unsigned spins = 0;; ++spins) {
+      const bool here = probe == nullptr || !is_empty(__builtin_bit_cast(float, atomic_load_u(
+                                                reinterpret_cast<const uint32_t*>(probe))));
+      if (__all(here)) break;
+      if (spins >= kSpinLimit) {
         ok = 0;
-        flag_error(a.plan.header, kErrSpin);
+        if (lane == 0) flag_error(a.plan.header, kErrSpin);
         break;
       }
+      __builtin_amdgcn_s_sleep(8);
     }
-    *s_flag = ok;
+    if (lane == 0) *s_flag = ok;
   }
   __syncthreads();
   return *s_flag != 0;
@@ -321,8 +334,9 @@ __device__ __forceinline__ bool wait_partials(const ApplyArgs& a, int b, int* s_
 // takes chunks s, s+P, ... in increasing order, and the sub-sums are added in
 // order s = 0..P-1, so every workgroup that reduces the block gets the same
 // bits.  Loads go out in unpredicated batches of four (a load past the last
-// chunk re-reads the last chunk and is discarded).  emit(j, r0, v4) receives
-// each unit.
+// chunk re-reads the last chunk and is discarded); a pass in which any word
+// still held kPartialEmpty is read again by the whole workgroup.
+// emit(j, r0, v4) receives each unit.
 template <int RANK, typename Emit>
 __device__ __forceinline__ void reduce_partials(const ApplyArgs& a, const Block& blk, float alpha, f32x4* s_tmp,
                                                 Emit emit) {
@@ -338,34 +352,88 @@ __device__ __forceinline__ void reduce_partials(const ApplyArgs& a, const Block&
   const int total = n_units * P;
   for (int t0 = 0; t0 < total; t0 += kThreads) {
     const int t = t0 + static_cast<int>(threadIdx.x);
+    const bool active = t < total;
     const int u = t / P;
     const int s = t - u * P;
     const int j = u / R4;
     const int r0 = (u - j * R4) * 4;
-    f32x4 sum{0.f, 0.f, 0.f, 0.f};
-    if (t < total) {
-      const uint32_t o0 = static_cast<uint32_t>(j * a.hs + r0) * 4u;
-      for (int i0 = 0; i0 < nper; i0 += 4) {
-        f32x4 v[4];
+    const uint32_t o0 = static_cast<uint32_t>(j * a.hs + r0) * 4u;
+    f32x4 sum;
+    // The whole pass is read again (by every thread) if any word was empty.
+    for (unsigned spins = 0;; ++spins) {
+      sum = f32x4{0.f, 0.f, 0.f, 0.f};
+      bool missing = false;
+      if (active) {
+        for (int i0 = 0; i0 < nper; i0 += 4) {
+          f32x4 v[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int cc = min(s + (i0 + i) * P, nch - 1);
-          v[i] = coherent_load_f4(reinterpret_cast<const float*>(pbase + (o0 + static_cast<uint32_t>(cc) * cstride)));
+          for (int i = 0; i < 4; ++i) {
+            const int cc = min(s + (i0 + i) * P, nch - 1);
+            v[i] = coherent_load_f4(reinterpret_cast<const float*>(pbase + (o0 + static_cast<uint32_t>(cc) * cstride)));
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            missing = missing || any_empty(v[i]);
+            if (s + (i0 + i) * P < nch) sum += v[i];
+          }
         }
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (s + (i0 + i) * P < nch) sum += v[i];
       }
+      if (!__syncthreads_or(missing)) break;
+      if (spins >= kSpinLimit) {
+        if (threadIdx.x == 0) flag_error(a.plan.header, kErrSpin);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(4);
     }
     if (P > 1) {
       s_tmp[threadIdx.x] = sum;
       __syncthreads();
-      if (t < total && s == 0) {
+      if (active && s == 0) {
         for (int q = 1; q < P; ++q) sum += s_tmp[threadIdx.x + q];
       }
       __syncthreads();
     }
-    if (t < total && s == 0) emit(j, r0, sum * alpha);
+    if (active && s == 0) emit(j, r0, sum * alpha);
+  }
+}
+
+// Waits until every partial word the block's shrink workgroups write (count x
+// rank values of every d-range) holds a value, without using them.
+__device__ __forceinline__ void await_partials(const ApplyArgs& a, const Block& blk, int rank) {
+  const int r4 = rank / 4;
+  const int per_chunk = blk.count * r4;
+  const int total = per_chunk * a.n_chunks;
+  for (int u = threadIdx.x; u < total; u += kThreads) {
+    const int c = u / per_chunk;
+    const int q = u - c * per_chunk;
+    const int j = q / r4;
+    const int r0 = (q - j * r4) * 4;
+    const float* p = a.part + (static_cast<int64_t>(c) * a.ptok + blk.first + j) * a.hs + r0;
+    for (unsigned spins = 0; any_empty(coherent_load_f4(p)); ++spins) {
+      if (spins >= kSpinLimit) {
+        flag_error(a.plan.header, kErrSpin);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(4);
+    }
+  }
+}
+
+// Restores kPartialEmpty over everything the block's shrink workgroups wrote
+// (count x rank values of every d-range) once its last reader is done, so the
+// next call finds the buffer empty.  `nthreads` threads take part.  Like every
+// access to the partial buffer, the stores are device-coherent.
+__device__ __forceinline__ void clear_partials(const ApplyArgs& a, const Block& blk, int rank, int tid, int nthreads) {
+  const int r4 = rank / 4;
+  const int per_chunk = blk.count * r4;
+  const int total = per_chunk * a.n_chunks;
+  const f32x4 e = __builtin_bit_cast(f32x4, u32x4{kPartialEmpty, kPartialEmpty, kPartialEmpty, kPartialEmpty});
+  for (int u = tid; u < total; u += nthreads) {
+    const int c = u / per_chunk;
+    const int q = u - c * per_chunk;
+    const int j = q / r4;
+    const int r0 = (q - j * r4) * 4;
+    coherent_store_f4(a.part + (static_cast<int64_t>(c) * a.ptok + blk.first + j) * a.hs + r0, e);
   }
 }
 
@@ -497,22 +565,33 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
   const int n_owg = (a.n_ochunks + a.n_sub - 1) / a.n_sub;
   OutChunk<T> cur = out_chunk<T>(a, blk, p);
   if (cur.res.err != 0 && p == 0 && threadIdx.x == 0) flag_error(a.plan.header, cur.res.err);
+  // Rank rows the block's shrink side writes (0: it could not resolve the
+  // adapter and writes nothing).
+  const int wrote = kFusedRole ? resolve_a<T>(a, blk).rank : 0;
   V8 bf[kOT][KS];
   u32x2 yq[kOT];
   load_chunk<T, RANK>(a, cur, tok0, bf, yq);
 
   bool go = cur.res.ptr != nullptr;
+  unsigned consumed_prev = 0;
   if constexpr (kFusedRole) {
-    // Every expand workgroup waits, even one that cannot compute, so that the
-    // last one to finish may reset the block's counters.
-    const bool arrived = wait_partials(a, b, s_flag);
-    go = go && arrived;
+    go = go && wrote > 0;
     if (go) {
-      reduce_partials<RANK>(a, blk, cur.res.alpha, s_tmp, [&](int j, int r0, f32x4 v) {
-        *reinterpret_cast<typename VecOf<T>::v4*>(s_h + j * HS + r0) = round4<T>(v);
-      });
+      go = wait_partials(a, blk, wrote, s_flag);
+      if (go) {
+        reduce_partials<RANK>(a, blk, cur.res.alpha, s_tmp, [&](int j, int r0, f32x4 v) {
+          *reinterpret_cast<typename VecOf<T>::v4*>(s_h + j * HS + r0) = round4<T>(v);
+        });
+      }
+    } else if (wrote > 0) {
+      // Nothing to compute, but this may be the workgroup that empties the
+      // partials: every store must have landed first.
+      await_partials(a, blk, wrote);
     }
     __syncthreads();
+    // This workgroup has read everything it needs from the partials; the
+    // count's latency hides behind the MFMAs.
+    if (threadIdx.x == 0) consumed_prev = atomic_add_u(&a.consumed[b * kCounterStride], 1u);
   }
   if (go) {
     if constexpr (ROLE == kFusedMulti) {
@@ -534,30 +613,31 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
   }
 
   if constexpr (kFusedRole) {
-    // The last expand workgroup of the block resets its counters; every
-    // expand workgroup has passed its wait by then, and every shrink
-    // workgroup has counted.
-    if (threadIdx.x == 0) {
-      if (atomic_add_u(&a.consumed[b * kCounterStride], 1u) == static_cast<unsigned>(n_owg - 1)) {
-        atomic_store_u(&a.consumed[b * kCounterStride], 0u);
-        atomic_store_u(&a.done[b * kCounterStride], 0u);
-      }
+    // The last expand workgroup of the block to finish reading (every other
+    // one has counted) empties the block's partials and resets the counter.
+    if (threadIdx.x == 0) *s_flag = consumed_prev == static_cast<unsigned>(n_owg - 1) ? 1 : 0;
+    __syncthreads();
+    if (*s_flag != 0) {
+      if (threadIdx.x == 0) atomic_store_u(&a.consumed[b * kCounterStride], 0u);
+      if (wrote > 0) clear_partials(a, blk, wrote, threadIdx.x, kThreads);
     }
   }
 }
 
-// shrink(): one workgroup per block reduces the partials into H[token].
+// shrink(): one workgroup per block reduces the partials into H[token] and
+// empties them again.
 template <typename T, int RANK>
 __device__ __forceinline__ void finish_body(const ApplyArgs& a, int b, const Block& blk, const Resolved<T>& res,
                                             f32x4* s_tmp, int* s_flag) {
-  const bool arrived = wait_partials(a, b, s_flag);
-  if (arrived && res.ptr != nullptr) {
+  if (res.ptr == nullptr) return;
+  if (wait_partials(a, blk, res.rank, s_flag)) {
     T* H = static_cast<T*>(a.h);
     reduce_partials<RANK>(a, blk, res.alpha, s_tmp, [&](int j, int r0, f32x4 v) {
       store4(H + static_cast<int64_t>(block_token(a, b, j, blk.count)) * a.ldh + r0, v);
     });
   }
-  if (threadIdx.x == 0) atomic_store_u(&a.done[b * kCounterStride], 0u);
+  __syncthreads();
+  clear_partials(a, blk, res.rank, threadIdx.x, kThreads);
 }
 
 // ---------------------------------------------------------------- kernels ----

@@ -127,7 +127,6 @@ struct wp_engine {
   Block* blocks = nullptr;
   int32_t* perm = nullptr;
   int32_t* bperm = nullptr;     // [block_cap][kBlockTokens]
-  uint32_t* done = nullptr;     // [block_cap]
   uint32_t* consumed = nullptr; // [block_cap]
   Entry* plan_entries = nullptr;
   float* part = nullptr;        // [kMaxChunks][tok_cap][kMaxRank] fp32 partial H
@@ -336,7 +335,6 @@ ApplyArgs base_args(const wp_engine* e, int rank) {
   a.hs = rank == 0 ? kMaxRank : rank;
   a.ptok = e->tok_cap;
   a.part = e->part;
-  a.done = e->done;
   a.consumed = e->consumed;
   a.plan = plan_view(e);
   return a;
@@ -420,19 +418,21 @@ int wp_create(const wp_config* cfg_in, wp_engine** out) {
   const size_t o_blk = carve(sizeof(Block) * e->block_cap);
   const size_t o_perm = carve(sizeof(int32_t) * e->tok_cap);
   const size_t o_bperm = carve(sizeof(int32_t) * static_cast<size_t>(e->block_cap) * kBlockTokens);
-  const size_t o_done = carve(sizeof(uint32_t) * e->block_cap * kCounterStride);
   const size_t o_cons = carve(sizeof(uint32_t) * e->block_cap * kCounterStride);
   const size_t o_ent = carve(sizeof(Entry) * e->entry_cap);
   const size_t o_part = carve(sizeof(float) * kMaxChunks * static_cast<size_t>(e->tok_cap) * kMaxRank);
   if (hipMalloc(reinterpret_cast<void**>(&e->ws), off) != hipSuccess)
     return bail(fail(WP_ERR_HIP, "wp_create: workspace allocation (%zu bytes) failed", off));
   if (hipMemset(e->ws, 0, off) != hipSuccess) return bail(fail(WP_ERR_HIP, "wp_create: workspace clear failed"));
+  if (hipMemsetD32(reinterpret_cast<hipDeviceptr_t>(e->ws + o_part), static_cast<int>(kPartialEmpty),
+                   kMaxChunks * static_cast<size_t>(e->tok_cap) * kMaxRank) != hipSuccess ||
+      hipDeviceSynchronize() != hipSuccess)
+    return bail(fail(WP_ERR_HIP, "wp_create: partial buffer fill failed"));
   e->header = reinterpret_cast<uint32_t*>(e->ws + o_hdr);
   e->segs = reinterpret_cast<Segment*>(e->ws + o_seg);
   e->blocks = reinterpret_cast<Block*>(e->ws + o_blk);
   e->perm = reinterpret_cast<int32_t*>(e->ws + o_perm);
   e->bperm = reinterpret_cast<int32_t*>(e->ws + o_bperm);
-  e->done = reinterpret_cast<uint32_t*>(e->ws + o_done);
   e->consumed = reinterpret_cast<uint32_t*>(e->ws + o_cons);
   e->plan_entries = reinterpret_cast<Entry*>(e->ws + o_ent);
   e->part = reinterpret_cast<float*>(e->ws + o_part);
@@ -749,8 +749,10 @@ int wp_read_device_errors(wp_engine* e, uint32_t* flags, void* stream_) {
   WP_HIP(hipMemcpyAsync(e->header + kHdrErrors, e->pinned_zero, sizeof(v), hipMemcpyHostToDevice, stream));
   WP_HIP(hipStreamSynchronize(stream));
   if (v & kErrSpin) {
-    // A wait that gave up leaves the per-block counters undefined: clear them.
-    WP_HIP(hipMemsetAsync(e->done, 0, sizeof(uint32_t) * e->block_cap * kCounterStride, stream));
+    // A wait that gave up leaves the partial buffer and the per-block
+    // counters undefined: empty and clear them.
+    WP_HIP(hipMemsetD32Async(reinterpret_cast<hipDeviceptr_t>(e->part), static_cast<int>(kPartialEmpty),
+                             kMaxChunks * static_cast<size_t>(e->tok_cap) * kMaxRank, stream));
     WP_HIP(hipMemsetAsync(e->consumed, 0, sizeof(uint32_t) * e->block_cap * kCounterStride, stream));
     WP_HIP(hipStreamSynchronize(stream));
   }

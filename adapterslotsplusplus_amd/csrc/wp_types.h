@@ -35,6 +35,11 @@ constexpr int kBlockTokens = 64;
 // the caches while the blocks run side by side.
 constexpr int kSmallPlanTokens = 512;
 inline constexpr int plan_block_tokens(int64_t T) { return T <= kSmallPlanTokens ? 16 : kBlockTokens; }
+// Word pattern of an empty fp32 partial: a quiet NaN whose payload has bits
+// set below bit 13.  Partials are fp32 sums of products of bf16/fp16 values;
+// a NaN among them is the canonical quiet NaN or carries a payload widened
+// from a 16-bit input (bits 0..12 clear), so no computed partial equals it.
+constexpr uint32_t kPartialEmpty = 0x7FC2A5A5u;
 // Stride (in 32-bit words) between two blocks' cross-workgroup counters: one
 // 256-byte line each, so polls and increments of different blocks never share
 // a line.
