@@ -188,10 +188,12 @@ class WarpPipeEngine:
         return int(v.value)
 
     # --------------------------------------------------------------- apply --
-    def shrink(self, X, d_model, rank, total_tokens):
+    def shrink(self, X, d_model, rank, total_tokens, out=None):
         """H = rn(alpha * X . A^T) per segment; returns a new zero-initialised
         [total_tokens, rank] tensor (reference bindings:132-139).  rank=0 or
-        None: mixed ranks, H is [T, 64] with each row's first r_a columns set."""
+        None: mixed ranks, H is [T, 64] with each row's first r_a columns set.
+        `out` (not in the reference): a caller-owned [T, width] H to write
+        instead; rows outside every segment keep their contents."""
         rank = int(rank or 0)
         self._on_device(X, "X")
         dt = _dtype_code(X, "X")
@@ -201,7 +203,13 @@ class WarpPipeEngine:
         if X.numel() < T * int(d_model):
             raise RuntimeError(f"X has {X.numel()} elements, fewer than total_tokens x d_model")
         width = rank if rank else 64
-        H = torch.zeros(T, width, dtype=X.dtype, device=X.device)
+        if out is None:
+            H = torch.zeros(T, width, dtype=X.dtype, device=X.device)
+        else:
+            H = out
+            self._on_device(H, "out")
+            if H.dtype != X.dtype or not H.is_contiguous() or tuple(H.shape) != (T, width):
+                raise RuntimeError(f"out must be a contiguous [{T}, {width}] tensor of X's dtype")
         _lib.check(self._lib.wp_shrink(self._handle, _ptr(X), _ptr(H), int(d_model), rank, T, width, dt,
                                        self._stream()), "shrink")
         return H

@@ -24,6 +24,12 @@ scaled by the same counters' reading for the plain copy this script launches
 once (COPY_BYTES read + written); null when that summary is absent.
 
 Prints one JSON line.  `--gpus N` with N > 1 exits: this build runs on one GPU.
+
+`--workload` selects another measurement (each prints its own JSON line; none
+is the metric line): `flatness` (cfg2 with 1..128 resident adapters), `cfg1`
+(with its CPU baseline), `cfg3` (13B mixed-rank decode
+through registered adapters: shrink + expand), `cfg4` (prefill chunk, MFMA),
+`cfg5` (88-call draft step in one graph, plus pinned-host prefetch overlap).
 """
 import argparse
 import json
@@ -49,6 +55,7 @@ def parse():
     ap.add_argument("--layers", type=int, default=40)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample length")
+    ap.add_argument("--workload", default="cfg2", choices=["cfg2", "flatness", "cfg1", "cfg3", "cfg4", "cfg5"])
     return ap.parse_args()
 
 
@@ -131,6 +138,295 @@ def pmc_traffic():
         return None
 
 
+def graph_us(fn, reps, warmup=3):
+    """Captures fn() into one HIP graph and returns us per replay (HIP events
+    on the launch stream around `reps` back-to-back replays)."""
+    import torch
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / reps, g
+
+
+def emit(out):
+    print(json.dumps(out), flush=True)
+
+
+def run_flatness(args):
+    """cfg2 shapes with N resident adapters, N = 1..128 (Zipf(1.1), seed 1):
+    8 layers x {qkv, o_proj} with distinct weights per layer, one graph per N."""
+    import torch
+
+    from adapterslotsplusplus_amd import WarpPipeEngine
+    from adapterslotsplusplus_amd import workloads as wl
+
+    dev = torch.device("cuda", 0)
+    T, r, h, dt, n_layers = 256, 32, 4096, torch.bfloat16, 8
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(99)
+
+    def rn(shape, std):
+        return (torch.randn(*shape, generator=gen, device=dev, dtype=torch.float32) * std).to(dt)
+
+    engine = WarpPipeEngine()
+    offs = [0, h, 2 * h]
+    rows = []
+    for N in (1, 2, 4, 8, 16, 32, 64, 128):
+        idx = wl.zipf_indices(T, N, 1.1, 1).to(dev)
+        touched = len(set(idx.tolist()))
+        layers = [dict(wa_q=rn((N, 1, r, h), .02), wb_q=[rn((N, 1, h, r), .02) for _ in range(3)],
+                       wa_o=rn((N, 1, r, h), .02), wb_o=rn((N, 1, h, r), .02), x=rn((T, h), 1.),
+                       y_q=rn((T, 3 * h), 1.), y_o=rn((T, h), 1.)) for _ in range(n_layers)]
+
+        def step():
+            engine.build_seg_bounds(idx)
+            for ly in layers:
+                engine.add_lora_slices(ly["y_q"], ly["x"], ly["wa_q"], ly["wb_q"], 0.5, offs)
+                engine.add_lora_packed(ly["y_o"], ly["x"], ly["wa_o"], ly["wb_o"], 0.5)
+
+        us, _ = graph_us(step, max(5, args.steps))
+        nbytes = n_layers * (wl.algorithmic_bytes(T, h, 3 * h, [r] * touched) + wl.algorithmic_bytes(T, h, h, [r] * touched))
+        rows.append({"resident": N, "touched": touched, "us_per_16_calls": round(us, 2),
+                     "us_per_80_call_step": round(us * 5, 1), "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1)})
+        log(f"flatness N={N}: {rows[-1]}")
+        del layers
+        torch.cuda.empty_cache()
+    lat = [x["us_per_16_calls"] for x in rows]
+    emit({"workload": "cfg2 flatness: resident adapters 1..128, 8 layers x (qkv, o_proj) + build_seg_bounds per graph",
+          "rows": rows, "max_over_min_latency": round(max(lat) / min(lat), 3), "target_max_over_min": 1.15})
+
+
+def run_cfg1(args):
+    """h=4096, r=16, 4 adapters, 64 uniformly routed tokens,
+    fp16, scale 1: one call on the GPU (graph of 40 calls over distinct copies)
+    and the oracle on the host."""
+    import torch
+
+    from adapterslotsplusplus_amd import WarpPipeEngine
+    from adapterslotsplusplus_amd import workloads as wl
+    from oracle import bgmv
+    from oracle import segments as so
+
+    dt = torch.float16
+    idx = wl.uniform_indices(64, 4, seed=0)
+    x = wl.normal((64, 4096), 1.0, dt, 10)
+    wa = wl.normal((4, 1, 16, 4096), 0.02, dt, 11)
+    wb = wl.normal((4, 1, 4096, 16), 0.02, dt, 12)
+    nbytes = wl.algorithmic_bytes(64, 4096, 4096, [16] * len(set(idx.tolist())))
+    engine = WarpPipeEngine()
+    assert engine.build_seg_bounds(idx.cuda())
+    copies = [(x.cuda(), wa.cuda(), wb.cuda(), torch.zeros(64, 4096, dtype=dt, device="cuda")) for _ in range(40)]
+
+    def calls():
+        for xc, ac, bc, yc in copies:
+            engine.add_lora_packed(yc, xc, ac, bc, 1.0)
+
+    us, _ = graph_us(calls, max(5, args.steps))
+    us /= len(copies)
+    segs = so.seg_bounds(idx.numpy()).tolist()
+    y = torch.zeros(64, 4096, dtype=dt)
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    for _ in range(3):
+        bgmv.add_lora(y, x, wa, wb, 1.0, segs)
+    times = []
+    t_end = time.perf_counter() + min(args.cpu_seconds, 10.0)
+    while time.perf_counter() < t_end or len(times) < 20:
+        t0 = time.perf_counter()
+        bgmv.add_lora(y, x, wa, wb, 1.0, segs)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    cpu_us = times[len(times) // 2] * 1e6
+    emit({"workload": "cfg1: T=64, h=4096, r=16, 4 adapters uniform (seed 0), fp16, one add_lora call",
+          "bytes_per_call": nbytes, "gpu_us_per_call": round(us, 3), "gpu_GB_s": round(nbytes / (us * 1e-6) / 1e9, 1),
+          "cpu_baseline": {"us_per_call": round(cpu_us, 1), "GB_s": round(nbytes / (cpu_us * 1e-6) / 1e9, 3),
+                           "cores": cores, "kind": "port", "runs": len(times)}})
+
+
+def run_cfg3(args):
+    """13B mixed-rank decode.  T=512 Zipf(1.1) (seed 3) over
+    128 adapters with ranks uniform in {8,16,32,64} (seed 2), bf16, registered
+    in the adapter store (one engine per layer-target: the store keeps one
+    (A, B) per id, like the reference's); per layer gate and up
+    (5120 -> r -> 13824) and down (13824 -> r -> 5120), each shrink + expand."""
+    import torch
+
+    from adapterslotsplusplus_amd import WarpPipeEngine
+    from adapterslotsplusplus_amd import workloads as wl
+
+    dev = torch.device("cuda", 0)
+    dt, T, n_layers = torch.bfloat16, 512, 4
+    g = torch.Generator().manual_seed(2)
+    ranks = [int(v) for v in torch.tensor([8, 16, 32, 64])[torch.randint(0, 4, (128,), generator=g)]]
+    idx = wl.zipf_indices(T, 128, 1.1, seed=3)
+    touched = sorted(set(idx.tolist()))
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(7)
+
+    def rn(shape, std):
+        return (torch.randn(*shape, generator=gen, device=dev, dtype=torch.float32) * std).to(dt)
+
+    shapes = {"gate": (5120, 13824), "up": (5120, 13824), "down": (13824, 5120)}
+    targets = []
+    for _ in range(n_layers):
+        for name, (d_in, d_out) in shapes.items():
+            eng = WarpPipeEngine()
+            for i in touched:
+                rr = ranks[i]
+                eng.register_adapter(i, rn((rr, d_in), .02), rn((d_out, rr), .02), 16.0 / rr, rank=rr)
+            assert eng.build_seg_bounds(idx.to(dev))
+            targets.append(dict(eng=eng, name=name, d_in=d_in, d_out=d_out, X=rn((T, d_in), 1.),
+                                Y=rn((T, d_out), 1.), H=torch.zeros(T, 64, dtype=dt, device=dev)))
+    torch.cuda.synchronize()
+
+    def calls():
+        for t in targets:
+            H = t["eng"].shrink(t["X"], t["d_in"], 0, T, out=t["H"])
+            t["eng"].expand(H, t["Y"], t["d_out"], 0)
+
+    us, _ = graph_us(calls, max(5, args.steps))
+    tr = [ranks[i] for i in touched]
+    nbytes = n_layers * sum(wl.algorithmic_bytes(T, d_in, d_out, tr) for d_in, d_out in shapes.values())
+    per = {}
+    for name, (d_in, d_out) in shapes.items():
+        sel = [t for t in targets if t["name"] == name]
+
+        def one(sel=sel):
+            for t in sel:
+                H = t["eng"].shrink(t["X"], t["d_in"], 0, T, out=t["H"])
+                t["eng"].expand(H, t["Y"], t["d_out"], 0)
+
+        u, _ = graph_us(one, max(5, args.steps))
+        b = wl.algorithmic_bytes(T, d_in, d_out, tr)
+        per[name] = {"us_per_call": round(u / len(sel), 2), "bytes_per_call": b,
+                     "GB_s": round(b / (u / len(sel) * 1e-6) / 1e9, 1)}
+    emit({"workload": f"cfg3: 13B mixed-rank decode, T=512, 128 adapters ({len(touched)} touched), ranks {{8,16,32,64}}, "
+                      f"bf16, {n_layers} layers x (gate, up, down), shrink + expand per target",
+          "us_per_layer": round(us / n_layers, 2), "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1), "per_target": per})
+
+
+def run_cfg4(args):
+    """prefill chunk, T=8192 over 16 adapters (lognormal(6,1)
+    segment lengths, seed 4), r=64, fp16: per layer the packed q/k/v call
+    (3 x 4096 outputs sharing X) and the o call; 4 layers with distinct weights."""
+    import torch
+
+    from adapterslotsplusplus_amd import WarpPipeEngine
+    from adapterslotsplusplus_amd import workloads as wl
+
+    dev = torch.device("cuda", 0)
+    dt, T, h, r, n_layers = torch.float16, 8192, 4096, 64, 4
+    lens = wl.lognormal_segments(T, 16, 6.0, 1.0, seed=4)
+    idx = torch.repeat_interleave(torch.arange(16), torch.tensor(lens)).to(dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(11)
+
+    def rn(shape, std):
+        return (torch.randn(*shape, generator=gen, device=dev, dtype=torch.float32) * std).to(dt)
+
+    engine = WarpPipeEngine()
+    layers = [dict(wa_q=rn((16, 1, r, h), .02), wb_q=[rn((16, 1, h, r), .02) for _ in range(3)],
+                   wa_o=rn((16, 1, r, h), .02), wb_o=rn((16, 1, h, r), .02), x=rn((T, h), 1.),
+                   y_q=rn((T, 3 * h), 1.), y_o=rn((T, h), 1.)) for _ in range(n_layers)]
+    offs = [0, h, 2 * h]
+    assert engine.build_seg_bounds(idx)
+
+    def calls():
+        for ly in layers:
+            engine.add_lora_slices(ly["y_q"], ly["x"], ly["wa_q"], ly["wb_q"], 0.25, offs)
+            engine.add_lora_packed(ly["y_o"], ly["x"], ly["wa_o"], ly["wb_o"], 0.25)
+
+    us, _ = graph_us(calls, max(5, args.steps))
+    b_q = wl.algorithmic_bytes(T, h, 3 * h, [r] * 16)
+    b_o = wl.algorithmic_bytes(T, h, h, [r] * 16)
+    f_q = wl.algorithmic_flops(T, h, 3 * h, [r] * T)
+    f_o = wl.algorithmic_flops(T, h, h, [r] * T)
+    per_layer = us / n_layers
+    emit({"workload": "cfg4: prefill chunk T=8192, 16 adapters lognormal(6,1) (seed 4), r=64, fp16, "
+                      f"{n_layers} layers x (packed q/k/v call, o call)",
+          "us_per_layer": round(per_layer, 2), "bytes_per_layer": b_q + b_o, "flops_per_layer": f_q + f_o,
+          "GB_s": round((b_q + b_o) / (per_layer * 1e-6) / 1e9, 1),
+          "TFLOP_s": round((f_q + f_o) / (per_layer * 1e-6) / 1e12, 2),
+          "hbm_frac": round((b_q + b_o) / (per_layer * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+          "mfma_frac_fp16_dense": round((f_q + f_o) / (per_layer * 1e-6) / 2.5e15, 5)})
+
+
+def run_cfg5(args):
+    """draft step, h=2048, 22 layers x {q,k,v,o} = 88
+    calls, 32 tenants x 4 draft tokens (tenant-contiguous), r=32, bf16;
+    build_seg_bounds + 88 calls in one graph.  Then the same step replayed
+    while 4 cold adapters (one layer-target's A and B each, 256 KiB) are
+    prefetched from the pinned host store on the engine's prefetch stream."""
+    import torch
+
+    from adapterslotsplusplus_amd import WarpPipeEngine
+    from adapterslotsplusplus_amd import workloads as wl
+
+    dev = torch.device("cuda", 0)
+    dt, T, L, h, r, n_calls = torch.bfloat16, 128, 32, 2048, 32, 88
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(13)
+
+    def rn(shape, std):
+        return (torch.randn(*shape, generator=gen, device=dev, dtype=torch.float32) * std).to(dt)
+
+    engine = WarpPipeEngine()
+    was = [rn((L, 1, r, h), .02) for _ in range(n_calls)]
+    wbs = [rn((L, 1, h, r), .02) for _ in range(n_calls)]
+    xs = [rn((T, h), 1.) for _ in range(n_calls)]
+    ys = [rn((T, h), 1.) for _ in range(n_calls)]
+    idx = torch.repeat_interleave(torch.arange(L), 4).to(dev)
+
+    def step():
+        engine.build_seg_bounds(idx)
+        for i in range(n_calls):
+            engine.add_lora_packed(ys[i], xs[i], was[i], wbs[i], 0.5)
+
+    us, g = graph_us(step, max(5, args.steps))
+    nbytes = n_calls * wl.algorithmic_bytes(T, h, h, [r] * L)
+    # Cold adapters: pinned host store, prefetched while the step replays.
+    for k in range(4):
+        engine.register_adapter(1000 + k, wl.normal((r, h), .02, dt, 70 + k), wl.normal((h, r), .02, dt, 80 + k), 1.0,
+                                rank=r)
+    reps = max(5, args.steps)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        for k in range(4):
+            engine.release_prefetch(1000 + k)
+            engine.prefetch_adapter(1000 + k)
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ready = all(engine.is_prefetch_ready(1000 + k) for k in range(4))
+    us_pf = e0.elapsed_time(e1) * 1e3 / reps
+    emit({"workload": "cfg5: draft step, h=2048, 22 layers x 4 targets = 88 add_lora calls, T=128 (32 tenants x 4), "
+                      "r=32, bf16, build_seg_bounds + 88 calls in one graph",
+          "us_per_step": round(us, 1), "us_per_call": round(us / n_calls, 2), "bytes_per_step": nbytes,
+          "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1),
+          "with_4_cold_prefetches": {"us_per_step": round(us_pf, 1), "prefetches_ready": ready,
+                                     "bytes_per_prefetch": 2 * r * h * 2}})
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -138,6 +434,12 @@ def main():
                           "n_gpus": args.gpus}))
         sys.exit(2)
     import torch
+
+    if args.workload != "cfg2":
+        torch.cuda.set_device(0)
+        {"flatness": run_flatness, "cfg1": run_cfg1, "cfg3": run_cfg3, "cfg4": run_cfg4,
+         "cfg5": run_cfg5}[args.workload](args)
+        return
 
     from adapterslotsplusplus_amd import WarpPipeEngine
     from adapterslotsplusplus_amd import workloads as wl
