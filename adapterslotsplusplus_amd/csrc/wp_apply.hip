@@ -115,6 +115,12 @@ template <typename T>
 __device__ __forceinline__ void store4(T* p, f32x4 v) {
   *reinterpret_cast<u32x2*>(p) = __builtin_bit_cast(u32x2, round4<T>(v));
 }
+// Streaming store (nt): Y is written once per call and not read again by the
+// call, so its lines need not stay dirty in L2 for the end-of-kernel writeback.
+template <typename T>
+__device__ __forceinline__ void store4_stream(T* p, f32x4 v) {
+  __builtin_nontemporal_store(__builtin_bit_cast(u32x2, round4<T>(v)), reinterpret_cast<u32x2*>(p));
+}
 
 // Device-scope (sc1) 8-byte loads and stores: coherent across XCDs without
 // cache maintenance.
@@ -547,7 +553,7 @@ __device__ __forceinline__ void compute_chunk(const ApplyArgs& a, int b, const B
 #pragma unroll
     for (int ot = 0; ot < kOT; ++ot) {
       const int o = ob + ot * 16 + oq;
-      if (yrow != nullptr && o < c.o_size) store4(yrow + o, acc[ot]);
+      if (yrow != nullptr && o < c.o_size) store4_stream(yrow + o, acc[ot]);
     }
   }
 }
@@ -648,8 +654,7 @@ __device__ __forceinline__ void finish_body(const ApplyArgs& a, int b, const Blo
 template <int RANK, int ROLE>
 constexpr int waves_per_simd() {
   constexpr bool wide = RANK == 0 || RANK == 64;
-  if (ROLE == kFusedMulti) return wide ? 5 : 7;
-  if (ROLE == kFused) return wide ? 5 : 7;
+  if (ROLE == kFusedMulti || ROLE == kFused) return wide ? 5 : 7;
   return wide ? 5 : 8;
 }
 
@@ -677,7 +682,7 @@ void apply_kernel(ApplyArgs a) {
   const int S = ROLE == kExpandOnly ? 0 : a.n_slots * per_shrink;
   const int per_block = ROLE == kShrinkOnly ? 1 : (a.n_ochunks + a.n_sub - 1) / a.n_sub;
   const int wg = static_cast<int>(blockIdx.x);
-  const bool shrink_role = wg < S;
+  const bool shrink_role = ROLE != kExpandOnly && wg < S;
   int b, part;
   if (shrink_role) {
     b = wg / per_shrink;
