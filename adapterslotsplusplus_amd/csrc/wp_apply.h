@@ -22,6 +22,7 @@ struct ApplyArgs {
   int32_t n_rgroups;  // rank groups of kShrinkRows rows; n_chunks * n_rgroups shrink workgroups per block
   int32_t n_ochunks;  // 256-column output chunks per block (all slices)
   int32_t n_sub;      // output chunks per expand workgroup (fused), else 1
+  int32_t tiles;      // most 16-token tiles per block of the plan (1 or 4)
   int32_t n_slots;    // block slots of the grid (>= the plan's block count)
   int32_t hs;         // elements per H row: rank, or 64 for mixed ranks
   int32_t ptok;       // rows per chunk of `part` (plan positions)

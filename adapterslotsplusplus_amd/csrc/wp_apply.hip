@@ -76,6 +76,10 @@ constexpr int kWaves = kThreads / 64;
 constexpr int kOT = 4;                  // output tiles per wave in expand
 constexpr int kOC = kWaves * kOT * 16;  // output columns per expand workgroup (256)
 constexpr int kShrinkKSteps = 4;        // 32-wide K-steps per wave per load batch
+// Token tiles a shrink()/expand() workgroup keeps in flight (blocks of 64
+// tokens in large plans); the fused kernel, which decode-sized plans use,
+// works one tile at a time to keep its registers for occupancy.
+constexpr int kTilesInFlight = kBlockTokens / 16;
 // Bound of the partials wait: polls of ~1 us each, so about 0.1 s.
 constexpr unsigned kSpinLimit = 1u << 17;
 
@@ -238,50 +242,64 @@ __device__ __forceinline__ int32_t block_token(const ApplyArgs& a, int b, int tl
 
 // Partial H of block b over d-range c for rank rows [r_begin, r_begin + 16),
 // stored coherently to part[c].  The rows are the MFMA tile's M side (rows
-// past the adapter's rank load zeros and are not stored).  Token tiles are
-// processed one after another; within a tile the loads of each batch of
-// K-steps are issued before the MFMAs that consume them.  The stores are the
+// past the adapter's rank load zeros and are not stored).  MAXT token tiles
+// are in flight at once: each batch of K-steps loads the A fragments once and
+// the X fragments of every tile, then runs the MFMAs.  The stores are the
 // publication: the partial buffer holds kPartialEmpty between calls, and the
 // readers poll for real values (no acknowledgement wait, no counter).
-template <typename T>
+template <typename T, int MAXT>
 __device__ __forceinline__ void shrink_body(const ApplyArgs& a, int b, int c, int r_begin, const Block& blk,
                                             int32_t tok0, const Resolved<T>& res, f32x4* s_red) {
   using V8 = typename VecOf<T>::v8;
-  constexpr int KB = kShrinkKSteps;
+  constexpr int KB = MAXT == 1 ? kShrinkKSteps : 2;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int row = lane & 15;
   const int kq = (lane >> 4) * 8;
   const int n_rows = min(kShrinkRows, res.rank - r_begin);
-  if (res.ptr != nullptr && n_rows > 0) {
-    const int d = a.d_model;
-    const int kw_len = a.dc / kWaves;
-    const int k_begin = c * a.dc + wave * kw_len;
-    const int k_end = min(k_begin + kw_len, d);
-    const int ntt = (blk.count + 15) >> 4;
-    const T* X = static_cast<const T*>(a.x);
-    const T* ar = row < n_rows ? res.ptr + static_cast<int64_t>(r_begin + row) * d : nullptr;
-    float* prow = a.part + (static_cast<int64_t>(c) * a.ptok + blk.first) * a.hs + r_begin;
-    for (int tt = 0; tt < ntt; ++tt) {
-      const int32_t tok = tt == 0 ? tok0 : block_token(a, b, tt * 16 + row, blk.count);
-      const T* xr = tok >= 0 ? X + static_cast<int64_t>(tok) * a.ldx : nullptr;
-      f32x4 acc{0.f, 0.f, 0.f, 0.f};
-      for (int k = k_begin; k < k_end; k += 32 * KB) {
-        V8 af[KB];
-        V8 xf[KB];
+  if (res.ptr == nullptr || n_rows <= 0) return;
+  const int d = a.d_model;
+  const int kw_len = a.dc / kWaves;
+  const int k_begin = c * a.dc + wave * kw_len;
+  const int k_end = min(k_begin + kw_len, d);
+  const int ntt = (blk.count + 15) >> 4;
+  const T* X = static_cast<const T*>(a.x);
+  const T* ar = row < n_rows ? res.ptr + static_cast<int64_t>(r_begin + row) * d : nullptr;
+  float* prow = a.part + (static_cast<int64_t>(c) * a.ptok + blk.first) * a.hs + r_begin;
+  for (int t0 = 0; t0 < ntt; t0 += MAXT) {
+    const T* xr[MAXT];
 #pragma unroll
-        for (int st = 0; st < KB; ++st) {
-          const int kk = k + st * 32 + kq;
-          const bool in = kk < k_end;
-          af[st] = (ar != nullptr && in) ? load8(ar + kk) : zero8<T>();
-          xf[st] = (xr != nullptr && in) ? load8(xr + kk) : zero8<T>();
-        }
+    for (int i = 0; i < MAXT; ++i) {
+      const int tt = t0 + i;
+      const int32_t tok = tt == 0 ? tok0 : (tt < ntt ? block_token(a, b, tt * 16 + row, blk.count) : -1);
+      xr[i] = tok >= 0 ? X + static_cast<int64_t>(tok) * a.ldx : nullptr;
+    }
+    f32x4 acc[MAXT];
 #pragma unroll
-        for (int st = 0; st < KB; ++st) acc = mfma16(af[st], xf[st], acc);
+    for (int i = 0; i < MAXT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int k = k_begin; k < k_end; k += 32 * KB) {
+      V8 af[KB];
+      V8 xf[KB][MAXT];
+#pragma unroll
+      for (int st = 0; st < KB; ++st) {
+        const int kk = k + st * 32 + kq;
+        const bool in = kk < k_end;
+        af[st] = (ar != nullptr && in) ? load8(ar + kk) : zero8<T>();
+#pragma unroll
+        for (int i = 0; i < MAXT; ++i) xf[st][i] = (xr[i] != nullptr && in) ? load8(xr[i] + kk) : zero8<T>();
       }
-      // Reduce the four waves' d-slices through LDS (fixed order) and store
-      // this tile's partial, coherently.
-      s_red[wave * 64 + lane] = acc;
+#pragma unroll
+      for (int st = 0; st < KB; ++st)
+#pragma unroll
+        for (int i = 0; i < MAXT; ++i) acc[i] = mfma16(af[st], xf[st][i], acc[i]);
+    }
+    // Reduce the four waves' d-slices through LDS (fixed order) and store
+    // each tile's partial, coherently.
+#pragma unroll
+    for (int i = 0; i < MAXT; ++i) {
+      const int tt = t0 + i;
+      if (tt >= ntt) break;
+      s_red[wave * 64 + lane] = acc[i];
       __syncthreads();
       if (threadIdx.x < 64) {
         const int tl = tt * 16 + (lane & 15);
@@ -471,17 +489,70 @@ __device__ __forceinline__ OutChunk<T> out_chunk(const ApplyArgs& a, const Block
   return c;
 }
 
-// This wave's 64 rows of the chunk's B and token tile 0 of its Y columns (Y
-// kept packed until the MFMAs, to spare registers).
+// A lane's share of one 16-token x 64-column Y tile (the columns of its wave)
+// in row order: rows lane/8 and lane/8 + 8, 16 bytes each at column 8*(lane%8).
+// Eight lanes cover a 128-byte row, so every load and store moves whole
+// lines; the MFMA layout (4 columns of one row per lane) is produced and
+// consumed through the wave's LDS stage instead (1.6x the HBM rate of
+// accessing Y in the MFMA layout directly, measured on MI355X).
+struct YRows {
+  u32x4 v[2];
+};
+constexpr int kStageStride = 72;  // elements per staged row: 64 + 8 against bank conflicts
+
+// Tokens of this lane's two rows, from `tok_row` (the token of row lane % 16).
+__device__ __forceinline__ void yrows_tokens(int32_t tok_row, int32_t (&tok)[2]) {
+  const int lane = threadIdx.x & 63;
+  tok[0] = __shfl(tok_row, lane >> 3, 64);
+  tok[1] = __shfl(tok_row, (lane >> 3) + 8, 64);
+}
+
+template <typename T>
+__device__ __forceinline__ YRows yrows_load(const ApplyArgs& a, int y_off, int ob, int o_size, const int32_t (&tok)[2]) {
+  const int o = ob + (threadIdx.x & 7) * 8;
+  const T* Y = static_cast<const T*>(a.y);
+  YRows r;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    r.v[h] = u32x4{0u, 0u, 0u, 0u};
+    if (tok[h] < 0) continue;
+    const T* p = Y + static_cast<int64_t>(tok[h]) * a.ldy + y_off + o;
+    if (o + 8 <= o_size) {
+      r.v[h] = *reinterpret_cast<const u32x4*>(p);
+    } else if (o + 4 <= o_size) {
+      const u32x2 lo = *reinterpret_cast<const u32x2*>(p);
+      r.v[h] = u32x4{lo[0], lo[1], 0u, 0u};
+    }
+  }
+  return r;
+}
+
+template <typename T>
+__device__ __forceinline__ void yrows_store(const ApplyArgs& a, int y_off, int ob, int o_size, const int32_t (&tok)[2],
+                                            const YRows& r) {
+  const int o = ob + (threadIdx.x & 7) * 8;
+  T* Y = static_cast<T*>(a.y);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    if (tok[h] < 0) continue;
+    T* p = Y + static_cast<int64_t>(tok[h]) * a.ldy + y_off + o;
+    if (o + 8 <= o_size) {
+      __builtin_nontemporal_store(r.v[h], reinterpret_cast<u32x4*>(p));
+    } else if (o + 4 <= o_size) {
+      __builtin_nontemporal_store(u32x2{r.v[h][0], r.v[h][1]}, reinterpret_cast<u32x2*>(p));
+    }
+  }
+}
+
+// This wave's 64 rows of the chunk's B and token tile 0 of its Y columns.
 template <typename T, int RANK>
 __device__ __forceinline__ void load_chunk(const ApplyArgs& a, const OutChunk<T>& c, int32_t tok0,
-                                           typename VecOf<T>::v8 (&bf)[kOT][(RANK + 31) / 32], u32x2 (&yq)[kOT]) {
+                                           typename VecOf<T>::v8 (&bf)[kOT][(RANK + 31) / 32], YRows& y0) {
   constexpr int KS = (RANK + 31) / 32;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int row = lane & 15;
   const int kq = (lane >> 4) * 8;
-  const int oq = (lane >> 4) * 4;
   const int ob = c.o_first + wave * (kOT * 16);
   const bool ok = c.res.ptr != nullptr;
 #pragma unroll
@@ -494,22 +565,21 @@ __device__ __forceinline__ void load_chunk(const ApplyArgs& a, const OutChunk<T>
                                                       : zero8<T>();
     }
   }
-  const T* yrow0 = (ok && tok0 >= 0) ? static_cast<const T*>(a.y) + static_cast<int64_t>(tok0) * a.ldy + c.y_off
-                                     : nullptr;
-#pragma unroll
-  for (int ot = 0; ot < kOT; ++ot) {
-    const int o = ob + ot * 16 + oq;
-    yq[ot] = (yrow0 != nullptr && o < c.o_size) ? *reinterpret_cast<const u32x2*>(yrow0 + o) : u32x2{0u, 0u};
-  }
+  int32_t tok[2];
+  yrows_tokens(ok ? tok0 : -1, tok);
+  y0 = yrows_load<T>(a, c.y_off, ob, c.o_size, tok);
 }
 
 // Y[tokens, chunk columns] = rn(Y + H.B^T) for every token tile of the block;
 // H comes from LDS (fused) or from the caller's token-indexed H (expand()).
-template <typename T, int RANK, bool kHFromLds>
+// MAXT tiles are in flight at once: their Y (and H) loads are issued
+// together before the MFMAs; y0 holds tile 0's Y, already loaded.  `stage`
+// is this wave's 16 x kStageStride LDS tile.
+template <typename T, int RANK, bool kHFromLds, int MAXT>
 __device__ __forceinline__ void compute_chunk(const ApplyArgs& a, int b, const Block& blk, int32_t tok0,
                                               const OutChunk<T>& c,
                                               const typename VecOf<T>::v8 (&bf)[kOT][(RANK + 31) / 32],
-                                              u32x2 (&yq)[kOT], const T* s_h) {
+                                              const YRows& y0, const T* s_h, T* stage) {
   using V8 = typename VecOf<T>::v8;
   constexpr int KS = (RANK + 31) / 32;
   constexpr int HS = RANK + 8;
@@ -520,40 +590,55 @@ __device__ __forceinline__ void compute_chunk(const ApplyArgs& a, int b, const B
   const int oq = (lane >> 4) * 4;
   const int ob = c.o_first + wave * (kOT * 16);
   const int ntt = (blk.count + 15) >> 4;
-  T* Y = static_cast<T*>(a.y);
-  for (int tt = 0; tt < ntt; ++tt) {
-    const int32_t tok = tt == 0 ? tok0 : block_token(a, b, tt * 16 + row, blk.count);
-    T* yrow = (tok >= 0) ? Y + static_cast<int64_t>(tok) * a.ldy + c.y_off : nullptr;
-    if (tt > 0) {
+  T* st_row = stage + row * kStageStride;                                 // MFMA-layout row of this lane
+  T* st_seg = stage + (lane >> 3) * kStageStride + (lane & 7) * 8;        // row-order segment of this lane
+  for (int t0 = 0; t0 < ntt; t0 += MAXT) {
+    int32_t tok_row[MAXT];
+    int32_t tok[MAXT][2];
+    YRows yt[MAXT];
+    V8 hf[MAXT][KS];
 #pragma unroll
-      for (int ot = 0; ot < kOT; ++ot) {
-        const int o = ob + ot * 16 + oq;
-        yq[ot] = (yrow != nullptr && o < c.o_size) ? *reinterpret_cast<const u32x2*>(yrow + o) : u32x2{0u, 0u};
+    for (int i = 0; i < MAXT; ++i) {
+      const int tt = t0 + i;
+      tok_row[i] = tt == 0 ? tok0 : (tt < ntt ? block_token(a, b, tt * 16 + row, blk.count) : -1);
+      yrows_tokens(tok_row[i], tok[i]);
+      if (tt == 0)
+        yt[i] = y0;
+      else
+        yt[i] = yrows_load<T>(a, c.y_off, ob, c.o_size, tok[i]);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int k = ks * 32 + kq;
+        if (tok_row[i] < 0 || k >= RANK) {
+          hf[i][ks] = zero8<T>();
+        } else if constexpr (kHFromLds) {
+          hf[i][ks] = __builtin_bit_cast(V8, *reinterpret_cast<const u32x4*>(s_h + (tt * 16 + row) * HS + k));
+        } else {
+          hf[i][ks] = load8(static_cast<const T*>(a.h) + static_cast<int64_t>(tok_row[i]) * a.ldh + k);
+        }
       }
     }
-    f32x4 acc[kOT];
 #pragma unroll
-    for (int ot = 0; ot < kOT; ++ot) acc[ot] = unpack4f<T>(yq[ot]);
-    V8 hf[KS];
+    for (int i = 0; i < MAXT; ++i) {
+      if (t0 + i >= ntt) break;
+      // Row order -> MFMA layout through the stage (one wave, in order).
+      *reinterpret_cast<u32x4*>(st_seg) = yt[i].v[0];
+      *reinterpret_cast<u32x4*>(st_seg + 8 * kStageStride) = yt[i].v[1];
+      f32x4 acc[kOT];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int k = ks * 32 + kq;
-      if (tok < 0 || k >= RANK) {
-        hf[ks] = zero8<T>();
-      } else if constexpr (kHFromLds) {
-        hf[ks] = __builtin_bit_cast(V8, *reinterpret_cast<const u32x4*>(s_h + (tt * 16 + row) * HS + k));
-      } else {
-        hf[ks] = load8(static_cast<const T*>(a.h) + static_cast<int64_t>(tok) * a.ldh + k);
-      }
-    }
+      for (int ot = 0; ot < kOT; ++ot) acc[ot] = unpack4f<T>(*reinterpret_cast<const u32x2*>(st_row + ot * 16 + oq));
 #pragma unroll
-    for (int ot = 0; ot < kOT; ++ot)
+      for (int ot = 0; ot < kOT; ++ot)
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) acc[ot] = mfma16(bf[ot][ks], hf[ks], acc[ot]);
+        for (int ks = 0; ks < KS; ++ks) acc[ot] = mfma16(bf[ot][ks], hf[i][ks], acc[ot]);
+      // MFMA layout -> row order, then whole-line stores.
 #pragma unroll
-    for (int ot = 0; ot < kOT; ++ot) {
-      const int o = ob + ot * 16 + oq;
-      if (yrow != nullptr && o < c.o_size) store4_stream(yrow + o, acc[ot]);
+      for (int ot = 0; ot < kOT; ++ot)
+        *reinterpret_cast<u32x2*>(st_row + ot * 16 + oq) = __builtin_bit_cast(u32x2, round4<T>(acc[ot]));
+      YRows out;
+      out.v[0] = *reinterpret_cast<const u32x4*>(st_seg);
+      out.v[1] = *reinterpret_cast<const u32x4*>(st_seg + 8 * kStageStride);
+      yrows_store<T>(a, c.y_off, ob, c.o_size, tok[i], out);
     }
   }
 }
@@ -561,21 +646,22 @@ __device__ __forceinline__ void compute_chunk(const ApplyArgs& a, int b, const B
 // Expand workgroup `p` of block b: output chunks p, p + n_owg, ... (at most
 // n_sub of them; with several slices of equal width, one chunk per slice).
 // Chunk 0's B and Y are loaded before the wait.
-template <typename T, int RANK, int ROLE>
+template <typename T, int RANK, int ROLE, int TILES>
 __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, const Block& blk, int32_t tok0,
-                                            T* s_h, f32x4* s_tmp, int* s_flag) {
+                                            T* s_h, f32x4* s_tmp, T* s_stage, int* s_flag) {
   using V8 = typename VecOf<T>::v8;
   constexpr int KS = (RANK + 31) / 32;
   constexpr bool kFusedRole = ROLE == kFused || ROLE == kFusedMulti;
   constexpr int HS = RANK + 8;
   const int n_owg = (a.n_ochunks + a.n_sub - 1) / a.n_sub;
+  T* stage = s_stage + (threadIdx.x >> 6) * 16 * kStageStride;
   OutChunk<T> cur = out_chunk<T>(a, blk, p);
   if (cur.res.err != 0 && p == 0 && threadIdx.x == 0) flag_error(a.plan.header, cur.res.err);
   // Rank rows the block's shrink side writes (0: it could not resolve the
   // adapter and writes nothing).
   const int wrote = kFusedRole ? resolve_a<T>(a, blk).rank : 0;
   V8 bf[kOT][KS];
-  u32x2 yq[kOT];
+  YRows yq;
   load_chunk<T, RANK>(a, cur, tok0, bf, yq);
 
   bool go = cur.res.ptr != nullptr;
@@ -611,10 +697,10 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
           if (cur.res.err != 0 && p == 0 && threadIdx.x == 0) flag_error(a.plan.header, cur.res.err);
           load_chunk<T, RANK>(a, cur, tok0, bf, yq);
         }
-        if (cur.res.ptr != nullptr) compute_chunk<T, RANK, true>(a, b, blk, tok0, cur, bf, yq, s_h);
+        if (cur.res.ptr != nullptr) compute_chunk<T, RANK, true, 1>(a, b, blk, tok0, cur, bf, yq, s_h, stage);
       }
     } else {
-      compute_chunk<T, RANK, kFusedRole>(a, b, blk, tok0, cur, bf, yq, s_h);
+      compute_chunk<T, RANK, kFusedRole, kFusedRole ? 1 : TILES>(a, b, blk, tok0, cur, bf, yq, s_h, stage);
     }
   }
 
@@ -630,32 +716,39 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
   }
 }
 
-// shrink(): one workgroup per block reduces the partials into H[token] and
-// empties them again.
+// shrink(): finishing workgroup f of block b reduces the partials of the
+// block's token tile f into H[token] and empties them again.
 template <typename T, int RANK>
-__device__ __forceinline__ void finish_body(const ApplyArgs& a, int b, const Block& blk, const Resolved<T>& res,
-                                            f32x4* s_tmp, int* s_flag) {
-  if (res.ptr == nullptr) return;
-  if (wait_partials(a, blk, res.rank, s_flag)) {
+__device__ __forceinline__ void finish_body(const ApplyArgs& a, int b, int f, const Block& blk,
+                                            const Resolved<T>& res, f32x4* s_tmp, int* s_flag) {
+  if (res.ptr == nullptr || f * 16 >= blk.count) return;
+  Block tile = blk;
+  tile.first = blk.first + f * 16;
+  tile.count = min(16, blk.count - f * 16);
+  if (wait_partials(a, tile, res.rank, s_flag)) {
     T* H = static_cast<T*>(a.h);
-    reduce_partials<RANK>(a, blk, res.alpha, s_tmp, [&](int j, int r0, f32x4 v) {
-      store4(H + static_cast<int64_t>(block_token(a, b, j, blk.count)) * a.ldh + r0, v);
+    reduce_partials<RANK>(a, tile, res.alpha, s_tmp, [&](int j, int r0, f32x4 v) {
+      store4(H + static_cast<int64_t>(block_token(a, b, f * 16 + j, blk.count)) * a.ldh + r0, v);
     });
   }
   __syncthreads();
-  clear_partials(a, blk, res.rank, threadIdx.x, kThreads);
+  clear_partials(a, tile, res.rank, threadIdx.x, kThreads);
 }
 
 // ---------------------------------------------------------------- kernels ----
 
 // Occupancy target (waves per SIMD), from the registers each variant needs
 // without spilling: the fused kernel holds B and Y across the partials'
-// reduction; rank 64 and mixed ranks hold twice the B fragments.
-template <int RANK, int ROLE>
+// reduction; shrink() and expand() keep four token tiles in flight; rank 64
+// and mixed ranks hold twice the B fragments.
+template <int RANK, int ROLE, int TILES>
 constexpr int waves_per_simd() {
   constexpr bool wide = RANK == 0 || RANK == 64;
-  if (ROLE == kFusedMulti || ROLE == kFused) return wide ? 5 : 7;
-  return wide ? 5 : 8;
+  if (ROLE == kFused) return wide ? 5 : 7;
+  if (ROLE == kFusedMulti) return wide ? 5 : 6;
+  if (TILES == 1) return wide ? 5 : 8;
+  if (ROLE == kShrinkOnly) return 6;
+  return wide ? 3 : 5;
 }
 
 // LDS of one workgroup: shrink's cross-wave tiles, or expand's block H plus
@@ -667,10 +760,13 @@ struct alignas(16) SharedMem {
   static constexpr int kH = (kBlockTokens * (RR + 8) * 2 + 15) / 16;   // f32x4 worth of T
   static constexpr int kExp = kH + kThreads;
   f32x4 buf[kRed > kExp ? kRed : kExp];
+  T stage[kWaves * 16 * kStageStride];  // each wave's Y tile (expand)
 };
 
-template <typename T, int RANK, int ROLE>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(waves_per_simd<RANK, ROLE>())))
+// TILES: token tiles in flight per workgroup in shrink()/expand() (4 for
+// plans of 64-token blocks, else 1); the fused kernel always works with 1.
+template <typename T, int RANK, int ROLE, int TILES>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(waves_per_simd<RANK, ROLE, TILES>())))
 void apply_kernel(ApplyArgs a) {
   using SM = SharedMem<T, RANK>;
   __shared__ SM smem;
@@ -680,7 +776,7 @@ void apply_kernel(ApplyArgs a) {
   f32x4* s_tmp = smem.buf + SM::kH;
   const int per_shrink = a.n_chunks * a.n_rgroups;
   const int S = ROLE == kExpandOnly ? 0 : a.n_slots * per_shrink;
-  const int per_block = ROLE == kShrinkOnly ? 1 : (a.n_ochunks + a.n_sub - 1) / a.n_sub;
+  const int per_block = ROLE == kShrinkOnly ? kBlockTokens / 16 : (a.n_ochunks + a.n_sub - 1) / a.n_sub;
   const int wg = static_cast<int>(blockIdx.x);
   const bool shrink_role = ROLE != kExpandOnly && wg < S;
   int b, part;
@@ -705,16 +801,17 @@ void apply_kernel(ApplyArgs a) {
     if (shrink_role) {
       if (res.err != 0 && part == 0 && threadIdx.x == 0) flag_error(a.plan.header, res.err);
       const int rg = part / a.n_chunks;
-      shrink_body<T>(a, b, part - rg * a.n_chunks, rg * kShrinkRows, blk, t0, res, s_red);
+      shrink_body<T, ROLE == kShrinkOnly ? TILES : 1>(a, b, part - rg * a.n_chunks, rg * kShrinkRows, blk, t0, res,
+                                                     s_red);
     } else if constexpr (ROLE == kShrinkOnly) {
       if constexpr (RANK != 0) {
-        finish_body<T, RANK>(a, b, blk, res, s_tmp, &s_flag);
+        finish_body<T, RANK>(a, b, part, blk, res, s_tmp, &s_flag);
       } else {
         switch (res.rank) {
-          case 16: finish_body<T, 16>(a, b, blk, res, s_tmp, &s_flag); break;
-          case 32: finish_body<T, 32>(a, b, blk, res, s_tmp, &s_flag); break;
-          case 64: finish_body<T, 64>(a, b, blk, res, s_tmp, &s_flag); break;
-          default: finish_body<T, 8>(a, b, blk, res, s_tmp, &s_flag); break;
+          case 16: finish_body<T, 16>(a, b, part, blk, res, s_tmp, &s_flag); break;
+          case 32: finish_body<T, 32>(a, b, part, blk, res, s_tmp, &s_flag); break;
+          case 64: finish_body<T, 64>(a, b, part, blk, res, s_tmp, &s_flag); break;
+          default: finish_body<T, 8>(a, b, part, blk, res, s_tmp, &s_flag); break;
         }
       }
     }
@@ -722,33 +819,40 @@ void apply_kernel(ApplyArgs a) {
   }
   if constexpr (ROLE != kShrinkOnly) {
     if constexpr (RANK != 0) {
-      expand_body<T, RANK, ROLE>(a, b, part, blk, t0, s_h, s_tmp, &s_flag);
+      expand_body<T, RANK, ROLE, TILES>(a, b, part, blk, t0, s_h, s_tmp, smem.stage, &s_flag);
     } else {
       // Mixed ranks: the block's adapter decides (resolved again inside).
       const Resolved<T> r0 = resolve_b<T>(a, blk, 0);
       switch (r0.rank) {
-        case 16: expand_body<T, 16, ROLE>(a, b, part, blk, t0, s_h, s_tmp, &s_flag); break;
-        case 32: expand_body<T, 32, ROLE>(a, b, part, blk, t0, s_h, s_tmp, &s_flag); break;
-        case 64: expand_body<T, 64, ROLE>(a, b, part, blk, t0, s_h, s_tmp, &s_flag); break;
-        default: expand_body<T, 8, ROLE>(a, b, part, blk, t0, s_h, s_tmp, &s_flag); break;
+        case 16: expand_body<T, 16, ROLE, TILES>(a, b, part, blk, t0, s_h, s_tmp, smem.stage, &s_flag); break;
+        case 32: expand_body<T, 32, ROLE, TILES>(a, b, part, blk, t0, s_h, s_tmp, smem.stage, &s_flag); break;
+        case 64: expand_body<T, 64, ROLE, TILES>(a, b, part, blk, t0, s_h, s_tmp, smem.stage, &s_flag); break;
+        default: expand_body<T, 8, ROLE, TILES>(a, b, part, blk, t0, s_h, s_tmp, smem.stage, &s_flag); break;
       }
     }
   }
 }
 
-template <typename T, int ROLE>
+template <typename T, int ROLE, int TILES>
 hipError_t launch_rank(const ApplyArgs& a, hipStream_t stream) {
   const int64_t S = ROLE == kExpandOnly ? 0 : static_cast<int64_t>(a.n_slots) * a.n_chunks * a.n_rgroups;
-  const int64_t E = static_cast<int64_t>(a.n_slots) * (ROLE == kShrinkOnly ? 1 : (a.n_ochunks + a.n_sub - 1) / a.n_sub);
+  const int64_t E = static_cast<int64_t>(a.n_slots) *
+                    (ROLE == kShrinkOnly ? kBlockTokens / 16 : (a.n_ochunks + a.n_sub - 1) / a.n_sub);
   const int64_t n = S + E;
   if (n <= 0) return hipSuccess;
   const dim3 grid(static_cast<unsigned>(n));
   switch (a.rank) {
-    case 0: apply_kernel<T, 0, ROLE><<<grid, kThreads, 0, stream>>>(a); break;
-    case 8: apply_kernel<T, 8, ROLE><<<grid, kThreads, 0, stream>>>(a); break;
-    case 16: apply_kernel<T, 16, ROLE><<<grid, kThreads, 0, stream>>>(a); break;
-    case 32: apply_kernel<T, 32, ROLE><<<grid, kThreads, 0, stream>>>(a); break;
-    case 64: apply_kernel<T, 64, ROLE><<<grid, kThreads, 0, stream>>>(a); break;
+    case 0:  // mixed ranks: registered adapters only, which the fused calls do not take
+      if constexpr (ROLE == kShrinkOnly || ROLE == kExpandOnly) {
+        apply_kernel<T, 0, ROLE, TILES><<<grid, kThreads, 0, stream>>>(a);
+        break;
+      } else {
+        return hipErrorInvalidValue;
+      }
+    case 8: apply_kernel<T, 8, ROLE, TILES><<<grid, kThreads, 0, stream>>>(a); break;
+    case 16: apply_kernel<T, 16, ROLE, TILES><<<grid, kThreads, 0, stream>>>(a); break;
+    case 32: apply_kernel<T, 32, ROLE, TILES><<<grid, kThreads, 0, stream>>>(a); break;
+    case 64: apply_kernel<T, 64, ROLE, TILES><<<grid, kThreads, 0, stream>>>(a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -756,7 +860,12 @@ hipError_t launch_rank(const ApplyArgs& a, hipStream_t stream) {
 
 template <int ROLE>
 hipError_t launch_role(int dtype_bf16, const ApplyArgs& a, hipStream_t stream) {
-  return dtype_bf16 ? launch_rank<__bf16, ROLE>(a, stream) : launch_rank<_Float16, ROLE>(a, stream);
+  if constexpr (ROLE != kFused && ROLE != kFusedMulti) {
+    if (a.tiles > 1)
+      return dtype_bf16 ? launch_rank<__bf16, ROLE, kTilesInFlight>(a, stream)
+                        : launch_rank<_Float16, ROLE, kTilesInFlight>(a, stream);
+  }
+  return dtype_bf16 ? launch_rank<__bf16, ROLE, 1>(a, stream) : launch_rank<_Float16, ROLE, 1>(a, stream);
 }
 
 }  // namespace

@@ -103,7 +103,10 @@ constexpr int kExpandWorkgroups = 16;
 constexpr int kMaxChunks = kShrinkWorkgroups;
 inline void shrink_split(int d, int rank, int* dc, int* n_chunks, int* n_rgroups) {
   const int g = shrink_rank_groups(rank);
-  const int nc = static_cast<int>(std::min<int64_t>(std::max(1, kShrinkWorkgroups / g), ceil_div(d, 128)));
+  // At least 8 d-ranges: workgroup ids map to the 8 XCDs round-robin, so with
+  // a multiple of 8 d-ranges every rank group of one d-range runs on the
+  // same XCD and its X rows are fetched once into that XCD's L2.
+  const int nc = static_cast<int>(std::min<int64_t>(std::max(8, kShrinkWorkgroups / g), ceil_div(d, 128)));
   const int c = static_cast<int>(ceil_div(ceil_div(d, nc), 128) * 128);
   *dc = c;
   *n_chunks = static_cast<int>(ceil_div(d, c));
@@ -130,6 +133,7 @@ struct wp_engine {
   uint32_t* consumed = nullptr; // [block_cap]
   Entry* plan_entries = nullptr;
   float* part = nullptr;        // [kMaxChunks][tok_cap][kMaxRank] fp32 partial H
+  void* hbuf = nullptr;         // [tok_cap][kMaxRank] 2-byte H of large-plan add_lora calls
   int seg_cap = 0, block_cap = 0, tok_cap = 0, entry_cap = 0;
 
   // Id-indexed adapter table for table-mode kernels on device-built plans.
@@ -332,6 +336,7 @@ ApplyArgs base_args(const wp_engine* e, int rank) {
   ApplyArgs a{};
   a.rank = rank;
   a.n_sub = 1;
+  a.tiles = (e->plan_bt + 15) / 16;
   a.hs = rank == 0 ? kMaxRank : rank;
   a.ptok = e->tok_cap;
   a.part = e->part;
@@ -421,6 +426,7 @@ int wp_create(const wp_config* cfg_in, wp_engine** out) {
   const size_t o_cons = carve(sizeof(uint32_t) * e->block_cap * kCounterStride);
   const size_t o_ent = carve(sizeof(Entry) * e->entry_cap);
   const size_t o_part = carve(sizeof(float) * kMaxChunks * static_cast<size_t>(e->tok_cap) * kMaxRank);
+  const size_t o_hbuf = carve(sizeof(uint16_t) * static_cast<size_t>(e->tok_cap) * kMaxRank);
   if (hipMalloc(reinterpret_cast<void**>(&e->ws), off) != hipSuccess)
     return bail(fail(WP_ERR_HIP, "wp_create: workspace allocation (%zu bytes) failed", off));
   if (hipMemset(e->ws, 0, off) != hipSuccess) return bail(fail(WP_ERR_HIP, "wp_create: workspace clear failed"));
@@ -436,6 +442,7 @@ int wp_create(const wp_config* cfg_in, wp_engine** out) {
   e->consumed = reinterpret_cast<uint32_t*>(e->ws + o_cons);
   e->plan_entries = reinterpret_cast<Entry*>(e->ws + o_ent);
   e->part = reinterpret_cast<float*>(e->ws + o_part);
+  e->hbuf = e->ws + o_hbuf;
 
   e->pinned_bytes = sizeof(uint32_t) * kHdrWords + sizeof(Segment) * e->seg_cap + sizeof(Block) * e->block_cap +
                     sizeof(int32_t) * e->tok_cap + sizeof(int32_t) * static_cast<size_t>(e->block_cap) * kBlockTokens +
@@ -939,6 +946,17 @@ int wp_add_lora(wp_engine* e, void* y, const void* x, const void* wa, int64_t wa
   // block are summed fewer times.
   a.n_sub = static_cast<int>(ceil_div(oc, kExpandWorkgroups));
   a.n_slots = block_bound(e, num_loras);
+  if (e->plan_bt > 16) {
+    // Large plans (prefill-sized, 64-token blocks): shrink into the engine's
+    // H, then expand from it.  Each launch keeps several token tiles in
+    // flight per workgroup; the kernel boundary replaces the in-kernel wait.
+    a.h = e->hbuf;
+    a.ldh = a.hs;
+    a.n_sub = 1;
+    WP_HIP(launch_shrink(dtype == WP_DTYPE_BF16, a, stream));
+    WP_HIP(launch_expand(dtype == WP_DTYPE_BF16, a, stream));
+    return WP_OK;
+  }
   WP_HIP(launch_fused(dtype == WP_DTYPE_BF16, a, stream));
   return WP_OK;
 }
