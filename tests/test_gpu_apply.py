@@ -355,3 +355,51 @@ def test_plan_token_count_must_fit_call():
     wb = torch.zeros(1, 1, 256, 32, dtype=torch.float16, device="cuda")
     with pytest.raises(RuntimeError, match="segments reach token"):
         engine.add_lora_packed(y, x, wa, wb, 1.0)
+
+
+@pytest.mark.parametrize("T,rank", [(513, 16), (1000, 64), (2049, 32)])
+def test_add_lora_large_plans(T, rank):
+    """Plans over more than 512 tokens (64-token blocks, shrink + expand
+    launches with several token tiles in flight): random routings with ids < 0
+    and ragged blocks, three output slices with offsets."""
+    announce(f"large plan T={T} r={rank}")
+    dtype = torch.bfloat16
+    engine = WarpPipeEngine()
+    L, d = 9, 1024
+    rng = np.random.default_rng(T)
+    idx = np.repeat(rng.integers(-1, L, size=T // 3 + 1), 3)[:T]
+    rng.shuffle(idx[: T // 2])
+    wa = randn((L, 1, rank, d), 200, dtype, 0.02)
+    wbs = [randn((L, 1, o, rank), 201 + i, dtype, 0.02) for i, o in enumerate([1024, 512, 512])]
+    x = randn((T, d), 205, dtype)
+    y0 = randn((T, 2048), 206, dtype)
+    offs = [0, 1024, 1536]
+    assert engine.build_seg_bounds(torch.from_numpy(idx).cuda())
+    y = y0.cuda()
+    assert engine.add_lora_slices(y, x.cuda(), wa.cuda(), [w.cuda() for w in wbs], 16.0 / rank, offs)
+    torch.cuda.synchronize()
+    segs = so.seg_bounds(idx).tolist()
+    assert_close(y, bgmv.add_lora(y0, x, wa, wbs, 16.0 / rank, segs, offs), f"T={T} r={rank}")
+    assert engine.device_errors() == 0
+
+
+def test_registered_adapters_large_plan():
+    """shrink / expand through the adapter store on a 64-token-block plan."""
+    announce("store shrink/expand T=1500")
+    dtype = torch.float16
+    engine = WarpPipeEngine()
+    adapters = register(engine, 5, 64, 1536, 1024, dtype, 210, 0.25, ids=[4, 1, 9, 6, 2])
+    rng = np.random.default_rng(11)
+    idx = np.sort(rng.choice([4, 1, 9, 6, 2, -1], size=1500))
+    X = randn((1500, 1536), 211, dtype)
+    Y0 = randn((1500, 1024), 212, dtype)
+    assert engine.build_seg_bounds(torch.from_numpy(idx).cuda())
+    H = engine.shrink(X.cuda(), 1536, 64, 1500)
+    Y = Y0.cuda()
+    engine.expand(H, Y, 1024, 64)
+    torch.cuda.synchronize()
+    segs = so.seg_bounds(idx).tolist()
+    H_ref = bgmv.shrink(X, segs, adapters, 64, 1500)
+    assert_close(H, H_ref, "H")
+    assert_close(Y, bgmv.expand(H_ref, Y0, segs, adapters), "Y")
+    assert engine.device_errors() == 0
