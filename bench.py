@@ -564,11 +564,11 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
             "traffic": pmc_traffic(),
-            "kernel": "wp::apply_kernel<__bf16, 32, kFusedMulti> (packed-qkv call: shrink + expand, one launch)",
+            "kernel": "wp::apply_kernel<__bf16, 32, kFusedMulti, 1> (packed-qkv call: shrink + expand, one launch)",
             "bytes_per_launch": bytes_qkv,
             "us_per_launch": round(qkv_us, 3),
             "other_kernels": {
-                "wp::apply_kernel<__bf16, 32, kFused> (o_proj call)": {
+                "wp::apply_kernel<__bf16, 32, kFused, 1> (o_proj call)": {
                     "us_per_launch": round(o_us, 3), "bytes_per_launch": bytes_o,
                     "achieved": round(bytes_o / (o_us * 1e-6) / 1e9, 2)},
             },
