@@ -426,7 +426,8 @@ int wp_create(const wp_config* cfg_in, wp_engine** out) {
   const size_t o_cons = carve(sizeof(uint32_t) * e->block_cap * kCounterStride);
   const size_t o_ent = carve(sizeof(Entry) * e->entry_cap);
   const size_t o_part = carve(sizeof(float) * kMaxChunks * static_cast<size_t>(e->tok_cap) * kMaxRank);
-  const size_t o_hbuf = carve(sizeof(uint16_t) * static_cast<size_t>(e->tok_cap) * kMaxRank);
+  const size_t hbuf_bytes = sizeof(uint16_t) * static_cast<size_t>(e->tok_cap) * kMaxRank;
+  const size_t o_hbuf = carve(hbuf_bytes);
   if (hipMalloc(reinterpret_cast<void**>(&e->ws), off) != hipSuccess)
     return bail(fail(WP_ERR_HIP, "wp_create: workspace allocation (%zu bytes) failed", off));
   if (hipMemset(e->ws, 0, off) != hipSuccess) return bail(fail(WP_ERR_HIP, "wp_create: workspace clear failed"));
@@ -459,6 +460,13 @@ int wp_create(const wp_config* cfg_in, wp_engine** out) {
   // with the null stream (reference: bindings:32).
   if (hipStreamCreateWithFlags(&e->pstream, hipStreamNonBlocking) != hipSuccess)
     return bail(fail(WP_ERR_HIP, "wp_create: prefetch stream creation failed"));
+  // The first host-to-device copy on a new stream sets up its copy queue
+  // (~5 ms on MI355X, with the host blocked): pay it here, not in the first
+  // prefetch_adapter of a serving loop.  hbuf is scratch with no contents yet.
+  if (hipMemcpyAsync(e->hbuf, e->pinned, std::min(e->pinned_bytes, hbuf_bytes), hipMemcpyHostToDevice,
+                     e->pstream) != hipSuccess ||
+      hipStreamSynchronize(e->pstream) != hipSuccess)
+    return bail(fail(WP_ERR_HIP, "wp_create: prefetch stream warm-up copy failed"));
   e->slots.resize(cfg.num_staging_slots);
   for (auto& s : e->slots) {
     if (hipEventCreateWithFlags(&s.ready, hipEventDisableTiming) != hipSuccess ||

@@ -406,6 +406,11 @@ def run_cfg5(args):
         engine.register_adapter(1000 + k, wl.normal((r, h), .02, dt, 70 + k), wl.normal((h, r), .02, dt, 80 + k), 1.0,
                                 rank=r)
     reps = max(5, args.steps)
+    for _ in range(max(1, args.warmup)):
+        for k in range(4):
+            engine.release_prefetch(1000 + k)
+            engine.prefetch_adapter(1000 + k)
+        g.replay()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
