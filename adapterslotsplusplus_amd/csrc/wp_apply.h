@@ -19,7 +19,8 @@ struct ApplyArgs {
   int32_t rank;       // 8/16/32/64, or 0 for mixed ranks (per adapter)
   int32_t dc;         // shrink d-range per workgroup, multiple of 128
   int32_t n_chunks;   // ceil(d_model / dc): d-ranges, i.e. partials per H value
-  int32_t n_rgroups;  // rank groups of kShrinkRows rows; n_chunks * n_rgroups shrink workgroups per block
+  int32_t srows;      // rank rows per shrink workgroup: kShrinkRows, or kShrinkRowsFused (fused roles only)
+  int32_t n_rgroups;  // rank groups of srows rows; n_chunks * n_rgroups shrink workgroups per block
   int32_t n_ochunks;  // 256-column output chunks per block (all slices)
   int32_t n_sub;      // output chunks per expand workgroup (fused), else 1
   int32_t tiles;      // most 16-token tiles per block of the plan (1 or 4)

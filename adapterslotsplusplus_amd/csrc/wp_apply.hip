@@ -240,14 +240,15 @@ __device__ __forceinline__ int32_t block_token(const ApplyArgs& a, int b, int tl
 
 // ---------------------------------------------------------------- shrink ----
 
-// Partial H of block b over d-range c for rank rows [r_begin, r_begin + 16),
-// stored coherently to part[c].  The rows are the MFMA tile's M side (rows
-// past the adapter's rank load zeros and are not stored).  MAXT token tiles
-// are in flight at once: each batch of K-steps loads the A fragments once and
-// the X fragments of every tile, then runs the MFMAs.  The stores are the
-// publication: the partial buffer holds kPartialEmpty between calls, and the
-// readers poll for real values (no acknowledgement wait, no counter).
-template <typename T, int MAXT>
+// Partial H of block b over d-range c for rank rows [r_begin, r_begin +
+// 16 * MT), stored coherently to part[c].  The rows are the M side of MT
+// MFMA tiles that share every X fragment (rows past the adapter's rank load
+// zeros and are not stored; a tile with no rows is skipped).  MAXT token
+// tiles are in flight at once: each batch of K-steps loads the A fragments
+// once and the X fragments of every tile, then runs the MFMAs.  The stores
+// are the publication: the partial buffer holds kPartialEmpty between calls,
+// and the readers poll for real values (no acknowledgement wait, no counter).
+template <typename T, int MAXT, int MT>
 __device__ __forceinline__ void shrink_body(const ApplyArgs& a, int b, int c, int r_begin, const Block& blk,
                                             int32_t tok0, const Resolved<T>& res, f32x4* s_red) {
   using V8 = typename VecOf<T>::v8;
@@ -256,15 +257,19 @@ __device__ __forceinline__ void shrink_body(const ApplyArgs& a, int b, int c, in
   const int wave = threadIdx.x >> 6;
   const int row = lane & 15;
   const int kq = (lane >> 4) * 8;
-  const int n_rows = min(kShrinkRows, res.rank - r_begin);
+  const int n_rows = min(16 * MT, res.rank - r_begin);
   if (res.ptr == nullptr || n_rows <= 0) return;
+  const int mt_used = (n_rows + 15) >> 4;
   const int d = a.d_model;
   const int kw_len = a.dc / kWaves;
   const int k_begin = c * a.dc + wave * kw_len;
   const int k_end = min(k_begin + kw_len, d);
   const int ntt = (blk.count + 15) >> 4;
   const T* X = static_cast<const T*>(a.x);
-  const T* ar = row < n_rows ? res.ptr + static_cast<int64_t>(r_begin + row) * d : nullptr;
+  const T* ar[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+    ar[m] = m * 16 + row < n_rows ? res.ptr + static_cast<int64_t>(r_begin + m * 16 + row) * d : nullptr;
   float* prow = a.part + (static_cast<int64_t>(c) * a.ptok + blk.first) * a.hs + r_begin;
   for (int t0 = 0; t0 < ntt; t0 += MAXT) {
     const T* xr[MAXT];
@@ -274,24 +279,30 @@ __device__ __forceinline__ void shrink_body(const ApplyArgs& a, int b, int c, in
       const int32_t tok = tt == 0 ? tok0 : (tt < ntt ? block_token(a, b, tt * 16 + row, blk.count) : -1);
       xr[i] = tok >= 0 ? X + static_cast<int64_t>(tok) * a.ldx : nullptr;
     }
-    f32x4 acc[MAXT];
+    f32x4 acc[MAXT][MT];
 #pragma unroll
-    for (int i = 0; i < MAXT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < MAXT; ++i)
+#pragma unroll
+      for (int m = 0; m < MT; ++m) acc[i][m] = f32x4{0.f, 0.f, 0.f, 0.f};
     for (int k = k_begin; k < k_end; k += 32 * KB) {
-      V8 af[KB];
+      V8 af[KB][MT];
       V8 xf[KB][MAXT];
 #pragma unroll
       for (int st = 0; st < KB; ++st) {
         const int kk = k + st * 32 + kq;
         const bool in = kk < k_end;
-        af[st] = (ar != nullptr && in) ? load8(ar + kk) : zero8<T>();
+#pragma unroll
+        for (int m = 0; m < MT; ++m) af[st][m] = (ar[m] != nullptr && in) ? load8(ar[m] + kk) : zero8<T>();
 #pragma unroll
         for (int i = 0; i < MAXT; ++i) xf[st][i] = (xr[i] != nullptr && in) ? load8(xr[i] + kk) : zero8<T>();
       }
 #pragma unroll
       for (int st = 0; st < KB; ++st)
 #pragma unroll
-        for (int i = 0; i < MAXT; ++i) acc[i] = mfma16(af[st], xf[st][i], acc[i]);
+        for (int i = 0; i < MAXT; ++i)
+#pragma unroll
+          for (int m = 0; m < MT; ++m)
+            if (m < mt_used) acc[i][m] = mfma16(af[st][m], xf[st][i], acc[i][m]);
     }
     // Reduce the four waves' d-slices through LDS (fixed order) and store
     // each tile's partial, coherently.
@@ -299,15 +310,17 @@ __device__ __forceinline__ void shrink_body(const ApplyArgs& a, int b, int c, in
     for (int i = 0; i < MAXT; ++i) {
       const int tt = t0 + i;
       if (tt >= ntt) break;
-      s_red[wave * 64 + lane] = acc[i];
-      __syncthreads();
-      if (threadIdx.x < 64) {
-        const int tl = tt * 16 + (lane & 15);
-        const int r0 = (lane >> 4) * 4;
-        if (tl < blk.count && r0 < n_rows) {
-          f32x4 sum = s_red[lane];
 #pragma unroll
-          for (int w = 1; w < kWaves; ++w) sum += s_red[w * 64 + lane];
+      for (int m = 0; m < MT; ++m) s_red[(m * kWaves + wave) * 64 + lane] = acc[i][m];
+      __syncthreads();
+      if (static_cast<int>(threadIdx.x) < 64 * mt_used) {
+        const int m = threadIdx.x >> 6;
+        const int tl = tt * 16 + (lane & 15);
+        const int r0 = m * 16 + (lane >> 4) * 4;
+        if (tl < blk.count && r0 < n_rows) {
+          f32x4 sum = s_red[m * kWaves * 64 + lane];
+#pragma unroll
+          for (int w = 1; w < kWaves; ++w) sum += s_red[(m * kWaves + w) * 64 + lane];
           coherent_store_f4(prow + static_cast<int64_t>(tl) * a.hs + r0, sum);
         }
       }
@@ -327,13 +340,13 @@ __device__ __forceinline__ bool any_empty(f32x4 v) { return is_empty(v[0]) || is
 __device__ __forceinline__ bool wait_partials(const ApplyArgs& a, const Block& blk, int rank, int* s_flag) {
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
-    const int n_rg = (rank + kShrinkRows - 1) / kShrinkRows;
+    const int n_rg = (rank + a.srows - 1) / a.srows;
     const int n_probe = a.n_chunks * n_rg;
     const float* probe = nullptr;
     if (lane < n_probe) {
       const int rg = lane / a.n_chunks;
       const int kc = lane - rg * a.n_chunks;
-      probe = a.part + (static_cast<int64_t>(kc) * a.ptok + blk.first) * a.hs + rg * kShrinkRows;
+      probe = a.part + (static_cast<int64_t>(kc) * a.ptok + blk.first) * a.hs + rg * a.srows;
     }
     int ok = 1;
     for (unsigned spins = 0;; ++spins) {
@@ -662,7 +675,30 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
   const int wrote = kFusedRole ? resolve_a<T>(a, blk).rank : 0;
   V8 bf[kOT][KS];
   YRows yq;
-  load_chunk<T, RANK>(a, cur, tok0, bf, yq);
+  // Multi-chunk workgroups keep two chunks' B and Y in registers: chunk 1
+  // loads before the wait too, and chunk i + 2 while chunk i + 1 runs.
+  constexpr bool kTwoSets = ROLE == kFusedMulti && RANK <= 32;
+  OutChunk<T> cur2;
+  V8 bf2[kOT][KS];
+  YRows yq2;
+  if constexpr (kTwoSets) {
+    if (a.n_sub > 1 && p + n_owg < a.n_ochunks) {
+      cur2 = out_chunk<T>(a, blk, p + n_owg);
+      if (cur2.res.err != 0 && p == 0 && threadIdx.x == 0) flag_error(a.plan.header, cur2.res.err);
+    }
+  }
+  // A wave's loads complete in order, so the wave that polls for the
+  // partials (wave 0) loads its chunk columns only once they are there:
+  // otherwise a workgroup that starts late sees the partials only after its
+  // own chunk loads have landed.
+  const bool defer = ROLE == kFusedMulti && (threadIdx.x >> 6) == 0;
+  auto load_first = [&]() {
+    load_chunk<T, RANK>(a, cur, tok0, bf, yq);
+    if constexpr (kTwoSets) {
+      if (cur2.res.ptr != nullptr) load_chunk<T, RANK>(a, cur2, tok0, bf2, yq2);
+    }
+  };
+  if (!defer) load_first();
 
   bool go = cur.res.ptr != nullptr;
   unsigned consumed_prev = 0;
@@ -671,6 +707,7 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
     if (go) {
       go = wait_partials(a, blk, wrote, s_flag);
       if (go) {
+        if (defer) load_first();
         reduce_partials<RANK>(a, blk, cur.res.alpha, s_tmp, [&](int j, int r0, f32x4 v) {
           *reinterpret_cast<typename VecOf<T>::v4*>(s_h + j * HS + r0) = round4<T>(v);
         });
@@ -686,9 +723,28 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
     if (threadIdx.x == 0) consumed_prev = atomic_add_u(&a.consumed[b * kCounterStride], 1u);
   }
   if (go) {
-    if constexpr (ROLE == kFusedMulti) {
-      // Chunks after the first load when they are reached: the registers a
-      // second set would take are worth more as occupancy.
+    if constexpr (kTwoSets) {
+      for (int i = 0; i < a.n_sub; i += 2) {
+        if (p + i * n_owg >= a.n_ochunks) break;
+        if (cur.res.ptr != nullptr) compute_chunk<T, RANK, true, 1>(a, b, blk, tok0, cur, bf, yq, s_h, stage);
+        const int oc_a = p + (i + 2) * n_owg;
+        if (i + 2 < a.n_sub && oc_a < a.n_ochunks) {
+          cur = out_chunk<T>(a, blk, oc_a);
+          if (cur.res.err != 0 && p == 0 && threadIdx.x == 0) flag_error(a.plan.header, cur.res.err);
+          load_chunk<T, RANK>(a, cur, tok0, bf, yq);
+        }
+        if (i + 1 >= a.n_sub || p + (i + 1) * n_owg >= a.n_ochunks) break;
+        if (cur2.res.ptr != nullptr) compute_chunk<T, RANK, true, 1>(a, b, blk, tok0, cur2, bf2, yq2, s_h, stage);
+        const int oc_b = p + (i + 3) * n_owg;
+        if (i + 3 < a.n_sub && oc_b < a.n_ochunks) {
+          cur2 = out_chunk<T>(a, blk, oc_b);
+          if (cur2.res.err != 0 && p == 0 && threadIdx.x == 0) flag_error(a.plan.header, cur2.res.err);
+          load_chunk<T, RANK>(a, cur2, tok0, bf2, yq2);
+        }
+      }
+    } else if constexpr (ROLE == kFusedMulti) {
+      // Rank 64: chunks after the first load when they are reached (a second
+      // set of its B fragments would cost more occupancy than it saves).
       for (int i = 0; i < a.n_sub; ++i) {
         const int oc = p + i * n_owg;
         if (oc >= a.n_ochunks) break;
@@ -745,7 +801,7 @@ template <int RANK, int ROLE, int TILES>
 constexpr int waves_per_simd() {
   constexpr bool wide = RANK == 0 || RANK == 64;
   if (ROLE == kFused) return wide ? 5 : 7;
-  if (ROLE == kFusedMulti) return wide ? 5 : 6;
+  if (ROLE == kFusedMulti) return 4;
   if (TILES == 1) return wide ? 5 : 8;
   if (ROLE == kShrinkOnly) return 6;
   return wide ? 3 : 5;
@@ -756,7 +812,7 @@ constexpr int waves_per_simd() {
 template <typename T, int RANK>
 struct alignas(16) SharedMem {
   static constexpr int RR = RANK == 0 ? kMaxRank : RANK;
-  static constexpr int kRed = kWaves * 64;                             // f32x4
+  static constexpr int kRed = kShrinkRowsFused / 16 * kWaves * 64;    // f32x4
   static constexpr int kH = (kBlockTokens * (RR + 8) * 2 + 15) / 16;   // f32x4 worth of T
   static constexpr int kExp = kH + kThreads;
   f32x4 buf[kRed > kExp ? kRed : kExp];
@@ -801,8 +857,13 @@ void apply_kernel(ApplyArgs a) {
     if (shrink_role) {
       if (res.err != 0 && part == 0 && threadIdx.x == 0) flag_error(a.plan.header, res.err);
       const int rg = part / a.n_chunks;
-      shrink_body<T, ROLE == kShrinkOnly ? TILES : 1>(a, b, part - rg * a.n_chunks, rg * kShrinkRows, blk, t0, res,
-                                                     s_red);
+      if constexpr (ROLE == kFusedMulti) {
+        shrink_body<T, 1, kShrinkRowsFused / 16>(a, b, part - rg * a.n_chunks, rg * kShrinkRowsFused, blk, t0, res,
+                                                 s_red);
+      } else {
+        shrink_body<T, ROLE == kShrinkOnly ? TILES : 1, 1>(a, b, part - rg * a.n_chunks, rg * kShrinkRows, blk, t0,
+                                                           res, s_red);
+      }
     } else if constexpr (ROLE == kShrinkOnly) {
       if constexpr (RANK != 0) {
         finish_body<T, RANK>(a, b, part, blk, res, s_tmp, &s_flag);
@@ -873,9 +934,13 @@ hipError_t launch_role(int dtype_bf16, const ApplyArgs& a, hipStream_t stream) {
 int expand_cols_per_workgroup() { return kOC; }
 
 hipError_t launch_fused(int dtype_bf16, const ApplyArgs& a, hipStream_t stream) {
+  // The kernels' shrink split is fixed per role; the grid and the readers
+  // follow a.srows, so the two must agree.
+  if (a.srows != (a.n_sub > 1 ? kShrinkRowsFused : kShrinkRows)) return hipErrorInvalidValue;
   return a.n_sub > 1 ? launch_role<kFusedMulti>(dtype_bf16, a, stream) : launch_role<kFused>(dtype_bf16, a, stream);
 }
 hipError_t launch_shrink(int dtype_bf16, const ApplyArgs& a, hipStream_t stream) {
+  if (a.srows != kShrinkRows) return hipErrorInvalidValue;
   return launch_role<kShrinkOnly>(dtype_bf16, a, stream);
 }
 hipError_t launch_expand(int dtype_bf16, const ApplyArgs& a, hipStream_t stream) {

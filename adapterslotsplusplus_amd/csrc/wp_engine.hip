@@ -98,19 +98,20 @@ struct Slot {
 // Expand workgroups per block a fused call aims for.
 constexpr int kExpandWorkgroups = 16;
 
-// Shrink split of a call: rank groups, then at most kShrinkWorkgroups /
-// groups d-ranges, each a multiple of 128 (four waves x 32).
-constexpr int kMaxChunks = kShrinkWorkgroups;
-inline void shrink_split(int d, int rank, int* dc, int* n_chunks, int* n_rgroups) {
-  const int g = shrink_rank_groups(rank);
+// Shrink split of a call with `rows`-row rank groups: the groups, then
+// shrink_workgroups(rows) / groups d-ranges (at least 8), each a multiple of
+// 128 (four waves x 32).
+inline void shrink_split(int d, int rank, int rows, ApplyArgs* a) {
+  const int g = shrink_rank_groups(rank, rows);
   // At least 8 d-ranges: workgroup ids map to the 8 XCDs round-robin, so with
   // a multiple of 8 d-ranges every rank group of one d-range runs on the
   // same XCD and its X rows are fetched once into that XCD's L2.
-  const int nc = static_cast<int>(std::min<int64_t>(std::max(8, kShrinkWorkgroups / g), ceil_div(d, 128)));
+  const int nc = static_cast<int>(std::min<int64_t>(std::max(8, shrink_workgroups(rows) / g), ceil_div(d, 128)));
   const int c = static_cast<int>(ceil_div(ceil_div(d, nc), 128) * 128);
-  *dc = c;
-  *n_chunks = static_cast<int>(ceil_div(d, c));
-  *n_rgroups = g;
+  a->dc = c;
+  a->n_chunks = static_cast<int>(ceil_div(d, c));
+  a->srows = rows;
+  a->n_rgroups = g;
 }
 
 }  // namespace
@@ -833,7 +834,7 @@ int wp_shrink(wp_engine* e, const void* X, void* H, int32_t d_model, int32_t ran
   a.h = H;
   a.ldh = h_row_stride;
   a.d_model = d_model;
-  shrink_split(d_model, rank, &a.dc, &a.n_chunks, &a.n_rgroups);
+  shrink_split(d_model, rank, kShrinkRows, &a);
   uint32_t mask = 0;
   if ((rc = table_weights(e, stream, &a.w, &mask)) != WP_OK) return rc;
   a.w.n_slices = 1;
@@ -930,7 +931,6 @@ int wp_add_lora(wp_engine* e, void* y, const void* x, const void* wa, int64_t wa
   a.y = y;
   a.ldy = y_row_stride;
   a.d_model = d_model;
-  shrink_split(d_model, rank, &a.dc, &a.n_chunks, &a.n_rgroups);
   a.w.mode = kStacked;
   a.w.num_ids = num_loras;
   a.w.a_base = wa;
@@ -953,6 +953,10 @@ int wp_add_lora(wp_engine* e, void* y, const void* x, const void* wa, int64_t wa
   // slices) give each workgroup several chunks, so that the partials of the
   // block are summed fewer times.
   a.n_sub = static_cast<int>(ceil_div(oc, kExpandWorkgroups));
+  // Multi-chunk calls split the shrink in 32-row groups: half the shrink
+  // workgroups, so more of their expand workgroups are resident from the
+  // start.
+  shrink_split(d_model, rank, a.n_sub > 1 ? kShrinkRowsFused : kShrinkRows, &a);
   a.n_slots = block_bound(e, num_loras);
   if (e->plan_bt > 16) {
     // Large plans (prefill-sized, 64-token blocks): shrink into the engine's
@@ -961,6 +965,7 @@ int wp_add_lora(wp_engine* e, void* y, const void* x, const void* wa, int64_t wa
     a.h = e->hbuf;
     a.ldh = a.hs;
     a.n_sub = 1;
+    shrink_split(d_model, rank, kShrinkRows, &a);
     WP_HIP(launch_shrink(dtype == WP_DTYPE_BF16, a, stream));
     WP_HIP(launch_expand(dtype == WP_DTYPE_BF16, a, stream));
     return WP_OK;

@@ -50,15 +50,22 @@ constexpr int kPlanMaxTokens = 8192;
 constexpr int kMaxSlices = 4;
 // Largest rank.
 constexpr int kMaxRank = 64;
-// Shrink work split: each block's shrink runs on kShrinkWorkgroups
-// workgroups, each owning kShrinkRows rank rows (one MFMA tile) over one
-// d-range; the d-range count times the rank-group count is at most
-// kShrinkWorkgroups.  Mixed-rank calls use kMaxRank / kShrinkRows groups.
+// Shrink work split: each block's shrink runs on d-ranges x rank groups
+// workgroups, each owning `rows` rank rows over one d-range.  shrink() uses
+// 16-row groups (one MFMA tile: its four token tiles in flight take the
+// registers a second one would need); the fused kernel uses 32-row groups
+// (two tiles that share every X fragment), which halves its shrink
+// workgroups so that a decode call's whole grid is resident at once.
+// Mixed-rank calls use kMaxRank / rows groups.
 constexpr int kShrinkRows = 16;
-constexpr int kShrinkWorkgroups = 16;
-inline constexpr int shrink_rank_groups(int rank) {
-  return rank == 0 ? kMaxRank / kShrinkRows : (rank + kShrinkRows - 1) / kShrinkRows;
+constexpr int kShrinkRowsFused = 32;
+// Shrink workgroups per block a split aims for (at least 8 d-ranges).
+inline constexpr int shrink_workgroups(int rows) { return rows == kShrinkRowsFused ? 8 : 16; }
+inline constexpr int shrink_rank_groups(int rank, int rows) {
+  return rank == 0 ? kMaxRank / rows : (rank + rows - 1) / rows;
 }
+// Most d-ranges of a split (the partial buffer's depth).
+constexpr int kMaxChunks = 16;
 
 enum HeaderWord : int {
   kHdrNumSegments = 0,
