@@ -38,6 +38,10 @@ struct ApplyArgs {
 hipError_t launch_plan(const void* idx, int idx_is_int64, int T, uint32_t* header, Segment* segments, Block* blocks,
                        int32_t* perm, int32_t* bperm, int seg_cap, int block_cap, int bt, hipStream_t stream);
 
+// shrink(): d-range of one workgroup, in 128-column slices (a.dc must be
+// at most kShrinkSlices * 128).
+constexpr int kShrinkSlices = 8;
+
 // One launch: shrink + expand of a whole add_lora call (partials, counters).
 hipError_t launch_fused(int dtype_bf16, const ApplyArgs& a, hipStream_t stream);
 // shrink(): split-K shrink; one finishing workgroup per block writes H[token].

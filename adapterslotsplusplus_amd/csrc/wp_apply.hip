@@ -35,14 +35,16 @@
 // writeback + invalidate costs ~60-100 ns serialised over the device, nor
 // through accumulation atomics.
 //
-// Grid: the shrink workgroups of every block slot, then the expand (or, for
-// shrink(), one finishing) workgroups.  Those wait only on shrink workgroups,
+// Grid: the shrink workgroups of every block slot, then the expand
+// workgroups.  Those wait only on shrink workgroups,
 // which have lower ids and never wait, so with in-order dispatch every wait
 // ends; it is bounded anyway and reports kErrSpin if the bound is hit.  Slots
 // past the device block count exit at once.
 //
-// The shrink-only and expand-only variants serve shrink()/expand() of the
-// engine API: shrink's finishing workgroup writes the token-indexed H.
+// The expand-only variant serves expand() of the engine API and the expand
+// half of large-plan calls; shrink() has its own kernel (shrink_kernel),
+// which computes every rank row of a block per workgroup and streams the
+// d-range through LDS.
 #include <hip/hip_runtime.h>
 
 #include "wp_apply.h"
@@ -76,15 +78,16 @@ constexpr int kWaves = kThreads / 64;
 constexpr int kOT = 4;                  // output tiles per wave in expand
 constexpr int kOC = kWaves * kOT * 16;  // output columns per expand workgroup (256)
 constexpr int kShrinkKSteps = 4;        // 32-wide K-steps per wave per load batch
-// Token tiles a shrink()/expand() workgroup keeps in flight (blocks of 64
-// tokens in large plans); the fused kernel, which decode-sized plans use,
-// works one tile at a time to keep its registers for occupancy.
+// Token tiles an expand() workgroup keeps in flight (blocks of 64 tokens in
+// large plans); the fused kernel, which decode-sized plans use, works one
+// tile at a time to keep its registers for occupancy.
 constexpr int kTilesInFlight = kBlockTokens / 16;
 // Bound of the partials wait: polls of ~1 us each, so about 0.1 s.
 constexpr unsigned kSpinLimit = 1u << 17;
+constexpr int kShrinkWavesPerSimd = 4;
 
 // kFusedMulti: fused, with several output chunks per expand workgroup.
-enum Role : int { kFused = 0, kShrinkOnly = 1, kExpandOnly = 2, kFusedMulti = 3 };
+enum Role : int { kFused = 0, kExpandOnly = 2, kFusedMulti = 3 };
 
 __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -96,6 +99,12 @@ __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
 template <typename T>
 __device__ __forceinline__ typename VecOf<T>::v8 load8(const T* p) {
   return __builtin_bit_cast(typename VecOf<T>::v8, *reinterpret_cast<const u32x4*>(p));
+}
+// 16-byte load through the global (not the generic) address space: a
+// generic load counts on both the vector-memory and the LDS counters, so a
+// wait for LDS would also wait for it.
+__device__ __forceinline__ u32x4 load16_global(const void* p) {
+  return *reinterpret_cast<const __attribute__((address_space(1))) u32x4*>(reinterpret_cast<uintptr_t>(p));
 }
 template <typename T>
 __device__ __forceinline__ typename VecOf<T>::v8 zero8() {
@@ -156,6 +165,10 @@ __device__ __forceinline__ void atomic_store_u(uint32_t* p, unsigned v) {
 // Waits until this wave's outstanding global loads, stores and atomics are
 // acknowledged, which for sc1 stores means they are device-visible.
 __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Workgroup barrier for LDS data only: waits for this wave's LDS accesses
+// but not for its global loads in flight, which __syncthreads (a
+// workgroup-scope fence + s_barrier) would drain with s_waitcnt vmcnt(0).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 __device__ __forceinline__ void flag_error(uint32_t* header, uint32_t bits) { atomicOr(&header[kHdrErrors], bits); }
 
@@ -240,19 +253,19 @@ __device__ __forceinline__ int32_t block_token(const ApplyArgs& a, int b, int tl
 
 // ---------------------------------------------------------------- shrink ----
 
-// Partial H of block b over d-range c for rank rows [r_begin, r_begin +
-// 16 * MT), stored coherently to part[c].  The rows are the M side of MT
-// MFMA tiles that share every X fragment (rows past the adapter's rank load
-// zeros and are not stored; a tile with no rows is skipped).  MAXT token
-// tiles are in flight at once: each batch of K-steps loads the A fragments
-// once and the X fragments of every tile, then runs the MFMAs.  The stores
-// are the publication: the partial buffer holds kPartialEmpty between calls,
-// and the readers poll for real values (no acknowledgement wait, no counter).
-template <typename T, int MAXT, int MT>
+// Fused kernel, shrink side: partial H of block b over d-range c for rank
+// rows [r_begin, r_begin + 16 * MT), stored coherently to part[c].  The rows
+// are the M side of MT MFMA tiles that share every X fragment (rows past the
+// adapter's rank load zeros and are not stored; a tile with no rows is
+// skipped).  The four waves split the d-range; each loads kShrinkKSteps
+// K-steps of A and X fragments at once, then runs the MFMAs.  The stores are
+// the publication: the partial buffer holds kPartialEmpty between calls, and
+// the readers poll for real values (no acknowledgement wait, no counter).
+template <typename T, int MT>
 __device__ __forceinline__ void shrink_body(const ApplyArgs& a, int b, int c, int r_begin, const Block& blk,
                                             int32_t tok0, const Resolved<T>& res, f32x4* s_red) {
   using V8 = typename VecOf<T>::v8;
-  constexpr int KB = MAXT == 1 ? kShrinkKSteps : 2;
+  constexpr int KB = kShrinkKSteps;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int row = lane & 15;
@@ -271,61 +284,46 @@ __device__ __forceinline__ void shrink_body(const ApplyArgs& a, int b, int c, in
   for (int m = 0; m < MT; ++m)
     ar[m] = m * 16 + row < n_rows ? res.ptr + static_cast<int64_t>(r_begin + m * 16 + row) * d : nullptr;
   float* prow = a.part + (static_cast<int64_t>(c) * a.ptok + blk.first) * a.hs + r_begin;
-  for (int t0 = 0; t0 < ntt; t0 += MAXT) {
-    const T* xr[MAXT];
+  for (int tt = 0; tt < ntt; ++tt) {
+    const int32_t tok = tt == 0 ? tok0 : block_token(a, b, tt * 16 + row, blk.count);
+    const T* xr = tok >= 0 ? X + static_cast<int64_t>(tok) * a.ldx : nullptr;
+    f32x4 acc[MT];
 #pragma unroll
-    for (int i = 0; i < MAXT; ++i) {
-      const int tt = t0 + i;
-      const int32_t tok = tt == 0 ? tok0 : (tt < ntt ? block_token(a, b, tt * 16 + row, blk.count) : -1);
-      xr[i] = tok >= 0 ? X + static_cast<int64_t>(tok) * a.ldx : nullptr;
-    }
-    f32x4 acc[MAXT][MT];
-#pragma unroll
-    for (int i = 0; i < MAXT; ++i)
-#pragma unroll
-      for (int m = 0; m < MT; ++m) acc[i][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int m = 0; m < MT; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
     for (int k = k_begin; k < k_end; k += 32 * KB) {
       V8 af[KB][MT];
-      V8 xf[KB][MAXT];
+      V8 xf[KB];
 #pragma unroll
       for (int st = 0; st < KB; ++st) {
         const int kk = k + st * 32 + kq;
         const bool in = kk < k_end;
 #pragma unroll
         for (int m = 0; m < MT; ++m) af[st][m] = (ar[m] != nullptr && in) ? load8(ar[m] + kk) : zero8<T>();
-#pragma unroll
-        for (int i = 0; i < MAXT; ++i) xf[st][i] = (xr[i] != nullptr && in) ? load8(xr[i] + kk) : zero8<T>();
+        xf[st] = (xr != nullptr && in) ? load8(xr + kk) : zero8<T>();
       }
 #pragma unroll
       for (int st = 0; st < KB; ++st)
 #pragma unroll
-        for (int i = 0; i < MAXT; ++i)
-#pragma unroll
-          for (int m = 0; m < MT; ++m)
-            if (m < mt_used) acc[i][m] = mfma16(af[st][m], xf[st][i], acc[i][m]);
+        for (int m = 0; m < MT; ++m)
+          if (m < mt_used) acc[m] = mfma16(af[st][m], xf[st], acc[m]);
     }
     // Reduce the four waves' d-slices through LDS (fixed order) and store
-    // each tile's partial, coherently.
+    // the tile's partial, coherently.
 #pragma unroll
-    for (int i = 0; i < MAXT; ++i) {
-      const int tt = t0 + i;
-      if (tt >= ntt) break;
+    for (int m = 0; m < MT; ++m) s_red[(m * kWaves + wave) * 64 + lane] = acc[m];
+    __syncthreads();
+    if (static_cast<int>(threadIdx.x) < 64 * mt_used) {
+      const int m = threadIdx.x >> 6;
+      const int tl = tt * 16 + (lane & 15);
+      const int r0 = m * 16 + (lane >> 4) * 4;
+      if (tl < blk.count && r0 < n_rows) {
+        f32x4 sum = s_red[m * kWaves * 64 + lane];
 #pragma unroll
-      for (int m = 0; m < MT; ++m) s_red[(m * kWaves + wave) * 64 + lane] = acc[i][m];
-      __syncthreads();
-      if (static_cast<int>(threadIdx.x) < 64 * mt_used) {
-        const int m = threadIdx.x >> 6;
-        const int tl = tt * 16 + (lane & 15);
-        const int r0 = m * 16 + (lane >> 4) * 4;
-        if (tl < blk.count && r0 < n_rows) {
-          f32x4 sum = s_red[m * kWaves * 64 + lane];
-#pragma unroll
-          for (int w = 1; w < kWaves; ++w) sum += s_red[(m * kWaves + w) * 64 + lane];
-          coherent_store_f4(prow + static_cast<int64_t>(tl) * a.hs + r0, sum);
-        }
+        for (int w = 1; w < kWaves; ++w) sum += s_red[(m * kWaves + w) * 64 + lane];
+        coherent_store_f4(prow + static_cast<int64_t>(tl) * a.hs + r0, sum);
       }
-      __syncthreads();
     }
+    __syncthreads();
   }
 }
 
@@ -772,38 +770,18 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
   }
 }
 
-// shrink(): finishing workgroup f of block b reduces the partials of the
-// block's token tile f into H[token] and empties them again.
-template <typename T, int RANK>
-__device__ __forceinline__ void finish_body(const ApplyArgs& a, int b, int f, const Block& blk,
-                                            const Resolved<T>& res, f32x4* s_tmp, int* s_flag) {
-  if (res.ptr == nullptr || f * 16 >= blk.count) return;
-  Block tile = blk;
-  tile.first = blk.first + f * 16;
-  tile.count = min(16, blk.count - f * 16);
-  if (wait_partials(a, tile, res.rank, s_flag)) {
-    T* H = static_cast<T*>(a.h);
-    reduce_partials<RANK>(a, tile, res.alpha, s_tmp, [&](int j, int r0, f32x4 v) {
-      store4(H + static_cast<int64_t>(block_token(a, b, f * 16 + j, blk.count)) * a.ldh + r0, v);
-    });
-  }
-  __syncthreads();
-  clear_partials(a, tile, res.rank, threadIdx.x, kThreads);
-}
-
 // ---------------------------------------------------------------- kernels ----
 
 // Occupancy target (waves per SIMD), from the registers each variant needs
 // without spilling: the fused kernel holds B and Y across the partials'
-// reduction; shrink() and expand() keep four token tiles in flight; rank 64
-// and mixed ranks hold twice the B fragments.
+// reduction (two chunks of them in multi-chunk calls); expand() keeps four
+// token tiles in flight; rank 64 and mixed ranks hold twice the B fragments.
 template <int RANK, int ROLE, int TILES>
 constexpr int waves_per_simd() {
   constexpr bool wide = RANK == 0 || RANK == 64;
   if (ROLE == kFused) return wide ? 5 : 7;
   if (ROLE == kFusedMulti) return 4;
   if (TILES == 1) return wide ? 5 : 8;
-  if (ROLE == kShrinkOnly) return 6;
   return wide ? 3 : 5;
 }
 
@@ -819,8 +797,8 @@ struct alignas(16) SharedMem {
   T stage[kWaves * 16 * kStageStride];  // each wave's Y tile (expand)
 };
 
-// TILES: token tiles in flight per workgroup in shrink()/expand() (4 for
-// plans of 64-token blocks, else 1); the fused kernel always works with 1.
+// TILES: token tiles in flight per workgroup in expand() (4 for plans of
+// 64-token blocks, else 1); the fused kernel always works with 1.
 template <typename T, int RANK, int ROLE, int TILES>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(waves_per_simd<RANK, ROLE, TILES>())))
 void apply_kernel(ApplyArgs a) {
@@ -832,7 +810,7 @@ void apply_kernel(ApplyArgs a) {
   f32x4* s_tmp = smem.buf + SM::kH;
   const int per_shrink = a.n_chunks * a.n_rgroups;
   const int S = ROLE == kExpandOnly ? 0 : a.n_slots * per_shrink;
-  const int per_block = ROLE == kShrinkOnly ? kBlockTokens / 16 : (a.n_ochunks + a.n_sub - 1) / a.n_sub;
+  const int per_block = (a.n_ochunks + a.n_sub - 1) / a.n_sub;
   const int wg = static_cast<int>(blockIdx.x);
   const bool shrink_role = ROLE != kExpandOnly && wg < S;
   int b, part;
@@ -852,59 +830,255 @@ void apply_kernel(ApplyArgs a) {
   if (b >= n_blocks) return;
   const int32_t t0 = row < blk.count ? tok0 : -1;
 
-  if (shrink_role || ROLE == kShrinkOnly) {
+  if (shrink_role) {
     const Resolved<T> res = resolve_a<T>(a, blk);
-    if (shrink_role) {
-      if (res.err != 0 && part == 0 && threadIdx.x == 0) flag_error(a.plan.header, res.err);
-      const int rg = part / a.n_chunks;
-      if constexpr (ROLE == kFusedMulti) {
-        shrink_body<T, 1, kShrinkRowsFused / 16>(a, b, part - rg * a.n_chunks, rg * kShrinkRowsFused, blk, t0, res,
-                                                 s_red);
-      } else {
-        shrink_body<T, ROLE == kShrinkOnly ? TILES : 1, 1>(a, b, part - rg * a.n_chunks, rg * kShrinkRows, blk, t0,
-                                                           res, s_red);
-      }
-    } else if constexpr (ROLE == kShrinkOnly) {
-      if constexpr (RANK != 0) {
-        finish_body<T, RANK>(a, b, part, blk, res, s_tmp, &s_flag);
-      } else {
-        switch (res.rank) {
-          case 16: finish_body<T, 16>(a, b, part, blk, res, s_tmp, &s_flag); break;
-          case 32: finish_body<T, 32>(a, b, part, blk, res, s_tmp, &s_flag); break;
-          case 64: finish_body<T, 64>(a, b, part, blk, res, s_tmp, &s_flag); break;
-          default: finish_body<T, 8>(a, b, part, blk, res, s_tmp, &s_flag); break;
-        }
-      }
+    if (res.err != 0 && part == 0 && threadIdx.x == 0) flag_error(a.plan.header, res.err);
+    const int rg = part / a.n_chunks;
+    if constexpr (ROLE == kFusedMulti) {
+      shrink_body<T, kShrinkRowsFused / 16>(a, b, part - rg * a.n_chunks, rg * kShrinkRowsFused, blk, t0, res, s_red);
+    } else {
+      shrink_body<T, 1>(a, b, part - rg * a.n_chunks, rg * kShrinkRows, blk, t0, res, s_red);
     }
     return;
   }
-  if constexpr (ROLE != kShrinkOnly) {
-    if constexpr (RANK != 0) {
-      expand_body<T, RANK, ROLE, TILES>(a, b, part, blk, t0, s_h, s_tmp, smem.stage, &s_flag);
-    } else {
-      // Mixed ranks: the block's adapter decides (resolved again inside).
-      const Resolved<T> r0 = resolve_b<T>(a, blk, 0);
-      switch (r0.rank) {
-        case 16: expand_body<T, 16, ROLE, TILES>(a, b, part, blk, t0, s_h, s_tmp, smem.stage, &s_flag); break;
-        case 32: expand_body<T, 32, ROLE, TILES>(a, b, part, blk, t0, s_h, s_tmp, smem.stage, &s_flag); break;
-        case 64: expand_body<T, 64, ROLE, TILES>(a, b, part, blk, t0, s_h, s_tmp, smem.stage, &s_flag); break;
-        default: expand_body<T, 8, ROLE, TILES>(a, b, part, blk, t0, s_h, s_tmp, smem.stage, &s_flag); break;
-      }
+  if constexpr (RANK != 0) {
+    expand_body<T, RANK, ROLE, TILES>(a, b, part, blk, t0, s_h, s_tmp, smem.stage, &s_flag);
+  } else {
+    // Mixed ranks: the block's adapter decides (resolved again inside).
+    const Resolved<T> r0 = resolve_b<T>(a, blk, 0);
+    switch (r0.rank) {
+      case 16: expand_body<T, 16, ROLE, TILES>(a, b, part, blk, t0, s_h, s_tmp, smem.stage, &s_flag); break;
+      case 32: expand_body<T, 32, ROLE, TILES>(a, b, part, blk, t0, s_h, s_tmp, smem.stage, &s_flag); break;
+      case 64: expand_body<T, 64, ROLE, TILES>(a, b, part, blk, t0, s_h, s_tmp, smem.stage, &s_flag); break;
+      default: expand_body<T, 8, ROLE, TILES>(a, b, part, blk, t0, s_h, s_tmp, smem.stage, &s_flag); break;
     }
   }
+}
+
+// ------------------------------------------------------------- shrink() ----
+//
+// shrink(), and the shrink half of large-plan add_lora calls: one workgroup
+// per (block, d-range) computes every rank row of the block, so each X
+// element is read once per call.  The d-range is streamed in K-slices of
+// kSliceK elements, software pipelined one slice ahead: the slice of A
+// (rank rows x kSliceK) is loaded once per workgroup and shared by the four
+// waves through LDS (double buffered), and each wave, which owns one
+// 16-token tile, loads its X fragments straight into registers.  The
+// block's d-ranges are summed by its last workgroup to finish (a per-block
+// counter), in d-range order, so the bits do not depend on timing; nothing
+// waits on another workgroup.
+constexpr int kSliceK = 128;
+constexpr int kSliceStride = kSliceK + 8;  // LDS row stride of an A slice: 16-byte skew per row
+
+template <typename T, int MAXR, bool kMixed>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kShrinkWavesPerSimd)))
+void shrink_kernel(ApplyArgs a) {
+  using V8 = typename VecOf<T>::v8;
+  constexpr int MT = (MAXR + 15) / 16;  // 16-row MFMA tiles of the largest rank
+  constexpr int KS = kSliceK / 32;      // K-steps per slice
+  __shared__ T s_a[2][MT * 16 * kSliceStride];
+  __shared__ int s_last;
+  const int tid = static_cast<int>(threadIdx.x);
+  const int n_kc = a.n_chunks;
+  const int b = static_cast<int>(blockIdx.x) / n_kc;
+  const int c = static_cast<int>(blockIdx.x) - b * n_kc;
+  const int n_blocks = static_cast<int>(a.plan.header[kHdrNumBlocks]);
+  if (b >= n_blocks) return;
+  const Block blk = a.plan.blocks[b];
+  const Resolved<T> res = resolve_a<T>(a, blk);
+  if (res.ptr == nullptr) {
+    if (res.err != 0 && c == 0 && tid == 0) flag_error(a.plan.header, res.err);
+    return;
+  }
+  const int rank = kMixed ? res.rank : MAXR;
+  const int n_mt = kMixed ? (rank + 15) >> 4 : MT;
+  const int d = a.d_model;
+  // The d-range [c * dc, ...) in groups of kShrinkSlices slices; k0/k1 are
+  // the current group's bounds.
+  const int kc_end = min((c + 1) * a.dc, d);
+  int k0 = c * a.dc;
+  int k1 = min(k0 + kShrinkSlices * kSliceK, kc_end);
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int row = lane & 15;
+  const int kq = (lane >> 4) * 8;
+  const int tl = wave * 16 + row;  // this lane's token slot in the block
+  const int32_t tok = tl < blk.count ? a.plan.bperm[static_cast<int64_t>(b) * kBlockTokens + tl] : -1;
+  const bool wave_live = wave * 16 < blk.count;
+  // Every load below is unconditional, at an address clamped into the
+  // operand (a missing token reads X row 0, a rank row past the adapter's
+  // reads its last row, a column past the d-range its last 8 columns); what
+  // is not part of the product is zeroed where the data is used.  Straight
+  // loads let the compiler wait for exactly the slice it needs while the
+  // next one stays in flight.
+  const T* xr = static_cast<const T*>(a.x) + static_cast<int64_t>(tok >= 0 ? tok : 0) * a.ldx;
+  // A slice loads: thread t moves 8 elements of rows t/16 + 16p.
+  const int arow = tid >> 4;
+  const int acol = (tid & 15) * 8;
+  // Element offsets from the adapter's A (rank x d < 2^31 elements).
+  const int arow0 = min(arow, rank - 1) * d;
+  struct Slice {
+    u32x4 a[MT];
+    V8 x[KS];
+  };
+  auto load_slice = [&](Slice& sl, int ks0) {
+#pragma unroll
+    for (int p = 0; p < MT; ++p) {
+      const int off = (kMixed ? min(p * 16 + arow, rank - 1) * d : arow0 + p * 16 * d) + min(ks0 + acol, k1 - 8);
+      sl.a[p] = load16_global(res.ptr + off);
+    }
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      sl.x[s] = __builtin_bit_cast(V8, load16_global(xr + min(ks0 + s * 32 + kq, k1 - 8)));
+  };
+  f32x4 acc[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // Slice at ks0 from `sl` (landed) through LDS buffer `buf`; then `sl`
+  // takes the slice two ahead, next_k (past the range's last slice it
+  // re-reads one of its slices, which is never used).
+  auto run_slice = [&](Slice& sl, int buf, int ks0, bool live, bool more, int next_k) {
+#pragma unroll
+    for (int p = 0; p < MT; ++p) {
+      const bool ok = ks0 + acol < k1 && (!kMixed || p * 16 + arow < rank);
+      *reinterpret_cast<u32x4*>(&s_a[buf][(p * 16 + arow) * kSliceStride + acol]) = ok ? sl.a[p] : u32x4{0u, 0u, 0u, 0u};
+    }
+    // The slice is in LDS for every wave; the other buffer was last read
+    // before this barrier, so the next slice may be written into it.
+    lds_barrier();
+    if (wave_live && live) {
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const V8 xf = (tok >= 0 && ks0 + s * 32 + kq < k1) ? sl.x[s] : zero8<T>();
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+          if (!kMixed || m < n_mt) {
+            const V8 af = __builtin_bit_cast(
+                V8, *reinterpret_cast<const u32x4*>(&s_a[buf][(m * 16 + row) * kSliceStride + s * 32 + kq]));
+            acc[m] = mfma16(af, xf, acc[m]);
+          }
+        }
+      }
+    }
+    if (more) load_slice(sl, next_k);
+  };
+  // Fully unrolled over the workgroup's kShrinkSlices slices: every path
+  // issues the same loads, so each wait is for exactly one slice.  A short
+  // last d-range skips the MFMAs of its missing slices, not their loads.
+  // Blocks of one adapter read the same A slices; each block starts at a
+  // different slice of its range (rotation by block index) so that they do
+  // not all hit the same lines at once.
+  Slice s0, s1;
+  for (; k0 < kc_end; k0 += kShrinkSlices * kSliceK, k1 = min(k0 + kShrinkSlices * kSliceK, kc_end)) {
+    const int n_sl = (k1 - k0 + kSliceK - 1) / kSliceK;
+    const int rot = b % n_sl;
+    auto slice_k = [&](int i) { return k0 + (i + rot < n_sl ? i + rot : i + rot - n_sl) * kSliceK; };
+    load_slice(s0, slice_k(0));
+    load_slice(s1, slice_k(1 % n_sl));
+#pragma unroll
+    for (int i = 0; i < kShrinkSlices; i += 2) {
+      run_slice(s0, 0, slice_k(i % n_sl), i < n_sl, i + 2 < kShrinkSlices, slice_k((i + 2) % n_sl));
+      run_slice(s1, 1, slice_k((i + 1) % n_sl), i + 1 < n_sl, i + 3 < kShrinkSlices, slice_k((i + 3) % n_sl));
+    }
+  }
+  // acc[m]: ranks m*16 + 4*(lane/16) + [0, 4) of token slot tl.
+  const int rq = (lane >> 4) * 4;
+  T* H = static_cast<T*>(a.h);
+  if (n_kc == 1) {
+    if (tok >= 0) {
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+        if (m * 16 + rq < rank) store4(H + static_cast<int64_t>(tok) * a.ldh + m * 16 + rq, acc[m] * res.alpha);
+    }
+    return;
+  }
+  // Partial of this d-range, stored coherently; the stores have landed
+  // before the count (s_waitcnt), so the last workgroup sees them all.
+  if (tok >= 0) {
+    float* prow = a.part + (static_cast<int64_t>(c) * a.ptok + blk.first + tl) * a.hs;
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+      if (m * 16 + rq < rank) coherent_store_f4(prow + m * 16 + rq, acc[m]);
+  }
+  wait_vm();
+  __syncthreads();
+  uint32_t* counter = &a.consumed[static_cast<int64_t>(b) * kCounterStride];
+  if (tid == 0) s_last = atomic_add_u(counter, 1u) == static_cast<unsigned>(n_kc - 1) ? 1 : 0;
+  __syncthreads();
+  if (s_last == 0) return;
+  // Last workgroup of the block: H = rn(alpha * sum_c part[c]) in d-range
+  // order, then the partials' empty pattern and the counter are restored
+  // for the next call.
+  const int r4 = rank >> 2;
+  const int units = blk.count * r4;
+  const int64_t cs = static_cast<int64_t>(a.ptok) * a.hs;
+  const f32x4 empty = __builtin_bit_cast(f32x4, u32x4{kPartialEmpty, kPartialEmpty, kPartialEmpty, kPartialEmpty});
+  // A thread's units are tid + 256 i (at most kBlockTokens * kMaxRank / 4 /
+  // 256 = 4); their loads go out together, four d-ranges at a time.
+  constexpr int kUnits = kBlockTokens * kMaxRank / 4 / kThreads;
+  const float* p0[kUnits];
+  f32x4 sum[kUnits];
+#pragma unroll
+  for (int i = 0; i < kUnits; ++i) {
+    const int u = min(tid + i * kThreads, units - 1);
+    const int j = u / r4;
+    p0[i] = a.part + (static_cast<int64_t>(blk.first) + j) * a.hs + (u - j * r4) * 4;
+    sum[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  for (int c0 = 0; c0 < n_kc; c0 += 4) {
+    f32x4 v[4][kUnits];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int i = 0; i < kUnits; ++i) v[q][i] = coherent_load_f4(p0[i] + min(c0 + q, n_kc - 1) * cs);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int i = 0; i < kUnits; ++i)
+        if (c0 + q < n_kc) sum[i] += v[q][i];
+  }
+#pragma unroll
+  for (int i = 0; i < kUnits; ++i) {
+    const int u = tid + i * kThreads;
+    if (u < units) {
+      const int j = u / r4;
+      const int32_t tj = a.plan.bperm[static_cast<int64_t>(b) * kBlockTokens + j];
+      store4(H + static_cast<int64_t>(tj) * a.ldh + (u - j * r4) * 4, sum[i] * res.alpha);
+      for (int cc = 0; cc < n_kc; ++cc) coherent_store_f4(const_cast<float*>(p0[i]) + cc * cs, empty);
+    }
+  }
+  if (tid == 0) atomic_store_u(counter, 0u);
+}
+
+template <typename T>
+hipError_t launch_shrink_t(const ApplyArgs& a, hipStream_t stream) {
+  const int64_t n = static_cast<int64_t>(a.n_slots) * a.n_chunks;
+  if (n <= 0) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>(n));
+  switch (a.rank) {
+    case 8: shrink_kernel<T, 8, false><<<grid, kThreads, 0, stream>>>(a); break;
+    case 16: shrink_kernel<T, 16, false><<<grid, kThreads, 0, stream>>>(a); break;
+    case 32: shrink_kernel<T, 32, false><<<grid, kThreads, 0, stream>>>(a); break;
+    case 64: shrink_kernel<T, 64, false><<<grid, kThreads, 0, stream>>>(a); break;
+    case 0:  // mixed ranks: each block's adapter decides, up to kMaxRank
+      shrink_kernel<T, kMaxRank, true><<<grid, kThreads, 0, stream>>>(a);
+      break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 template <typename T, int ROLE, int TILES>
 hipError_t launch_rank(const ApplyArgs& a, hipStream_t stream) {
   const int64_t S = ROLE == kExpandOnly ? 0 : static_cast<int64_t>(a.n_slots) * a.n_chunks * a.n_rgroups;
   const int64_t E = static_cast<int64_t>(a.n_slots) *
-                    (ROLE == kShrinkOnly ? kBlockTokens / 16 : (a.n_ochunks + a.n_sub - 1) / a.n_sub);
+                    ((a.n_ochunks + a.n_sub - 1) / a.n_sub);
   const int64_t n = S + E;
   if (n <= 0) return hipSuccess;
   const dim3 grid(static_cast<unsigned>(n));
   switch (a.rank) {
     case 0:  // mixed ranks: registered adapters only, which the fused calls do not take
-      if constexpr (ROLE == kShrinkOnly || ROLE == kExpandOnly) {
+      if constexpr (ROLE == kExpandOnly) {
         apply_kernel<T, 0, ROLE, TILES><<<grid, kThreads, 0, stream>>>(a);
         break;
       } else {
@@ -940,8 +1114,8 @@ hipError_t launch_fused(int dtype_bf16, const ApplyArgs& a, hipStream_t stream) 
   return a.n_sub > 1 ? launch_role<kFusedMulti>(dtype_bf16, a, stream) : launch_role<kFused>(dtype_bf16, a, stream);
 }
 hipError_t launch_shrink(int dtype_bf16, const ApplyArgs& a, hipStream_t stream) {
-  if (a.srows != kShrinkRows) return hipErrorInvalidValue;
-  return launch_role<kShrinkOnly>(dtype_bf16, a, stream);
+  if (a.n_chunks < 1 || a.n_chunks > kMaxChunks) return hipErrorInvalidValue;
+  return dtype_bf16 ? launch_shrink_t<__bf16>(a, stream) : launch_shrink_t<_Float16>(a, stream);
 }
 hipError_t launch_expand(int dtype_bf16, const ApplyArgs& a, hipStream_t stream) {
   return launch_role<kExpandOnly>(dtype_bf16, a, stream);

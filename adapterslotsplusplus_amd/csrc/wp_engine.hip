@@ -114,6 +114,18 @@ inline void shrink_split(int d, int rank, int rows, ApplyArgs* a) {
   a->n_rgroups = g;
 }
 
+// d-ranges of a shrink() launch: one workgroup per block and d-range, every
+// rank row; a d-range is kShrinkSlices x 128 columns (a multiple of that
+// past kMaxChunks ranges).
+inline void shrink_range_split(int d, ApplyArgs* a) {
+  const int group = kShrinkSlices * 128;
+  const int64_t n = std::min<int64_t>(ceil_div(d, group), kMaxChunks);
+  a->dc = static_cast<int>(ceil_div(ceil_div(d, n), group) * group);
+  a->n_chunks = static_cast<int>(ceil_div(d, a->dc));
+  a->srows = 0;
+  a->n_rgroups = 1;
+}
+
 }  // namespace
 
 struct wp_engine {
@@ -834,11 +846,11 @@ int wp_shrink(wp_engine* e, const void* X, void* H, int32_t d_model, int32_t ran
   a.h = H;
   a.ldh = h_row_stride;
   a.d_model = d_model;
-  shrink_split(d_model, rank, kShrinkRows, &a);
   uint32_t mask = 0;
   if ((rc = table_weights(e, stream, &a.w, &mask)) != WP_OK) return rc;
   a.w.n_slices = 1;
   a.n_slots = block_bound(e, e->plan_T);
+  shrink_range_split(d_model, &a);
   WP_HIP(launch_shrink(dtype == WP_DTYPE_BF16, a, stream));
   if (e->plan_kind == 1) record_slot_uses(e, e->plan_entry_slot, stream);
   else record_mask_uses(e, mask, stream);
@@ -965,7 +977,7 @@ int wp_add_lora(wp_engine* e, void* y, const void* x, const void* wa, int64_t wa
     a.h = e->hbuf;
     a.ldh = a.hs;
     a.n_sub = 1;
-    shrink_split(d_model, rank, kShrinkRows, &a);
+    shrink_range_split(d_model, &a);
     WP_HIP(launch_shrink(dtype == WP_DTYPE_BF16, a, stream));
     WP_HIP(launch_expand(dtype == WP_DTYPE_BF16, a, stream));
     return WP_OK;
