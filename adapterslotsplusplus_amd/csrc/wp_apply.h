@@ -51,5 +51,8 @@ hipError_t launch_expand(int dtype_bf16, const ApplyArgs& a, hipStream_t stream)
 
 // Output columns one expand workgroup produces.
 int expand_cols_per_workgroup();
+// Waves per SIMD the fused kernel for `rank` (0: mixed) runs at, single- or
+// multi-chunk: with the CU count, how many of its workgroups are resident.
+int fused_waves_per_simd(int rank, int multi);
 
 }  // namespace wp

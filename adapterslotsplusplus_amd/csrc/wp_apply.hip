@@ -1106,6 +1106,11 @@ hipError_t launch_role(int dtype_bf16, const ApplyArgs& a, hipStream_t stream) {
 }  // namespace
 
 int expand_cols_per_workgroup() { return kOC; }
+int fused_waves_per_simd(int rank, int multi) {
+  const bool wide = rank == 0 || rank == 64;
+  if (multi) return wide ? waves_per_simd<64, kFusedMulti, 1>() : waves_per_simd<32, kFusedMulti, 1>();
+  return wide ? waves_per_simd<64, kFused, 1>() : waves_per_simd<32, kFused, 1>();
+}
 
 hipError_t launch_fused(int dtype_bf16, const ApplyArgs& a, hipStream_t stream) {
   // The kernels' shrink split is fixed per role; the grid and the readers

@@ -98,15 +98,27 @@ struct Slot {
 // Expand workgroups per block a fused call aims for.
 constexpr int kExpandWorkgroups = 16;
 
-// Shrink split of a call with `rows`-row rank groups: the groups, then
+// Shrink split of a fused call with `rows`-row rank groups: the groups, then
 // shrink_workgroups(rows) / groups d-ranges (at least 8), each a multiple of
-// 128 (four waves x 32).
-inline void shrink_split(int d, int rank, int rows, ApplyArgs* a) {
+// 128 (four waves x 32).  Workgroup ids map to the 8 XCDs round-robin, so
+// with a multiple of 8 d-ranges every rank group of one d-range runs on the
+// same XCD and its X rows are fetched once into that XCD's L2.  The count is
+// then halved (down to 4) while
+//   - a wave's share of a d-range is under one full batch of K-steps
+//     (4 x 32 columns: fewer columns leave loads of the batch unused), or
+//   - the grid (block bound x (shrink + expand workgroups)) exceeds the
+//     workgroups the device holds at the kernel's occupancy (`resident`,
+//     0 to skip this test): workgroups that start late issue their loads
+//     during the partials exchange.
+// Measured on MI355X: cfg2 o_proj 14.3 -> 14.1 us, cfg5 step 836 -> 797 us,
+// cfg1 9.2 -> 8.8 us.  Multi-slice calls skip the residency test: their grid
+// does not fit at either count, and the halved one only adds a load round
+// (qkv 20.6 -> 20.8 us).
+inline void shrink_split(int d, int rank, int rows, int64_t slots, int64_t expand_per_block, int64_t resident,
+                         ApplyArgs* a) {
   const int g = shrink_rank_groups(rank, rows);
-  // At least 8 d-ranges: workgroup ids map to the 8 XCDs round-robin, so with
-  // a multiple of 8 d-ranges every rank group of one d-range runs on the
-  // same XCD and its X rows are fetched once into that XCD's L2.
-  const int nc = static_cast<int>(std::min<int64_t>(std::max(8, shrink_workgroups(rows) / g), ceil_div(d, 128)));
+  int nc = static_cast<int>(std::min<int64_t>(std::max(8, shrink_workgroups(rows) / g), ceil_div(d, 128)));
+  while (nc > 4 && (d < nc * 512 || (resident > 0 && slots * (nc * g + expand_per_block) > resident))) nc /= 2;
   const int c = static_cast<int>(ceil_div(ceil_div(d, nc), 128) * 128);
   a->dc = c;
   a->n_chunks = static_cast<int>(ceil_div(d, c));
@@ -148,6 +160,7 @@ struct wp_engine {
   float* part = nullptr;        // [kMaxChunks][tok_cap][kMaxRank] fp32 partial H
   void* hbuf = nullptr;         // [tok_cap][kMaxRank] 2-byte H of large-plan add_lora calls
   int seg_cap = 0, block_cap = 0, tok_cap = 0, entry_cap = 0;
+  int n_cu = 256;  // compute units of the device
 
   // Id-indexed adapter table for table-mode kernels on device-built plans.
   Entry* dtable = nullptr;
@@ -406,6 +419,10 @@ int wp_create(const wp_config* cfg_in, wp_engine** out) {
 
   wp_engine* e = new wp_engine();
   e->device = cfg.device;
+  // Four SIMDs per CU and four waves per workgroup: a CU holds as many
+  // workgroups as a SIMD holds waves.
+  if (hipDeviceGetAttribute(&e->n_cu, hipDeviceAttributeMultiprocessorCount, cfg.device) != hipSuccess || e->n_cu <= 0)
+    e->n_cu = 256;
   e->cfg = cfg;
   auto bail = [&](int rc) {
     wp_destroy(e);
@@ -965,11 +982,13 @@ int wp_add_lora(wp_engine* e, void* y, const void* x, const void* wa, int64_t wa
   // slices) give each workgroup several chunks, so that the partials of the
   // block are summed fewer times.
   a.n_sub = static_cast<int>(ceil_div(oc, kExpandWorkgroups));
+  a.n_slots = block_bound(e, num_loras);
   // Multi-chunk calls split the shrink in 32-row groups: half the shrink
   // workgroups, so more of their expand workgroups are resident from the
   // start.
-  shrink_split(d_model, rank, a.n_sub > 1 ? kShrinkRowsFused : kShrinkRows, &a);
-  a.n_slots = block_bound(e, num_loras);
+  const int multi = a.n_sub > 1 ? 1 : 0;
+  shrink_split(d_model, rank, multi ? kShrinkRowsFused : kShrinkRows, a.n_slots, ceil_div(oc, a.n_sub),
+               multi ? 0 : static_cast<int64_t>(e->n_cu) * fused_waves_per_simd(rank, multi), &a);
   if (e->plan_bt > 16) {
     // Large plans (prefill-sized, 64-token blocks): shrink into the engine's
     // H, then expand from it.  Each launch keeps several token tiles in
