@@ -270,6 +270,49 @@ def test_seg_bounds_with_registered_adapters():
     assert engine.device_errors() == 0
 
 
+@pytest.mark.parametrize("d,rank", [(1032, 16), (1032, 64), (20480, 32), (20480, 0)])
+def test_shrink_unaligned_and_wide_d(d, rank):
+    """shrink()/expand() with d not a multiple of the 128-column slice (the
+    last slice is clamped and zeroed) and d past 16 d-ranges of 1024 columns
+    (each workgroup streams several 1024-column groups); rank 0 = mixed."""
+    announce(f"shrink d={d} rank={rank}")
+    dtype = torch.bfloat16
+    engine = WarpPipeEngine()
+    ranks = [rank] * 5 if rank else [8, 16, 32, 64, 32]
+    adapters = {}
+    for i, r in enumerate(ranks):
+        A = randn((r, d), 300 + i, dtype, 0.02)
+        B = randn((640, r), 310 + i, dtype, 0.02)
+        engine.register_adapter(i, A.cuda(), B.cuda(), 16.0 / r, rank=r)
+        adapters[i] = (A, B, 16.0 / r)
+    rng = np.random.default_rng(d + rank)
+    idx = rng.integers(-1, 5, size=150)
+    X = randn((150, d), 320, dtype)
+    Y0 = randn((150, 640), 321, dtype)
+    assert engine.build_seg_bounds(torch.from_numpy(idx).cuda())
+    H = engine.shrink(X.cuda(), d, rank, 150)
+    Y = Y0.cuda()
+    engine.expand(H, Y, 640, rank)
+    torch.cuda.synchronize()
+    segs = so.seg_bounds(idx).tolist()
+    H_ref = bgmv.shrink(X, segs, adapters, rank if rank else 64, 150)
+    assert_close(H, H_ref, "H")
+    assert_close(Y, bgmv.expand(H_ref, Y0, segs, adapters), "Y")
+    assert engine.device_errors() == 0
+
+
+@pytest.mark.parametrize("T", [40, 700])
+def test_add_lora_unaligned_d(T):
+    """add_lora with d = 1032 on a decode-sized (fused) and a large plan."""
+    announce(f"add_lora d=1032 T={T}")
+    engine = WarpPipeEngine()
+    rng = np.random.default_rng(T)
+    idx = rng.integers(-1, 6, size=T).tolist()
+    y, y_ref = add_lora_case(engine, idx, 32, torch.float16, 330, L=6, d=1032, o=1032)
+    assert_close(y, y_ref, f"T={T}")
+    assert engine.device_errors() == 0
+
+
 def test_mixed_rank_store():
     """Mixed ranks in one grouped call (configuration 3's shape, reduced)."""
     announce("mixed rank")
