@@ -1,0 +1,151 @@
+"""Draft-model integration: nn.Linear + per-token LoRA delta through the engine.
+
+The reference's speculative-decoding benchmarks wrap the draft model's
+projections in `BGMVLoRALinear` (benchmarks/e2e/serve_multitenant.py:56-87):
+the base linear plus a per-row delta from vLLM's bgmv_shrink/bgmv_expand,
+routed by a module-global `STATE["idx"]`, inside a CUDA-graph-captured
+fixed-shape step (benchmarks/e2e/batched_spec_loop.py:69-131).  This module
+is the engine-backed counterpart:
+
+  * `DraftLoRAContext` owns the routing tensor (one adapter id per TOKEN of
+    the flattened [B*S, in] activations, as batched_spec_loop.py:88-92 notes)
+    and the engine.  `begin_step()` builds the step's segment table once
+    (build_seg_bounds); every wrapped linear of the step then reuses it.
+    Both are capture-safe, so a whole draft step -- routing table included --
+    records into one graph, and a replay reads whatever ids were copied into
+    `ctx.idx` before it.
+  * `WarpPipeLoRALinear.forward` computes the base linear and adds
+    scale * (x . A_idx^T) . B_idx^T to it in place with one add_lora_packed
+    call (shrink + expand in one launch, fp32 accumulation, one rounding of
+    base + delta).  mode "none" returns the base only (the reference's
+    shared-draft mode).
+
+There is no fallback: a call the engine cannot take (a rank without kernels,
+more tokens than the engine was sized for) raises.
+"""
+from __future__ import annotations
+
+from typing import Dict, Iterable, Optional, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .engine import WarpPipeEngine
+
+
+class DraftLoRAContext:
+    """Routing and engine shared by every WarpPipeLoRALinear of one model.
+
+    tokens: the fixed number of flattened rows a step's linears see (B * S);
+    idx holds one adapter id per row (-1: no LoRA for that row)."""
+
+    def __init__(self, engine: WarpPipeEngine, tokens: int, scale: float = 2.0, device=None):
+        self.engine = engine
+        self.tokens = int(tokens)
+        self.scale = float(scale)
+        self.mode = "lora"
+        dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+        self.idx = torch.zeros(self.tokens, dtype=torch.int64, device=dev)
+
+    def set_routing(self, ids: torch.Tensor) -> None:
+        """Copies per-token adapter ids into the routing buffer (stream-ordered,
+        so it may sit between graph replays)."""
+        ids = ids.reshape(-1)
+        if ids.numel() != self.tokens:
+            raise RuntimeError(f"DraftLoRAContext: routing has {ids.numel()} ids, the step has {self.tokens} tokens")
+        self.idx.copy_(ids)
+
+    def begin_step(self) -> None:
+        """Builds the step's segment table from `idx` (once per step, before the
+        model's forward; inside a captured step it is one graph node)."""
+        if self.mode == "none":
+            return
+        if not self.engine.build_seg_bounds(self.idx):
+            raise RuntimeError(f"DraftLoRAContext: {self.tokens} tokens exceed the engine's max_tokens")
+
+
+class WarpPipeLoRALinear(nn.Module):
+    """Base nn.Linear + per-token draft-LoRA delta, K adapter slots.
+
+    A: [K, rank, in], B: [K, out, rank] (the layouts of serve_multitenant.py:
+    74-75), same dtype and device as the base weight."""
+
+    def __init__(self, base: nn.Linear, A: torch.Tensor, B: torch.Tensor, ctx: DraftLoRAContext):
+        super().__init__()
+        if A.dim() != 3 or B.dim() != 3 or A.size(0) != B.size(0) or A.size(1) != B.size(2):
+            raise RuntimeError("WarpPipeLoRALinear: A must be [K, rank, in] and B [K, out, rank]")
+        if A.size(2) != base.in_features or B.size(1) != base.out_features:
+            raise RuntimeError("WarpPipeLoRALinear: A/B do not match the base linear's shape")
+        self.in_features = base.in_features
+        self.out_features = base.out_features
+        self.weight = base.weight
+        self.bias = base.bias
+        self.rank = int(A.size(1))
+        self.ctx = ctx
+        # The engine's stacked layout: wa_t_all [K, 1, r, in], wb_t_all [K, 1, out, r].
+        self.register_buffer("wa_t_all", A.detach().unsqueeze(1).contiguous(), persistent=False)
+        self.register_buffer("wb_t_all", B.detach().unsqueeze(1).contiguous(), persistent=False)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        y = F.linear(x, self.weight, self.bias)
+        if self.ctx.mode == "none":
+            return y
+        x2d = x.reshape(-1, self.in_features)
+        if not x2d.is_contiguous():
+            x2d = x2d.contiguous()
+        y = y.contiguous()
+        if x2d.size(0) != self.ctx.tokens:
+            raise RuntimeError(
+                f"WarpPipeLoRALinear: {x2d.size(0)} rows, but the step's routing covers {self.ctx.tokens} tokens")
+        if not self.ctx.engine.add_lora_packed(y.view(-1, self.out_features), x2d, self.wa_t_all, self.wb_t_all,
+                                               self.ctx.scale):
+            raise RuntimeError(f"WarpPipeLoRALinear: rank {self.rank} has no kernels")
+        return y
+
+
+def wrap_linears(model: nn.Module, weights: Dict[str, Tuple[torch.Tensor, torch.Tensor]],
+                 ctx: DraftLoRAContext) -> Iterable[str]:
+    """Replaces every nn.Linear of `model` whose qualified name is a key of
+    `weights` ({name: (A [K, r, in], B [K, out, r])}) by a WarpPipeLoRALinear;
+    returns the names replaced (the counterpart of extract_draft_lora's
+    module selection, serve_multitenant.py:90-110)."""
+    done = []
+    for name, (A, B) in weights.items():
+        parent_name, _, child = name.rpartition(".")
+        parent = model.get_submodule(parent_name) if parent_name else model
+        base = getattr(parent, child)
+        if not isinstance(base, nn.Linear):
+            raise RuntimeError(f"wrap_linears: {name} is not an nn.Linear")
+        setattr(parent, child, WarpPipeLoRALinear(base, A, B, ctx))
+        done.append(name)
+    return done
+
+
+class CapturedStep:
+    """One fixed-shape step (routing table + model forward) recorded into a
+    HIP graph; replay() reads the inputs and routing copied in before it
+    (batched_spec_loop.py:69-131's Step, reduced to what the LoRA path needs)."""
+
+    def __init__(self, fn, ctx: DraftLoRAContext, warmup: int = 2):
+        self.fn = fn
+        self.ctx = ctx
+        self.out: Optional[torch.Tensor] = None
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(warmup):
+                ctx.begin_step()
+                fn()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            ctx.begin_step()
+            self.out = fn()
+
+    def replay(self, routing: Optional[torch.Tensor] = None) -> torch.Tensor:
+        if routing is not None:
+            self.ctx.set_routing(routing)
+        self.graph.replay()
+        return self.out

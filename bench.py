@@ -29,7 +29,9 @@ Prints one JSON line.  `--gpus N` with N > 1 exits: this build runs on one GPU.
 is the metric line): `flatness` (cfg2 with 1..128 resident adapters), `cfg1`
 (with its CPU baseline), `cfg3` (13B mixed-rank decode
 through registered adapters: shrink + expand), `cfg4` (prefill chunk, MFMA),
-`cfg5` (88-call draft step in one graph, plus pinned-host prefetch overlap).
+`cfg5` (88-call draft step in one graph, plus pinned-host prefetch overlap),
+`draft` (the cfg5 step as a model forward through WarpPipeLoRALinear, with
+and without the adapters).
 """
 import argparse
 import json
@@ -55,7 +57,7 @@ def parse():
     ap.add_argument("--layers", type=int, default=40)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample length")
-    ap.add_argument("--workload", default="cfg2", choices=["cfg2", "flatness", "cfg1", "cfg3", "cfg4", "cfg5"])
+    ap.add_argument("--workload", default="cfg2", choices=["cfg2", "flatness", "cfg1", "cfg3", "cfg4", "cfg5", "draft"])
     return ap.parse_args()
 
 
@@ -432,6 +434,66 @@ def run_cfg5(args):
                                      "bytes_per_prefetch": 2 * r * h * 2}})
 
 
+def run_draft(args):
+    """The cfg5 draft step as a model forward: 22 blocks of q/k/v/o linears
+    (h=2048, bf16, synthetic weights) on T=128 tokens (32 tenants x 4), every
+    projection wrapped by WarpPipeLoRALinear (r=32, one adapter per tenant);
+    routing table + forward in one graph.  The same model with LoRA off gives
+    the base-linear cost, so the difference is what the adapters add."""
+    import torch
+    import torch.nn as nn
+    import torch.nn.functional as F
+
+    from adapterslotsplusplus_amd import WarpPipeEngine
+    from adapterslotsplusplus_amd.lora_linear import DraftLoRAContext, wrap_linears
+
+    dev = torch.device("cuda", 0)
+    dt, T, L, h, r, n_layers = torch.bfloat16, 128, 32, 2048, 32, 22
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(17)
+
+    def rn(shape, std):
+        return (torch.randn(*shape, generator=gen, device=dev, dtype=torch.float32) * std).to(dt)
+
+    class Block(nn.Module):
+        def __init__(self):
+            super().__init__()
+            for n in ("q_proj", "k_proj", "v_proj", "o_proj"):
+                lin = nn.Linear(h, h, bias=False, device=dev, dtype=dt)
+                with torch.no_grad():
+                    lin.weight.copy_(rn((h, h), 0.02))
+                setattr(self, n, lin)
+
+        def forward(self, x):
+            a = self.q_proj(x) + self.k_proj(x) + self.v_proj(x)
+            return x + self.o_proj(F.silu(a))
+
+    model = nn.Sequential(*[Block() for _ in range(n_layers)]).eval()
+    engine = WarpPipeEngine()
+    ctx = DraftLoRAContext(engine, T, scale=2.0, device=dev)
+    weights = {f"{i}.{n}": (rn((L, r, h), .02), rn((L, h, r), .02))
+               for i in range(n_layers) for n in ("q_proj", "k_proj", "v_proj", "o_proj")}
+    wrap_linears(model, weights, ctx)
+    ctx.set_routing(torch.repeat_interleave(torch.arange(L, device=dev), 4))
+    x = rn((T, h), 1.0)
+    res = {}
+    with torch.inference_mode():
+        for mode in ("none", "lora"):
+            ctx.mode = mode
+
+            def step():
+                ctx.begin_step()
+                return model(x)
+
+            us, _ = graph_us(step, max(5, args.steps))
+            res[mode] = us
+    emit({"workload": "draft step: 22 x (q, k, v, o) bf16 linears h=2048 on T=128 (32 tenants x 4), "
+                      "WarpPipeLoRALinear r=32 on all 88, routing table + forward in one graph",
+          "us_per_step_base_only": round(res["none"], 1), "us_per_step_with_lora": round(res["lora"], 1),
+          "lora_us_per_step": round(res["lora"] - res["none"], 1),
+          "lora_us_per_call": round((res["lora"] - res["none"]) / 88, 2)})
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -443,7 +505,7 @@ def main():
     if args.workload != "cfg2":
         torch.cuda.set_device(0)
         {"flatness": run_flatness, "cfg1": run_cfg1, "cfg3": run_cfg3, "cfg4": run_cfg4,
-         "cfg5": run_cfg5}[args.workload](args)
+         "cfg5": run_cfg5, "draft": run_draft}[args.workload](args)
         return
 
     from adapterslotsplusplus_amd import WarpPipeEngine
