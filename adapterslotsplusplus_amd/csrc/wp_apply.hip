@@ -12,9 +12,10 @@
 // csrc/kernels/warp_pipe_r32.cu:280-423) runs both halves of a call in ONE
 // launch, which saves a ~1.7 us graph launch per call:
 //
-//   shrink workgroups   block b, d-range c, 16 rank rows.  The four waves
-//                       split the d-range and reduce through LDS; the
-//                       workgroup stores its fp32 partial H coherently.
+//   shrink workgroups   block b, d-range c, 16 rank rows (32 in calls with
+//                       several output slices).  The four waves split the
+//                       d-range and reduce through LDS; the workgroup
+//                       stores its fp32 partial H coherently.
 //   expand workgroups   block b, 256 output columns (of each slice).  They
 //                       load their B rows and current Y, wait until the
 //                       block's partials hold values (the buffer holds the
@@ -509,7 +510,24 @@ __device__ __forceinline__ OutChunk<T> out_chunk(const ApplyArgs& a, const Block
 struct YRows {
   u32x4 v[2];
 };
-constexpr int kStageStride = 72;  // elements per staged row: 64 + 8 against bank conflicts
+// Elements per staged row: 64 + 4, so the 8-byte MFMA-layout accesses of 16
+// rows fall in distinct banks (SQ_LDS_BANK_CONFLICT 0 on MI355X; 72 gave a
+// two-way conflict).  Rows are then 8-byte aligned only: the row-order side
+// moves its 16 bytes as two 8-byte halves.
+constexpr int kStageStride = 68;
+
+// A row-order 16-byte segment into / out of the stage, as two 8-byte halves.
+template <typename T>
+__device__ __forceinline__ void stage_put(T* p, u32x4 v) {
+  reinterpret_cast<u32x2*>(p)[0] = u32x2{v[0], v[1]};
+  reinterpret_cast<u32x2*>(p)[1] = u32x2{v[2], v[3]};
+}
+template <typename T>
+__device__ __forceinline__ u32x4 stage_get(const T* p) {
+  const u32x2 lo = reinterpret_cast<const u32x2*>(p)[0];
+  const u32x2 hi = reinterpret_cast<const u32x2*>(p)[1];
+  return u32x4{lo[0], lo[1], hi[0], hi[1]};
+}
 
 // Tokens of this lane's two rows, from `tok_row` (the token of row lane % 16).
 __device__ __forceinline__ void yrows_tokens(int32_t tok_row, int32_t (&tok)[2]) {
@@ -633,8 +651,8 @@ __device__ __forceinline__ void compute_chunk(const ApplyArgs& a, int b, const B
     for (int i = 0; i < MAXT; ++i) {
       if (t0 + i >= ntt) break;
       // Row order -> MFMA layout through the stage (one wave, in order).
-      *reinterpret_cast<u32x4*>(st_seg) = yt[i].v[0];
-      *reinterpret_cast<u32x4*>(st_seg + 8 * kStageStride) = yt[i].v[1];
+      stage_put(st_seg, yt[i].v[0]);
+      stage_put(st_seg + 8 * kStageStride, yt[i].v[1]);
       f32x4 acc[kOT];
 #pragma unroll
       for (int ot = 0; ot < kOT; ++ot) acc[ot] = unpack4f<T>(*reinterpret_cast<const u32x2*>(st_row + ot * 16 + oq));
@@ -647,8 +665,8 @@ __device__ __forceinline__ void compute_chunk(const ApplyArgs& a, int b, const B
       for (int ot = 0; ot < kOT; ++ot)
         *reinterpret_cast<u32x2*>(st_row + ot * 16 + oq) = __builtin_bit_cast(u32x2, round4<T>(acc[ot]));
       YRows out;
-      out.v[0] = *reinterpret_cast<const u32x4*>(st_seg);
-      out.v[1] = *reinterpret_cast<const u32x4*>(st_seg + 8 * kStageStride);
+      out.v[0] = stage_get(st_seg);
+      out.v[1] = stage_get(st_seg + 8 * kStageStride);
       yrows_store<T>(a, c.y_off, ob, c.o_size, tok[i], out);
     }
   }
