@@ -28,7 +28,8 @@ struct ApplyArgs {
   int32_t hs;         // elements per H row: rank, or 64 for mixed ranks
   int32_t ptok;       // rows per chunk of `part` (plan positions)
   float* part;        // fp32 partial H by plan position: [n_chunks][ptok][hs], kPartialEmpty between calls
-  uint32_t* consumed; // per block (stride kCounterStride): expand workgroups finished, zero between calls
+  uint32_t* consumed; // per block (stride kCounterStride): fused calls count expand workgroups done reading,
+                      // shrink() counts d-range workgroups done; zero between calls
   PlanView plan;
   Weights w;
 };
@@ -38,13 +39,14 @@ struct ApplyArgs {
 hipError_t launch_plan(const void* idx, int idx_is_int64, int T, uint32_t* header, Segment* segments, Block* blocks,
                        int32_t* perm, int32_t* bperm, int seg_cap, int block_cap, int bt, hipStream_t stream);
 
-// shrink(): d-range of one workgroup, in 128-column slices (a.dc must be
-// at most kShrinkSlices * 128).
+// shrink(): a workgroup streams its d-range (a.dc, a multiple of
+// kShrinkSlices * 128 columns) in groups of kShrinkSlices 128-column slices.
 constexpr int kShrinkSlices = 8;
 
 // One launch: shrink + expand of a whole add_lora call (partials, counters).
 hipError_t launch_fused(int dtype_bf16, const ApplyArgs& a, hipStream_t stream);
-// shrink(): split-K shrink; one finishing workgroup per block writes H[token].
+// shrink(): one workgroup per (block, d-range) computes every rank row; the
+// block's last workgroup to finish sums the d-ranges into H[token].
 hipError_t launch_shrink(int dtype_bf16, const ApplyArgs& a, hipStream_t stream);
 // expand(): expand from a caller-provided token-indexed H.
 hipError_t launch_expand(int dtype_bf16, const ApplyArgs& a, hipStream_t stream);
