@@ -1029,12 +1029,12 @@ void shrink_kernel(ApplyArgs a) {
   __syncthreads();
   if (s_last == 0) return;
   // Last workgroup of the block: H = rn(alpha * sum_c part[c]) in d-range
-  // order, then the partials' empty pattern and the counter are restored
-  // for the next call.
+  // order, then the counter is reset for the next call.  The partials are
+  // left as they are: every launch writes each word it later reads (the
+  // buffer is shrink()'s own, not the fused calls' with its empty pattern).
   const int r4 = rank >> 2;
   const int units = blk.count * r4;
   const int64_t cs = static_cast<int64_t>(a.ptok) * a.hs;
-  const f32x4 empty = __builtin_bit_cast(f32x4, u32x4{kPartialEmpty, kPartialEmpty, kPartialEmpty, kPartialEmpty});
   // A thread's units are tid + 256 i (at most kBlockTokens * kMaxRank / 4 /
   // 256 = 4); their loads go out together, four d-ranges at a time.
   constexpr int kUnits = kBlockTokens * kMaxRank / 4 / kThreads;
@@ -1066,7 +1066,6 @@ void shrink_kernel(ApplyArgs a) {
       const int j = u / r4;
       const int32_t tj = a.plan.bperm[static_cast<int64_t>(b) * kBlockTokens + j];
       store4(H + static_cast<int64_t>(tj) * a.ldh + (u - j * r4) * 4, sum[i] * res.alpha);
-      for (int cc = 0; cc < n_kc; ++cc) coherent_store_f4(const_cast<float*>(p0[i]) + cc * cs, empty);
     }
   }
   if (tid == 0) atomic_store_u(counter, 0u);

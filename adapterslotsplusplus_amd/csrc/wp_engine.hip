@@ -157,7 +157,8 @@ struct wp_engine {
   int32_t* bperm = nullptr;     // [block_cap][kBlockTokens]
   uint32_t* consumed = nullptr; // [block_cap]
   Entry* plan_entries = nullptr;
-  float* part = nullptr;        // [kMaxChunks][tok_cap][kMaxRank] fp32 partial H
+  float* part = nullptr;        // [kMaxChunks][tok_cap][kMaxRank] fp32 partial H of fused calls (kPartialEmpty between calls)
+  float* spart = nullptr;       // same shape, d-range partials of shrink() launches (no invariant between calls)
   void* hbuf = nullptr;         // [tok_cap][kMaxRank] 2-byte H of large-plan add_lora calls
   int seg_cap = 0, block_cap = 0, tok_cap = 0, entry_cap = 0;
   int n_cu = 256;  // compute units of the device
@@ -456,6 +457,7 @@ int wp_create(const wp_config* cfg_in, wp_engine** out) {
   const size_t o_cons = carve(sizeof(uint32_t) * e->block_cap * kCounterStride);
   const size_t o_ent = carve(sizeof(Entry) * e->entry_cap);
   const size_t o_part = carve(sizeof(float) * kMaxChunks * static_cast<size_t>(e->tok_cap) * kMaxRank);
+  const size_t o_spart = carve(sizeof(float) * kMaxChunks * static_cast<size_t>(e->tok_cap) * kMaxRank);
   const size_t hbuf_bytes = sizeof(uint16_t) * static_cast<size_t>(e->tok_cap) * kMaxRank;
   const size_t o_hbuf = carve(hbuf_bytes);
   if (hipMalloc(reinterpret_cast<void**>(&e->ws), off) != hipSuccess)
@@ -473,6 +475,7 @@ int wp_create(const wp_config* cfg_in, wp_engine** out) {
   e->consumed = reinterpret_cast<uint32_t*>(e->ws + o_cons);
   e->plan_entries = reinterpret_cast<Entry*>(e->ws + o_ent);
   e->part = reinterpret_cast<float*>(e->ws + o_part);
+  e->spart = reinterpret_cast<float*>(e->ws + o_spart);
   e->hbuf = e->ws + o_hbuf;
 
   e->pinned_bytes = sizeof(uint32_t) * kHdrWords + sizeof(Segment) * e->seg_cap + sizeof(Block) * e->block_cap +
@@ -868,6 +871,7 @@ int wp_shrink(wp_engine* e, const void* X, void* H, int32_t d_model, int32_t ran
   a.w.n_slices = 1;
   a.n_slots = block_bound(e, e->plan_T);
   shrink_range_split(d_model, &a);
+  a.part = e->spart;
   WP_HIP(launch_shrink(dtype == WP_DTYPE_BF16, a, stream));
   if (e->plan_kind == 1) record_slot_uses(e, e->plan_entry_slot, stream);
   else record_mask_uses(e, mask, stream);
@@ -997,6 +1001,7 @@ int wp_add_lora(wp_engine* e, void* y, const void* x, const void* wa, int64_t wa
     a.ldh = a.hs;
     a.n_sub = 1;
     shrink_range_split(d_model, &a);
+    a.part = e->spart;
     WP_HIP(launch_shrink(dtype == WP_DTYPE_BF16, a, stream));
     WP_HIP(launch_expand(dtype == WP_DTYPE_BF16, a, stream));
     return WP_OK;
