@@ -21,3 +21,9 @@ class WarpPipeConfig:
     max_tokens: int = 8192
     # HIP device ordinal; None = torch.cuda.current_device() at construction.
     device: Optional[int] = None
+    # Multi-layer adapter store (not in the reference, whose store holds one
+    # (A, B) per id): with a stride S > 0, register_adapter(..., layer=l)
+    # keeps adapter ids 0..S-1 of layer l apart from every other layer's, and
+    # shrink / expand(..., layer=l) on a build_seg_bounds table apply layer
+    # l's weights to each token's adapter id.  0: one layer, plain ids.
+    layer_stride: int = 0

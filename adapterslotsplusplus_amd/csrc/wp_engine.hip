@@ -162,6 +162,8 @@ struct wp_engine {
   void* hbuf = nullptr;         // [tok_cap][kMaxRank] 2-byte H of large-plan add_lora calls
   int seg_cap = 0, block_cap = 0, tok_cap = 0, entry_cap = 0;
   int n_cu = 256;  // compute units of the device
+  int32_t entry_offset = 0;  // table-mode calls on device-built plans read dtable + entry_offset
+  int32_t entry_count = 0;   // ... and at most this many entries (0: to the table's end)
 
   // Id-indexed adapter table for table-mode kernels on device-built plans.
   Entry* dtable = nullptr;
@@ -594,6 +596,14 @@ int wp_evict_adapter(wp_engine* e, int32_t adapter_id, void* stream) {
 
 int wp_has_adapter(wp_engine* e, int32_t adapter_id) { return (e && e->adapters.count(adapter_id)) ? 1 : 0; }
 
+int wp_set_entry_offset(wp_engine* e, int32_t offset, int32_t count) {
+  if (!e) return fail(WP_ERR_INVALID, "set_entry_offset: engine is NULL");
+  if (offset < 0 || count < 0) return fail(WP_ERR_INVALID, "set_entry_offset: negative offset %d / count %d", offset, count);
+  e->entry_offset = offset;
+  e->entry_count = count;
+  return WP_OK;
+}
+
 int wp_build_segments(wp_engine* e, const int32_t* ids, int32_t K, const int32_t* offsets, int32_t n_offsets,
                       void* stream_) {
   if (!e) return fail(WP_ERR_INVALID, "build_segments: engine is NULL");
@@ -821,14 +831,20 @@ int table_weights(wp_engine* e, hipStream_t stream, Weights* w, uint32_t* mask) 
   *mask = 0;
   w->mode = kTable;
   if (e->plan_kind == 1) {
+    if (e->entry_offset != 0)
+      return fail(WP_ERR_INVALID, "adapter layers other than 0 need a build_seg_bounds table (build_segments resolves "
+                                  "its adapters when it is called)");
     w->entries = e->plan_entries;
     w->num_ids = static_cast<int32_t>(e->plan_entry_ids.size());
     return WP_OK;
   }
   int rc = sync_table(e, stream, mask);
   if (rc != WP_OK) return rc;
-  w->entries = e->dtable;
-  w->num_ids = e->dtable_cap;
+  // A layer's adapters sit at ids offset by layer * stride: the plan's
+  // per-token ids index the table from that offset.
+  w->entries = e->dtable + std::min(e->entry_offset, e->dtable_cap);
+  w->num_ids = std::max(0, e->dtable_cap - e->entry_offset);
+  if (e->entry_count > 0) w->num_ids = std::min(w->num_ids, e->entry_count);
   return WP_OK;
 }
 

@@ -73,6 +73,33 @@ class WarpPipeEngine:
         cfg = _lib.WpConfig(int(dev), int(self.config.num_staging_slots), int(self.config.max_tokens), 64)
         _lib.check(self._lib.wp_create(ctypes.byref(cfg), ctypes.byref(self._handle)), "WarpPipeEngine")
         self._held = {}
+        self._layers = {}  # adapter id -> layers registered under it (multi-layer store)
+
+    # ----------------------------------------------------- adapter layers --
+    def _store_id(self, adapter_id, layer) -> int:
+        """The store's id for (adapter_id, layer): adapter_id itself for layer
+        None / 0 without a layer stride, else layer * stride + adapter_id."""
+        aid = int(adapter_id)
+        stride = int(self.config.layer_stride or 0)
+        if stride <= 0:
+            if layer not in (None, 0):
+                raise RuntimeError("adapter layers need WarpPipeConfig.layer_stride > 0")
+            return aid
+        lay = int(layer or 0)
+        if not 0 <= aid < stride or lay < 0:
+            raise RuntimeError(f"with layer_stride {stride}, adapter ids must be in [0, {stride}) and layers >= 0")
+        sid = lay * stride + aid
+        if sid >= 2 ** 31:
+            raise RuntimeError("layer * layer_stride + adapter_id exceeds the int32 id range")
+        return sid
+
+    def _select_layer(self, layer) -> None:
+        stride = int(self.config.layer_stride or 0)
+        if layer not in (None, 0) and stride <= 0:
+            raise RuntimeError("adapter layers need WarpPipeConfig.layer_stride > 0")
+        if layer is not None and int(layer) < 0:
+            raise RuntimeError("layer must be >= 0")
+        _lib.check(self._lib.wp_set_entry_offset(self._handle, int(layer or 0) * stride, stride), "layer")
 
     # ------------------------------------------------------------ lifetime --
     def close(self) -> None:
@@ -97,10 +124,13 @@ class WarpPipeEngine:
             raise RuntimeError(f"{what} is on {t.device}, the engine on {self.device}")
 
     # ------------------------------------------------------- adapter store --
-    def register_adapter(self, adapter_id, A, B, alpha_scale, rank=None):
+    def register_adapter(self, adapter_id, A, B, alpha_scale, rank=None, layer=None):
         """A [rank, d], B [o, rank], contiguous fp16/bf16 (reference engine.py:12-14,
         bindings:110-119).  CUDA tensors: the adapter is device-resident.  CPU
-        tensors: it goes to the pinned host store and is usable once prefetched."""
+        tensors: it goes to the pinned host store and is usable once prefetched.
+        layer (multi-layer store, config.layer_stride > 0): the layer these
+        weights belong to."""
+        sid = self._store_id(adapter_id, layer)
         rank = int(rank or self.config.rank)
         if A.is_cuda != B.is_cuda:
             raise RuntimeError("A/B must both be CUDA tensors or both CPU tensors")
@@ -118,16 +148,26 @@ class WarpPipeEngine:
             raise RuntimeError(
                 f"A must be [rank={rank}, d] and B [o, rank={rank}]; got {tuple(A.shape)} and {tuple(B.shape)}")
         host = 0 if A.is_cuda else 1
-        _lib.check(self._lib.wp_register_adapter(self._handle, int(adapter_id), _ptr(A), _ptr(B), rank, d_model,
+        _lib.check(self._lib.wp_register_adapter(self._handle, sid, _ptr(A), _ptr(B), rank, d_model,
                                                  out_features, float(alpha_scale), dt, host, self._stream()),
                    "register_adapter")
         # Keeps the source alive until the stream-ordered copy has run (the
         # reference holds the tensors until eviction as well, bindings:118).
-        self._held[int(adapter_id)] = (A, B) if host == 0 else None
+        self._held[sid] = (A, B) if host == 0 else None
+        self._layers.setdefault(int(adapter_id), set()).add(int(layer or 0))
 
-    def evict_adapter(self, adapter_id):
-        _lib.check(self._lib.wp_evict_adapter(self._handle, int(adapter_id), self._stream()), "evict_adapter")
-        self._held.pop(int(adapter_id), None)
+    def evict_adapter(self, adapter_id, layer=None):
+        """Silent for an unknown id.  With a layer stride and layer=None, every
+        layer registered under the id is evicted."""
+        if int(self.config.layer_stride or 0) > 0 and layer is None:
+            layers = sorted(self._layers.pop(int(adapter_id), {0}))
+        else:
+            layers = [layer]
+            self._layers.get(int(adapter_id), set()).discard(int(layer or 0))
+        for lay in layers:
+            sid = self._store_id(adapter_id, lay)
+            _lib.check(self._lib.wp_evict_adapter(self._handle, sid, self._stream()), "evict_adapter")
+            self._held.pop(sid, None)
 
     # ------------------------------------------------------ segment tables --
     def build_segments(self, sorted_adapter_ids, seg_offsets):
@@ -188,12 +228,13 @@ class WarpPipeEngine:
         return int(v.value)
 
     # --------------------------------------------------------------- apply --
-    def shrink(self, X, d_model, rank, total_tokens, out=None):
+    def shrink(self, X, d_model, rank, total_tokens, out=None, layer=None):
         """H = rn(alpha * X . A^T) per segment; returns a new zero-initialised
         [total_tokens, rank] tensor (reference bindings:132-139).  rank=0 or
         None: mixed ranks, H is [T, 64] with each row's first r_a columns set.
         `out` (not in the reference): a caller-owned [T, width] H to write
-        instead; rows outside every segment keep their contents."""
+        instead; rows outside every segment keep their contents.  `layer`:
+        the adapters' layer in a multi-layer store (build_seg_bounds tables)."""
         rank = int(rank or 0)
         self._on_device(X, "X")
         dt = _dtype_code(X, "X")
@@ -210,13 +251,14 @@ class WarpPipeEngine:
             self._on_device(H, "out")
             if H.dtype != X.dtype or not H.is_contiguous() or tuple(H.shape) != (T, width):
                 raise RuntimeError(f"out must be a contiguous [{T}, {width}] tensor of X's dtype")
+        self._select_layer(layer)
         _lib.check(self._lib.wp_shrink(self._handle, _ptr(X), _ptr(H), int(d_model), rank, T, width, dt,
                                        self._stream()), "shrink")
         return H
 
-    def expand(self, H, Y, out_features, rank, y_offset: int = 0):
+    def expand(self, H, Y, out_features, rank, y_offset: int = 0, layer=None):
         """Y[:, y_offset:y_offset+o] += H . B^T per segment, in place
-        (reference bindings:141-148)."""
+        (reference bindings:141-148); `layer` as for shrink()."""
         rank = int(rank or 0)
         self._on_device(H, "H")
         self._on_device(Y, "Y")
@@ -226,6 +268,7 @@ class WarpPipeEngine:
         if not (H.is_contiguous() and Y.is_contiguous()):
             raise RuntimeError("H/Y must be contiguous")
         T = int(Y.size(0))
+        self._select_layer(layer)
         _lib.check(self._lib.wp_expand(self._handle, _ptr(H), _ptr(Y), int(out_features), rank, T, int(H.size(-1)),
                                        int(Y.size(-1)), int(y_offset), dt, self._stream()), "expand")
 
@@ -286,18 +329,19 @@ class WarpPipeEngine:
         return rc == _lib.WP_OK
 
     # ------------------------------------------------------------- staging --
-    def prefetch_adapter(self, adapter_id) -> int:
+    def prefetch_adapter(self, adapter_id, layer=None) -> int:
         """Stages the adapter's A/B in a slot on the prefetch stream; returns the
         slot index or -1 (unknown id / pool exhausted) (reference bindings:46-57)."""
         slot = ctypes.c_int32(-1)
-        _lib.check(self._lib.wp_prefetch_adapter(self._handle, int(adapter_id), ctypes.byref(slot)),
+        _lib.check(self._lib.wp_prefetch_adapter(self._handle, self._store_id(adapter_id, layer), ctypes.byref(slot)),
                    "prefetch_adapter")
         return int(slot.value)
 
-    def is_prefetch_ready(self, adapter_id) -> bool:
+    def is_prefetch_ready(self, adapter_id, layer=None) -> bool:
         r = ctypes.c_int32(0)
-        _lib.check(self._lib.wp_is_prefetch_ready(self._handle, int(adapter_id), ctypes.byref(r)), "is_prefetch_ready")
+        _lib.check(self._lib.wp_is_prefetch_ready(self._handle, self._store_id(adapter_id, layer), ctypes.byref(r)),
+                   "is_prefetch_ready")
         return bool(r.value)
 
-    def release_prefetch(self, adapter_id):
-        _lib.check(self._lib.wp_release_prefetch(self._handle, int(adapter_id)), "release_prefetch")
+    def release_prefetch(self, adapter_id, layer=None):
+        _lib.check(self._lib.wp_release_prefetch(self._handle, self._store_id(adapter_id, layer)), "release_prefetch")

@@ -102,6 +102,17 @@ int wp_evict_adapter(wp_engine* e, int32_t adapter_id, void* stream);
 /* 1 if the id is registered, 0 otherwise. */
 int wp_has_adapter(wp_engine* e, int32_t adapter_id);
 
+/* Multi-layer adapter store (no counterpart in the reference, whose store
+ * holds one (A, B) per id, csrc/bridge/adapter_store.h:12-19): a layer's
+ * adapters are registered under ids offset by layer * stride.  After this
+ * call, the per-token ids of a build_seg_bounds plan select the adapters
+ * registered under offset + id in the shrink / expand calls that
+ * follow on adapter-store weights; with count > 0, ids >= count are skipped
+ * and flagged like unregistered ones (they would reach the next layer).
+ * (0, 0) restores the plain ids.  Calls on a build_segments table require
+ * offset 0. */
+int wp_set_entry_offset(wp_engine* e, int32_t offset, int32_t count);
+
 /* ---- segment tables ----------------------------------------------------- */
 
 /* Replaces WarpPipeExtension::build_segments (bindings:128-130) /
