@@ -32,6 +32,12 @@ COMMON = [
 ]
 
 
+# apply_kernel's first six arguments (plan pointers and grid split) are
+# preloaded into SGPRs at wave launch (gfx950 kernarg preloading); kernels
+# whose first argument is a struct preload nothing.
+EXTRA = {"wp_apply.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=6"]}
+
+
 def _run(cmd):
     r = subprocess.run(cmd, capture_output=True, text=True)
     out = "\n".join(line for line in (r.stdout + r.stderr).splitlines()
@@ -45,7 +51,7 @@ def build(verbose: bool = False) -> str:
     """Compiles every source (always) and links the shared library."""
     os.makedirs(OBJ_DIR, exist_ok=True)
     objs = [os.path.join(OBJ_DIR, s.rsplit(".", 1)[0] + ".o") for s in SOURCES]
-    cmds = [[HIPCC, *COMMON, "-c", os.path.join(CSRC, s), "-o", o] for s, o in zip(SOURCES, objs)]
+    cmds = [[HIPCC, *COMMON, *EXTRA.get(s, []), "-c", os.path.join(CSRC, s), "-o", o] for s, o in zip(SOURCES, objs)]
     with ThreadPoolExecutor(max_workers=len(cmds)) as ex:
         outs = list(ex.map(_run, cmds))
     tmp = LIB_PATH + ".tmp"

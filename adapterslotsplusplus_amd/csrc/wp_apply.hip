@@ -821,18 +821,24 @@ struct alignas(16) SharedMem {
 
 // TILES: token tiles in flight per workgroup in expand() (4 for plans of
 // 64-token blocks, else 1); the fused kernel always works with 1.
+//
+// The leading scalar arguments repeat what a workgroup needs before its
+// first memory access (the plan's header, blocks and token lists, and the
+// grid's split into roles).  The library is built with kernarg preloading
+// (-amdgpu-kernarg-preload-count), so these arrive in SGPRs at wave launch
+// and the plan loads go out without a kernel-argument load ahead of them.
 template <typename T, int RANK, int ROLE, int TILES>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(waves_per_simd<RANK, ROLE, TILES>())))
-void apply_kernel(ApplyArgs a) {
+void apply_kernel(const uint32_t* header, const Block* __restrict__ blocks,
+                  const int32_t* __restrict__ bperm, int32_t per_shrink, int32_t n_shrink, int32_t per_block,
+                  ApplyArgs a) {
   using SM = SharedMem<T, RANK>;
   __shared__ SM smem;
   __shared__ int s_flag;
   f32x4* s_red = smem.buf;
   T* s_h = reinterpret_cast<T*>(smem.buf);
   f32x4* s_tmp = smem.buf + SM::kH;
-  const int per_shrink = a.n_chunks * a.n_rgroups;
-  const int S = ROLE == kExpandOnly ? 0 : a.n_slots * per_shrink;
-  const int per_block = (a.n_ochunks + a.n_sub - 1) / a.n_sub;
+  const int S = ROLE == kExpandOnly ? 0 : n_shrink;
   const int wg = static_cast<int>(blockIdx.x);
   const bool shrink_role = ROLE != kExpandOnly && wg < S;
   int b, part;
@@ -844,12 +850,16 @@ void apply_kernel(ApplyArgs a) {
     b = e / per_block;
     part = e - b * per_block;
   }
-  // Independent loads: block count, block descriptor, this lane's first token.
-  const int n_blocks = static_cast<int>(a.plan.header[kHdrNumBlocks]);
-  const Block blk = a.plan.blocks[b];
+  // Independent loads: block count, block descriptor, this lane's first token
+  // (blocks and bperm hold every slot of the grid).  The exit test reads all
+  // three so that they are issued together, one memory latency in all:
+  // tested on the count alone, the compiler would load the descriptor and the
+  // token only after the count had arrived.
+  const int n_blocks = static_cast<int>(header[kHdrNumBlocks]);
+  const Block blk = blocks[b];
   const int row = threadIdx.x & 15;
-  const int32_t tok0 = a.plan.bperm[static_cast<int64_t>(b) * kBlockTokens + row];
-  if (b >= n_blocks) return;
+  const int32_t tok0 = bperm[static_cast<int64_t>(b) * kBlockTokens + row];
+  if ((b >= n_blocks) | (blk.count <= 0) | (tok0 < -1)) return;
   const int32_t t0 = row < blk.count ? tok0 : -1;
 
   if (shrink_role) {
@@ -1097,20 +1107,24 @@ hipError_t launch_rank(const ApplyArgs& a, hipStream_t stream) {
   const int64_t n = S + E;
   if (n <= 0) return hipSuccess;
   const dim3 grid(static_cast<unsigned>(n));
+  const int32_t per_shrink = a.n_chunks * a.n_rgroups;
+  const int32_t per_block = (a.n_ochunks + a.n_sub - 1) / a.n_sub;
+#define WP_APPLY_ARGS a.plan.header, a.plan.blocks, a.plan.bperm, per_shrink, static_cast<int32_t>(S), per_block, a
   switch (a.rank) {
     case 0:  // mixed ranks: registered adapters only, which the fused calls do not take
       if constexpr (ROLE == kExpandOnly) {
-        apply_kernel<T, 0, ROLE, TILES><<<grid, kThreads, 0, stream>>>(a);
+        apply_kernel<T, 0, ROLE, TILES><<<grid, kThreads, 0, stream>>>(WP_APPLY_ARGS);
         break;
       } else {
         return hipErrorInvalidValue;
       }
-    case 8: apply_kernel<T, 8, ROLE, TILES><<<grid, kThreads, 0, stream>>>(a); break;
-    case 16: apply_kernel<T, 16, ROLE, TILES><<<grid, kThreads, 0, stream>>>(a); break;
-    case 32: apply_kernel<T, 32, ROLE, TILES><<<grid, kThreads, 0, stream>>>(a); break;
-    case 64: apply_kernel<T, 64, ROLE, TILES><<<grid, kThreads, 0, stream>>>(a); break;
+    case 8: apply_kernel<T, 8, ROLE, TILES><<<grid, kThreads, 0, stream>>>(WP_APPLY_ARGS); break;
+    case 16: apply_kernel<T, 16, ROLE, TILES><<<grid, kThreads, 0, stream>>>(WP_APPLY_ARGS); break;
+    case 32: apply_kernel<T, 32, ROLE, TILES><<<grid, kThreads, 0, stream>>>(WP_APPLY_ARGS); break;
+    case 64: apply_kernel<T, 64, ROLE, TILES><<<grid, kThreads, 0, stream>>>(WP_APPLY_ARGS); break;
     default: return hipErrorInvalidValue;
   }
+#undef WP_APPLY_ARGS
   return hipGetLastError();
 }
 
