@@ -365,71 +365,49 @@ __device__ __forceinline__ bool wait_partials(const ApplyArgs& a, const Block& b
   return *s_flag != 0;
 }
 
-// H of block b: rn(alpha * sum_c part[c]) for its count x RANK values.  P
-// threads share one 4-wide unit (as many as the 256 threads allow): sub-sum s
-// takes chunks s, s+P, ... in increasing order, and the sub-sums are added in
-// order s = 0..P-1, so every workgroup that reduces the block gets the same
-// bits.  Loads go out in unpredicated batches of four (a load past the last
-// chunk re-reads the last chunk and is discarded); a pass in which any word
-// still held kPartialEmpty is read again by the whole workgroup.
-// emit(j, r0, v4) receives each unit.
-template <int RANK, typename Emit>
-__device__ __forceinline__ void reduce_partials(const ApplyArgs& a, const Block& blk, float alpha, f32x4* s_tmp,
-                                                Emit emit) {
+// H of block b: rn(alpha * sum_c part[c]), each thread polling the partial
+// words it sums until they hold values (CB d-ranges per load batch), so the
+// loads that find a block's last partial also bring its data: once the gate
+// has opened there is no separate read.  A thread owns whole 4-wide units
+// and adds their d-ranges in increasing order, so every workgroup that
+// reduces the block gets the same bits.  (Sharing a unit between lanes and
+// combining with shuffles costs the single-slice kernel spills at its 7
+// waves per SIMD and measured slower.)  emit(j, r0, v4) receives each unit.
+template <int RANK, int CB, typename Emit>
+__device__ __forceinline__ void collect_partials(const ApplyArgs& a, const Block& blk, float alpha, Emit emit) {
   constexpr int R4 = RANK / 4;
   const int n_units = blk.count * R4;
   const int nch = a.n_chunks;
-  int P = 1;
-  while (P < nch && n_units * P * 2 <= kThreads) P *= 2;
-  const int nper = (nch + P - 1) / P;
-  // Byte offsets from a uniform base: the workspace keeps them below 2^32.
   const uint32_t cstride = static_cast<uint32_t>(a.ptok) * static_cast<uint32_t>(a.hs) * 4u;
   const char* pbase = reinterpret_cast<const char*>(a.part + static_cast<int64_t>(blk.first) * a.hs);
-  const int total = n_units * P;
-  for (int t0 = 0; t0 < total; t0 += kThreads) {
-    const int t = t0 + static_cast<int>(threadIdx.x);
-    const bool active = t < total;
-    const int u = t / P;
-    const int s = t - u * P;
+  for (int u = threadIdx.x; u < n_units; u += kThreads) {
     const int j = u / R4;
     const int r0 = (u - j * R4) * 4;
     const uint32_t o0 = static_cast<uint32_t>(j * a.hs + r0) * 4u;
-    f32x4 sum;
-    // The whole pass is read again (by every thread) if any word was empty.
-    for (unsigned spins = 0;; ++spins) {
-      sum = f32x4{0.f, 0.f, 0.f, 0.f};
-      bool missing = false;
-      if (active) {
-        for (int i0 = 0; i0 < nper; i0 += 4) {
-          f32x4 v[4];
+    f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int c0 = 0; c0 < nch; c0 += CB) {
+      f32x4 v[CB];
+      for (unsigned spins = 0;; ++spins) {
+        bool missing = false;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int cc = min(s + (i0 + i) * P, nch - 1);
-            v[i] = coherent_load_f4(reinterpret_cast<const float*>(pbase + (o0 + static_cast<uint32_t>(cc) * cstride)));
-          }
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            missing = missing || any_empty(v[i]);
-            if (s + (i0 + i) * P < nch) sum += v[i];
-          }
+        for (int i = 0; i < CB; ++i) {
+          const int cc = min(c0 + i, nch - 1);
+          v[i] = coherent_load_f4(reinterpret_cast<const float*>(pbase + (o0 + static_cast<uint32_t>(cc) * cstride)));
         }
+#pragma unroll
+        for (int i = 0; i < CB; ++i) missing = missing || any_empty(v[i]);
+        if (!missing) break;
+        if (spins >= kSpinLimit) {
+          flag_error(a.plan.header, kErrSpin);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
       }
-      if (!__syncthreads_or(missing)) break;
-      if (spins >= kSpinLimit) {
-        if (threadIdx.x == 0) flag_error(a.plan.header, kErrSpin);
-        break;
-      }
-      __builtin_amdgcn_s_sleep(4);
+#pragma unroll
+      for (int i = 0; i < CB; ++i)
+        if (c0 + i < nch) sum += v[i];
     }
-    if (P > 1) {
-      s_tmp[threadIdx.x] = sum;
-      __syncthreads();
-      if (active && s == 0) {
-        for (int q = 1; q < P; ++q) sum += s_tmp[threadIdx.x + q];
-      }
-      __syncthreads();
-    }
-    if (active && s == 0) emit(j, r0, sum * alpha);
+    emit(j, r0, sum * alpha);
   }
 }
 
@@ -681,7 +659,7 @@ __device__ __forceinline__ void compute_chunk(const ApplyArgs& a, int b, const B
 // Chunk 0's B and Y are loaded before the wait.
 template <typename T, int RANK, int ROLE, int TILES>
 __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, const Block& blk, int32_t tok0,
-                                            T* s_h, f32x4* s_tmp, T* s_stage, int* s_flag) {
+                                            T* s_h, T* s_stage, int* s_flag) {
   using V8 = typename VecOf<T>::v8;
   constexpr int KS = (RANK + 31) / 32;
   constexpr bool kFusedRole = ROLE == kFused || ROLE == kFusedMulti;
@@ -728,9 +706,14 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
       go = wait_partials(a, blk, wrote, s_flag);
       if (go) {
         if (defer) load_first();
-        reduce_partials<RANK>(a, blk, cur.res.alpha, s_tmp, [&](int j, int r0, f32x4 v) {
+        const auto to_lds = [&](int j, int r0, f32x4 v) {
           *reinterpret_cast<typename VecOf<T>::v4*>(s_h + j * HS + r0) = round4<T>(v);
-        });
+        };
+        if constexpr (ROLE == kFusedMulti) {
+          collect_partials<RANK, 4>(a, blk, cur.res.alpha, to_lds);
+        } else {
+          collect_partials<RANK, 2>(a, blk, cur.res.alpha, to_lds);
+        }
       }
     } else if (wrote > 0) {
       // Nothing to compute, but this may be the workgroup that empties the
@@ -807,15 +790,13 @@ constexpr int waves_per_simd() {
   return wide ? 3 : 5;
 }
 
-// LDS of one workgroup: shrink's cross-wave tiles, or expand's block H plus
-// the reduction's exchange buffer.
+// LDS of one workgroup: shrink's cross-wave tiles, or expand's block H.
 template <typename T, int RANK>
 struct alignas(16) SharedMem {
   static constexpr int RR = RANK == 0 ? kMaxRank : RANK;
   static constexpr int kRed = kShrinkRowsFused / 16 * kWaves * 64;    // f32x4
   static constexpr int kH = (kBlockTokens * (RR + 8) * 2 + 15) / 16;   // f32x4 worth of T
-  static constexpr int kExp = kH + kThreads;
-  f32x4 buf[kRed > kExp ? kRed : kExp];
+  f32x4 buf[kRed > kH ? kRed : kH];
   T stage[kWaves * 16 * kStageStride];  // each wave's Y tile (expand)
 };
 
@@ -837,7 +818,6 @@ void apply_kernel(const uint32_t* header, const Block* __restrict__ blocks,
   __shared__ int s_flag;
   f32x4* s_red = smem.buf;
   T* s_h = reinterpret_cast<T*>(smem.buf);
-  f32x4* s_tmp = smem.buf + SM::kH;
   const int S = ROLE == kExpandOnly ? 0 : n_shrink;
   const int wg = static_cast<int>(blockIdx.x);
   const bool shrink_role = ROLE != kExpandOnly && wg < S;
@@ -874,15 +854,15 @@ void apply_kernel(const uint32_t* header, const Block* __restrict__ blocks,
     return;
   }
   if constexpr (RANK != 0) {
-    expand_body<T, RANK, ROLE, TILES>(a, b, part, blk, t0, s_h, s_tmp, smem.stage, &s_flag);
+    expand_body<T, RANK, ROLE, TILES>(a, b, part, blk, t0, s_h, smem.stage, &s_flag);
   } else {
     // Mixed ranks: the block's adapter decides (resolved again inside).
     const Resolved<T> r0 = resolve_b<T>(a, blk, 0);
     switch (r0.rank) {
-      case 16: expand_body<T, 16, ROLE, TILES>(a, b, part, blk, t0, s_h, s_tmp, smem.stage, &s_flag); break;
-      case 32: expand_body<T, 32, ROLE, TILES>(a, b, part, blk, t0, s_h, s_tmp, smem.stage, &s_flag); break;
-      case 64: expand_body<T, 64, ROLE, TILES>(a, b, part, blk, t0, s_h, s_tmp, smem.stage, &s_flag); break;
-      default: expand_body<T, 8, ROLE, TILES>(a, b, part, blk, t0, s_h, s_tmp, smem.stage, &s_flag); break;
+      case 16: expand_body<T, 16, ROLE, TILES>(a, b, part, blk, t0, s_h, smem.stage, &s_flag); break;
+      case 32: expand_body<T, 32, ROLE, TILES>(a, b, part, blk, t0, s_h, smem.stage, &s_flag); break;
+      case 64: expand_body<T, 64, ROLE, TILES>(a, b, part, blk, t0, s_h, smem.stage, &s_flag); break;
+      default: expand_body<T, 8, ROLE, TILES>(a, b, part, blk, t0, s_h, smem.stage, &s_flag); break;
     }
   }
 }
