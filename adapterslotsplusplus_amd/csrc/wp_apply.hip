@@ -703,7 +703,10 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
   if constexpr (kFusedRole) {
     go = go && wrote > 0;
     if (go) {
-      go = wait_partials(a, blk, wrote, s_flag);
+      // Multi-slice workgroups of small blocks (at most 2048 partial words)
+      // poll the data straight away; the probe gate in front pays off for
+      // larger blocks and for the single-slice kernel (measured on MI355X).
+      go = (ROLE == kFused || blk.count * wrote * a.n_chunks > 2048) ? wait_partials(a, blk, wrote, s_flag) : true;
       if (go) {
         if (defer) load_first();
         const auto to_lds = [&](int j, int r0, f32x4 v) {
