@@ -842,6 +842,10 @@ void apply_kernel(const uint32_t* header, const Block* __restrict__ blocks,
   const Block blk = blocks[b];
   const int row = threadIdx.x & 15;
   const int32_t tok0 = bperm[static_cast<int64_t>(b) * kBlockTokens + row];
+  if constexpr (ROLE == kExpandOnly) {
+    if (b == a.n_slots - 1 && part == 0 && threadIdx.x == 0 && n_blocks > a.n_slots)
+      flag_error(a.plan.header, kErrCapacity);
+  }
   if ((b >= n_blocks) | (blk.count <= 0) | (tok0 < -1)) return;
   const int32_t t0 = row < blk.count ? tok0 : -1;
 
@@ -898,6 +902,7 @@ void shrink_kernel(ApplyArgs a) {
   const int b = static_cast<int>(blockIdx.x) / n_kc;
   const int c = static_cast<int>(blockIdx.x) - b * n_kc;
   const int n_blocks = static_cast<int>(a.plan.header[kHdrNumBlocks]);
+  if (b == a.n_slots - 1 && c == 0 && tid == 0 && n_blocks > a.n_slots) flag_error(a.plan.header, kErrCapacity);
   if (b >= n_blocks) return;
   const Block blk = a.plan.blocks[b];
   const Resolved<T> res = resolve_a<T>(a, blk);

@@ -376,10 +376,17 @@ ApplyArgs base_args(const wp_engine* e, int rank) {
 
 // Upper bound on the block count of the current plan, given at most `groups`
 // distinct adapters: sum_g ceil(n_g / TB) <= floor(T / TB) + G, and <= T.
+// shrink() / expand() on a device-built plan pass the number of registered
+// adapters: a routing that only names registered adapters stays within the
+// bound, and the kernels flag kErrCapacity when it does not (ids that are
+// not registered sort among the others and can push blocks past it).
+// Bounding by T alone would launch mostly empty workgroups on large plans
+// (8192 tokens: 8192 slots x 48 chunks for 144 real blocks, ~150 us of
+// dispatch), and a loop over items in the kernels costs their registers.
 int block_bound(const wp_engine* e, int64_t groups) {
   if (e->plan_kind == 1) return e->plan_blocks;
   const int64_t T = e->plan_T;
-  const int64_t g = std::min<int64_t>(T, std::max<int64_t>(groups, 0));
+  const int64_t g = std::min<int64_t>(T, std::max<int64_t>(groups, 1));
   return static_cast<int>(std::min<int64_t>(T, T / e->plan_bt + g));
 }
 
@@ -885,7 +892,7 @@ int wp_shrink(wp_engine* e, const void* X, void* H, int32_t d_model, int32_t ran
   uint32_t mask = 0;
   if ((rc = table_weights(e, stream, &a.w, &mask)) != WP_OK) return rc;
   a.w.n_slices = 1;
-  a.n_slots = block_bound(e, e->plan_T);
+  a.n_slots = block_bound(e, static_cast<int64_t>(e->adapters.size()));
   shrink_range_split(d_model, &a);
   a.part = e->spart;
   WP_HIP(launch_shrink(dtype == WP_DTYPE_BF16, a, stream));
@@ -938,7 +945,7 @@ int wp_expand(wp_engine* e, const void* H, void* Y, int32_t out_features, int32_
   a.w.oc_start[0] = 0;
   a.w.oc_start[1] = static_cast<int32_t>(ceil_div(out_features, cols));
   a.n_ochunks = a.w.oc_start[1];
-  a.n_slots = block_bound(e, e->plan_T);
+  a.n_slots = block_bound(e, static_cast<int64_t>(e->adapters.size()));
   WP_HIP(launch_expand(dtype == WP_DTYPE_BF16, a, stream));
   if (e->plan_kind == 1) record_slot_uses(e, e->plan_entry_slot, stream);
   else record_mask_uses(e, mask, stream);

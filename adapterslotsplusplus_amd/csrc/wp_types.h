@@ -83,7 +83,9 @@ enum DeviceError : uint32_t {
   kErrIdRange = 1u,       // stacked weights: adapter id >= num_loras
   kErrUnregistered = 2u,  // adapter table: id not registered / not resident
   kErrShape = 4u,         // adapter rank / d / o differs from the call's
-  kErrSpin = 8u           // a fused call's expand side gave up waiting
+  kErrSpin = 8u,          // a fused call's expand side gave up waiting
+  kErrCapacity = 16u      // shrink() / expand(): the plan has more blocks than the call's grid
+                          // (the routing names adapter ids that are not registered)
 };
 
 struct Segment {  // 16 B; the reference descriptor's first three fields

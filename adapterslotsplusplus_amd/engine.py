@@ -222,7 +222,9 @@ class WarpPipeEngine:
 
     def device_errors(self) -> int:
         """Reads and clears the device error word (adapters the kernels had to
-        skip: id out of range / unregistered / shape mismatch)."""
+        skip: 1 id out of range, 2 unregistered, 4 shape mismatch; 8 a fused
+        call's wait gave up; 16 shrink()/expand() found more blocks than the
+        registered adapters allow, i.e. the routing names unregistered ids)."""
         v = ctypes.c_uint32(0)
         _lib.check(self._lib.wp_read_device_errors(self._handle, ctypes.byref(v), self._stream()), "device_errors")
         return int(v.value)

@@ -389,6 +389,32 @@ def test_out_of_range_ids_are_skipped_and_flagged():
     assert engine.device_errors() & 1
 
 
+def test_store_calls_flag_routing_past_the_block_bound():
+    """shrink()/expand() on a build_seg_bounds plan size their grid for the
+    registered adapters (T/16 + 2 blocks here).  A routing that names 48
+    unregistered ids has more blocks than that: the call skips what it does
+    not cover and says so (unregistered 2, capacity 16); registered-only
+    routing of the same length is complete."""
+    announce("block bound of store calls")
+    dtype = torch.bfloat16
+    engine = WarpPipeEngine()
+    adapters = register(engine, 2, 16, 512, 256, dtype, 290, 0.5, ids=[50, 51])
+    T = 64
+    X = randn((T, 512), 291, dtype)
+    idx = np.concatenate([np.arange(48), np.full(8, 50), np.full(8, 51)])
+    assert engine.build_seg_bounds(torch.from_numpy(idx).cuda())
+    engine.shrink(X.cuda(), 512, 16, T)
+    torch.cuda.synchronize()
+    err = engine.device_errors()
+    assert err & 16 and err & 2
+    idx = np.random.default_rng(4).choice([50, 51], size=T)
+    assert engine.build_seg_bounds(torch.from_numpy(idx).cuda())
+    H = engine.shrink(X.cuda(), 512, 16, T)
+    torch.cuda.synchronize()
+    assert_close(H, bgmv.shrink(X, so.seg_bounds(idx).tolist(), adapters, 16, T), "H")
+    assert engine.device_errors() == 0
+
+
 def test_plan_token_count_must_fit_call():
     engine = WarpPipeEngine()
     assert engine.build_seg_bounds(torch.zeros(32, dtype=torch.int64, device="cuda"))
