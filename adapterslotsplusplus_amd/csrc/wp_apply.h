@@ -48,6 +48,10 @@ hipError_t launch_fused(int dtype_bf16, const ApplyArgs& a, hipStream_t stream);
 // shrink(): one workgroup per (block, d-range) computes every rank row; the
 // block's last workgroup to finish sums the d-ranges into H[token].
 hipError_t launch_shrink(int dtype_bf16, const ApplyArgs& a, hipStream_t stream);
+// shrink() of decode-sized plans: the fused kernel's shrink workgroups
+// (kShrinkRowsFused rows x d-range) and one reducer per block writing H;
+// a.part is the fused calls' partial buffer (kPartialEmpty between calls).
+hipError_t launch_shrink_small(int dtype_bf16, const ApplyArgs& a, hipStream_t stream);
 // expand(): expand from a caller-provided token-indexed H.
 hipError_t launch_expand(int dtype_bf16, const ApplyArgs& a, hipStream_t stream);
 

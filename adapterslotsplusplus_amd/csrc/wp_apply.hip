@@ -88,7 +88,9 @@ constexpr unsigned kSpinLimit = 1u << 17;
 constexpr int kShrinkWavesPerSimd = 4;
 
 // kFusedMulti: fused, with several output chunks per expand workgroup.
-enum Role : int { kFused = 0, kExpandOnly = 2, kFusedMulti = 3 };
+// kShrinkOnly: shrink() of decode-sized plans: the fused shrink side, and
+// one workgroup per block that sums the partials into H.
+enum Role : int { kFused = 0, kShrinkOnly = 1, kExpandOnly = 2, kFusedMulti = 3 };
 
 __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -373,9 +375,9 @@ __device__ __forceinline__ bool wait_partials(const ApplyArgs& a, const Block& b
 // reduces the block gets the same bits.  (Sharing a unit between lanes and
 // combining with shuffles costs the single-slice kernel spills at its 7
 // waves per SIMD and measured slower.)  emit(j, r0, v4) receives each unit.
-template <int RANK, int CB, typename Emit>
-__device__ __forceinline__ void collect_partials(const ApplyArgs& a, const Block& blk, float alpha, Emit emit) {
-  constexpr int R4 = RANK / 4;
+template <int CB, typename Emit>
+__device__ __forceinline__ void collect_partials(const ApplyArgs& a, const Block& blk, const int R4, float alpha,
+                                                 Emit emit) {
   const int n_units = blk.count * R4;
   const int nch = a.n_chunks;
   const uint32_t cstride = static_cast<uint32_t>(a.ptok) * static_cast<uint32_t>(a.hs) * 4u;
@@ -713,9 +715,9 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
           *reinterpret_cast<typename VecOf<T>::v4*>(s_h + j * HS + r0) = round4<T>(v);
         };
         if constexpr (ROLE == kFusedMulti) {
-          collect_partials<RANK, 4>(a, blk, cur.res.alpha, to_lds);
+          collect_partials<4>(a, blk, RANK / 4, cur.res.alpha, to_lds);
         } else {
-          collect_partials<RANK, 2>(a, blk, cur.res.alpha, to_lds);
+          collect_partials<2>(a, blk, RANK / 4, cur.res.alpha, to_lds);
         }
       }
     } else if (wrote > 0) {
@@ -778,6 +780,25 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
   }
 }
 
+// shrink() of decode-sized plans (role kShrinkOnly): block b's one reader
+// sums its partials into H[token] = rn(alpha * sum_c part[c]) and, once
+// every thread has read its words, restores kPartialEmpty over them.
+template <typename T>
+__device__ __forceinline__ void reduce_to_h(const ApplyArgs& a, int b, const Block& blk, int* s_flag) {
+  const Resolved<T> res = resolve_a<T>(a, blk);
+  // Rank rows the shrink side wrote (none if it could not resolve the adapter).
+  const int wrote = res.ptr != nullptr ? res.rank : 0;
+  if (wrote <= 0) return;
+  if (blk.count * wrote * a.n_chunks > 2048) wait_partials(a, blk, wrote, s_flag);
+  T* H = static_cast<T*>(a.h);
+  const int32_t* toks = a.plan.bperm + static_cast<int64_t>(b) * kBlockTokens;
+  collect_partials<4>(a, blk, wrote / 4, res.alpha, [&](int j, int r0, f32x4 v) {
+    store4<T>(H + static_cast<int64_t>(toks[j]) * a.ldh + r0, v);
+  });
+  __syncthreads();
+  clear_partials(a, blk, wrote, threadIdx.x, kThreads);
+}
+
 // ---------------------------------------------------------------- kernels ----
 
 // Occupancy target (waves per SIMD), from the registers each variant needs
@@ -789,6 +810,7 @@ constexpr int waves_per_simd() {
   constexpr bool wide = RANK == 0 || RANK == 64;
   if (ROLE == kFused) return wide ? 5 : 7;
   if (ROLE == kFusedMulti) return 4;
+  if (ROLE == kShrinkOnly) return 5;
   if (TILES == 1) return wide ? 5 : 8;
   return wide ? 3 : 5;
 }
@@ -842,7 +864,7 @@ void apply_kernel(const uint32_t* header, const Block* __restrict__ blocks,
   const Block blk = blocks[b];
   const int row = threadIdx.x & 15;
   const int32_t tok0 = bperm[static_cast<int64_t>(b) * kBlockTokens + row];
-  if constexpr (ROLE == kExpandOnly) {
+  if constexpr (ROLE == kExpandOnly || ROLE == kShrinkOnly) {
     if (b == a.n_slots - 1 && part == 0 && threadIdx.x == 0 && n_blocks > a.n_slots)
       flag_error(a.plan.header, kErrCapacity);
   }
@@ -853,14 +875,16 @@ void apply_kernel(const uint32_t* header, const Block* __restrict__ blocks,
     const Resolved<T> res = resolve_a<T>(a, blk);
     if (res.err != 0 && part == 0 && threadIdx.x == 0) flag_error(a.plan.header, res.err);
     const int rg = part / a.n_chunks;
-    if constexpr (ROLE == kFusedMulti) {
+    if constexpr (ROLE == kFusedMulti || ROLE == kShrinkOnly) {
       shrink_body<T, kShrinkRowsFused / 16>(a, b, part - rg * a.n_chunks, rg * kShrinkRowsFused, blk, t0, res, s_red);
     } else {
       shrink_body<T, 1>(a, b, part - rg * a.n_chunks, rg * kShrinkRows, blk, t0, res, s_red);
     }
     return;
   }
-  if constexpr (RANK != 0) {
+  if constexpr (ROLE == kShrinkOnly) {
+    reduce_to_h<T>(a, b, blk, &s_flag);
+  } else if constexpr (RANK != 0) {
     expand_body<T, RANK, ROLE, TILES>(a, b, part, blk, t0, s_h, smem.stage, &s_flag);
   } else {
     // Mixed ranks: the block's adapter decides (resolved again inside).
@@ -1098,19 +1122,24 @@ hipError_t launch_rank(const ApplyArgs& a, hipStream_t stream) {
   const int32_t per_shrink = a.n_chunks * a.n_rgroups;
   const int32_t per_block = (a.n_ochunks + a.n_sub - 1) / a.n_sub;
 #define WP_APPLY_ARGS a.plan.header, a.plan.blocks, a.plan.bperm, per_shrink, static_cast<int32_t>(S), per_block, a
-  switch (a.rank) {
-    case 0:  // mixed ranks: registered adapters only, which the fused calls do not take
-      if constexpr (ROLE == kExpandOnly) {
-        apply_kernel<T, 0, ROLE, TILES><<<grid, kThreads, 0, stream>>>(WP_APPLY_ARGS);
-        break;
-      } else {
-        return hipErrorInvalidValue;
-      }
-    case 8: apply_kernel<T, 8, ROLE, TILES><<<grid, kThreads, 0, stream>>>(WP_APPLY_ARGS); break;
-    case 16: apply_kernel<T, 16, ROLE, TILES><<<grid, kThreads, 0, stream>>>(WP_APPLY_ARGS); break;
-    case 32: apply_kernel<T, 32, ROLE, TILES><<<grid, kThreads, 0, stream>>>(WP_APPLY_ARGS); break;
-    case 64: apply_kernel<T, 64, ROLE, TILES><<<grid, kThreads, 0, stream>>>(WP_APPLY_ARGS); break;
-    default: return hipErrorInvalidValue;
+  if constexpr (ROLE == kShrinkOnly) {
+    // Its shrink side takes the rank from each block's adapter.
+    apply_kernel<T, 0, ROLE, TILES><<<grid, kThreads, 0, stream>>>(WP_APPLY_ARGS);
+  } else {
+    switch (a.rank) {
+      case 0:  // mixed ranks: registered adapters only, which the fused calls do not take
+        if constexpr (ROLE == kExpandOnly) {
+          apply_kernel<T, 0, ROLE, TILES><<<grid, kThreads, 0, stream>>>(WP_APPLY_ARGS);
+          break;
+        } else {
+          return hipErrorInvalidValue;
+        }
+      case 8: apply_kernel<T, 8, ROLE, TILES><<<grid, kThreads, 0, stream>>>(WP_APPLY_ARGS); break;
+      case 16: apply_kernel<T, 16, ROLE, TILES><<<grid, kThreads, 0, stream>>>(WP_APPLY_ARGS); break;
+      case 32: apply_kernel<T, 32, ROLE, TILES><<<grid, kThreads, 0, stream>>>(WP_APPLY_ARGS); break;
+      case 64: apply_kernel<T, 64, ROLE, TILES><<<grid, kThreads, 0, stream>>>(WP_APPLY_ARGS); break;
+      default: return hipErrorInvalidValue;
+    }
   }
 #undef WP_APPLY_ARGS
   return hipGetLastError();
@@ -1144,6 +1173,11 @@ hipError_t launch_fused(int dtype_bf16, const ApplyArgs& a, hipStream_t stream) 
 hipError_t launch_shrink(int dtype_bf16, const ApplyArgs& a, hipStream_t stream) {
   if (a.n_chunks < 1 || a.n_chunks > kMaxChunks) return hipErrorInvalidValue;
   return dtype_bf16 ? launch_shrink_t<__bf16>(a, stream) : launch_shrink_t<_Float16>(a, stream);
+}
+hipError_t launch_shrink_small(int dtype_bf16, const ApplyArgs& a, hipStream_t stream) {
+  if (a.srows != kShrinkRowsFused || a.n_ochunks != 1 || a.n_sub != 1 || a.n_chunks < 1 || a.n_chunks > kMaxChunks)
+    return hipErrorInvalidValue;
+  return launch_role<kShrinkOnly>(dtype_bf16, a, stream);
 }
 hipError_t launch_expand(int dtype_bf16, const ApplyArgs& a, hipStream_t stream) {
   return launch_role<kExpandOnly>(dtype_bf16, a, stream);

@@ -126,6 +126,22 @@ inline void shrink_split(int d, int rank, int rows, int64_t slots, int64_t expan
   a->n_rgroups = g;
 }
 
+// Split of a decode-sized shrink() launch: 32-row rank groups x d-ranges of
+// about 512 columns (each wave's share one batch of loads), or 1024 columns
+// past ten ranges (fewer workgroups than residency rounds; measured on
+// MI355X at d = 5120 and 13824), at most kMaxChunks; one reducer workgroup
+// per block.
+inline void shrink_small_split(int d, int rank, ApplyArgs* a) {
+  int64_t n = std::max<int64_t>(ceil_div(d, 512), 1);
+  if (n > 10) n = std::min<int64_t>(ceil_div(d, 1024), kMaxChunks);
+  a->dc = static_cast<int>(ceil_div(ceil_div(d, n), 128) * 128);
+  a->n_chunks = static_cast<int>(ceil_div(d, a->dc));
+  a->srows = kShrinkRowsFused;
+  a->n_rgroups = shrink_rank_groups(rank, kShrinkRowsFused);
+  a->n_ochunks = 1;
+  a->n_sub = 1;
+}
+
 // d-ranges of a shrink() launch: one workgroup per block and d-range, every
 // rank row; a d-range is kShrinkSlices x 128 columns (a multiple of that
 // past kMaxChunks ranges).
@@ -893,9 +909,17 @@ int wp_shrink(wp_engine* e, const void* X, void* H, int32_t d_model, int32_t ran
   if ((rc = table_weights(e, stream, &a.w, &mask)) != WP_OK) return rc;
   a.w.n_slices = 1;
   a.n_slots = block_bound(e, static_cast<int64_t>(e->adapters.size()));
-  shrink_range_split(d_model, &a);
-  a.part = e->spart;
-  WP_HIP(launch_shrink(dtype == WP_DTYPE_BF16, a, stream));
+  if (e->plan_T <= kSmallPlanTokens) {
+    // Decode-sized plans: many small shrink workgroups and a reducer per
+    // block (the fused calls' shrink side), not one workgroup per block and
+    // d-range streaming every rank row.
+    shrink_small_split(d_model, rank, &a);
+    WP_HIP(launch_shrink_small(dtype == WP_DTYPE_BF16, a, stream));
+  } else {
+    shrink_range_split(d_model, &a);
+    a.part = e->spart;
+    WP_HIP(launch_shrink(dtype == WP_DTYPE_BF16, a, stream));
+  }
   if (e->plan_kind == 1) record_slot_uses(e, e->plan_entry_slot, stream);
   else record_mask_uses(e, mask, stream);
   return WP_OK;
