@@ -176,6 +176,21 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 __device__ __forceinline__ void flag_error(uint32_t* header, uint32_t bits) { atomicOr(&header[kHdrErrors], bits); }
 
 // A block's weights as the kernels see them.
+// The adapter-table entry as two 16-byte loads (field by field, with a test
+// between, the compiler issued three dependent loads).
+__device__ __forceinline__ Entry load_entry(const Entry* p) {
+  const u32x4 lo = load16_global(p);
+  const u32x4 hi = load16_global(reinterpret_cast<const char*>(p) + 16);
+  Entry e;
+  e.a_ptr = static_cast<uint64_t>(lo[0]) | (static_cast<uint64_t>(lo[1]) << 32);
+  e.b_ptr = static_cast<uint64_t>(lo[2]) | (static_cast<uint64_t>(lo[3]) << 32);
+  e.alpha = __builtin_bit_cast(float, hi[0]);
+  e.rank = static_cast<int32_t>(hi[1]);
+  e.d_model = static_cast<int32_t>(hi[2]);
+  e.out_features = static_cast<int32_t>(hi[3]);
+  return e;
+}
+
 template <typename T>
 struct Resolved {
   const T* ptr = nullptr;
@@ -201,8 +216,9 @@ __device__ __forceinline__ Resolved<T> resolve_a(const ApplyArgs& a, const Block
     r.err = kErrUnregistered;
     return r;
   }
-  const Entry en = a.w.entries[blk.entry];
-  if (en.a_ptr == 0 || en.b_ptr == 0) {
+  const Entry en = load_entry(a.w.entries + blk.entry);
+  // One test over both halves, so that both loads go out before the wait.
+  if ((en.a_ptr == 0) | (en.b_ptr == 0) | (en.rank <= 0)) {
     r.err = kErrUnregistered;
     return r;
   }
@@ -233,8 +249,9 @@ __device__ __forceinline__ Resolved<T> resolve_b(const ApplyArgs& a, const Block
     r.err = kErrUnregistered;
     return r;
   }
-  const Entry en = a.w.entries[blk.entry];
-  if (en.a_ptr == 0 || en.b_ptr == 0) {
+  const Entry en = load_entry(a.w.entries + blk.entry);
+  // One test over both halves, so that both loads go out before the wait.
+  if ((en.a_ptr == 0) | (en.b_ptr == 0) | (en.rank <= 0)) {
     r.err = kErrUnregistered;
     return r;
   }
