@@ -692,30 +692,7 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
   const int wrote = kFusedRole ? resolve_a<T>(a, blk).rank : 0;
   V8 bf[kOT][KS];
   YRows yq;
-  // Multi-chunk workgroups keep two chunks' B and Y in registers: chunk 1
-  // loads before the wait too, and chunk i + 2 while chunk i + 1 runs.
-  constexpr bool kTwoSets = ROLE == kFusedMulti && RANK <= 32;
-  OutChunk<T> cur2;
-  V8 bf2[kOT][KS];
-  YRows yq2;
-  if constexpr (kTwoSets) {
-    if (a.n_sub > 1 && p + n_owg < a.n_ochunks) {
-      cur2 = out_chunk<T>(a, blk, p + n_owg);
-      if (cur2.res.err != 0 && p == 0 && threadIdx.x == 0) flag_error(a.plan.header, cur2.res.err);
-    }
-  }
-  // A wave's loads complete in order, so the wave that polls for the
-  // partials (wave 0) loads its chunk columns only once they are there:
-  // otherwise a workgroup that starts late sees the partials only after its
-  // own chunk loads have landed.
-  const bool defer = ROLE == kFusedMulti && (threadIdx.x >> 6) == 0;
-  auto load_first = [&]() {
-    load_chunk<T, RANK>(a, cur, tok0, bf, yq);
-    if constexpr (kTwoSets) {
-      if (cur2.res.ptr != nullptr) load_chunk<T, RANK>(a, cur2, tok0, bf2, yq2);
-    }
-  };
-  if (!defer) load_first();
+  load_chunk<T, RANK>(a, cur, tok0, bf, yq);
 
   bool go = cur.res.ptr != nullptr;
   unsigned consumed_prev = 0;
@@ -727,7 +704,6 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
       // larger blocks and for the single-slice kernel (measured on MI355X).
       go = (ROLE == kFused || blk.count * wrote * a.n_chunks > 2048) ? wait_partials(a, blk, wrote, s_flag) : true;
       if (go) {
-        if (defer) load_first();
         const auto to_lds = [&](int j, int r0, f32x4 v) {
           *reinterpret_cast<typename VecOf<T>::v4*>(s_h + j * HS + r0) = round4<T>(v);
         };
@@ -748,28 +724,10 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
     if (threadIdx.x == 0) consumed_prev = atomic_add_u(&a.consumed[b * kCounterStride], 1u);
   }
   if (go) {
-    if constexpr (kTwoSets) {
-      for (int i = 0; i < a.n_sub; i += 2) {
-        if (p + i * n_owg >= a.n_ochunks) break;
-        if (cur.res.ptr != nullptr) compute_chunk<T, RANK, true, 1>(a, b, blk, tok0, cur, bf, yq, s_h, stage);
-        const int oc_a = p + (i + 2) * n_owg;
-        if (i + 2 < a.n_sub && oc_a < a.n_ochunks) {
-          cur = out_chunk<T>(a, blk, oc_a);
-          if (cur.res.err != 0 && p == 0 && threadIdx.x == 0) flag_error(a.plan.header, cur.res.err);
-          load_chunk<T, RANK>(a, cur, tok0, bf, yq);
-        }
-        if (i + 1 >= a.n_sub || p + (i + 1) * n_owg >= a.n_ochunks) break;
-        if (cur2.res.ptr != nullptr) compute_chunk<T, RANK, true, 1>(a, b, blk, tok0, cur2, bf2, yq2, s_h, stage);
-        const int oc_b = p + (i + 3) * n_owg;
-        if (i + 3 < a.n_sub && oc_b < a.n_ochunks) {
-          cur2 = out_chunk<T>(a, blk, oc_b);
-          if (cur2.res.err != 0 && p == 0 && threadIdx.x == 0) flag_error(a.plan.header, cur2.res.err);
-          load_chunk<T, RANK>(a, cur2, tok0, bf2, yq2);
-        }
-      }
-    } else if constexpr (ROLE == kFusedMulti) {
-      // Rank 64: chunks after the first load when they are reached (a second
-      // set of its B fragments would cost more occupancy than it saves).
+    if constexpr (ROLE == kFusedMulti) {
+      // Chunks after the first load when they are reached: a second set of
+      // B and Y registers (the next chunk loading while one is computed)
+      // costs a wave per SIMD, and measured slower (qkv 19.33 vs 19.08 us).
       for (int i = 0; i < a.n_sub; ++i) {
         const int oc = p + i * n_owg;
         if (oc >= a.n_ochunks) break;
@@ -826,7 +784,7 @@ template <int RANK, int ROLE, int TILES>
 constexpr int waves_per_simd() {
   constexpr bool wide = RANK == 0 || RANK == 64;
   if (ROLE == kFused) return wide ? 5 : 7;
-  if (ROLE == kFusedMulti) return 4;
+  if (ROLE == kFusedMulti) return wide ? 4 : 5;
   if (ROLE == kShrinkOnly) return 5;
   if (TILES == 1) return wide ? 5 : 8;
   return wide ? 3 : 5;
