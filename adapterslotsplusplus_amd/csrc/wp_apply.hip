@@ -54,12 +54,15 @@ namespace wp {
 namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 template <typename T>
 struct VecOf;
@@ -67,11 +70,13 @@ template <>
 struct VecOf<__bf16> {
   using v8 = bf16x8;
   using v4 = bf16x4;
+  using v2 = bf16x2;
 };
 template <>
 struct VecOf<_Float16> {
   using v8 = f16x8;
   using v4 = f16x4;
+  using v2 = f16x2;
 };
 
 constexpr int kThreads = 256;
@@ -430,6 +435,47 @@ __device__ __forceinline__ void collect_partials(const ApplyArgs& a, const Block
   }
 }
 
+// The same with 2-wide units (8-byte loads): half the registers per d-range
+// in flight, so the single-slice kernel, at its 7 waves per SIMD, takes four
+// d-ranges per batch.  emit(j, r0, v2).
+template <int CB, typename Emit>
+__device__ __forceinline__ void collect_partials2(const ApplyArgs& a, const Block& blk, const int R2, float alpha,
+                                                  Emit emit) {
+  const int n_units = blk.count * R2;
+  const int nch = a.n_chunks;
+  const uint32_t cstride = static_cast<uint32_t>(a.ptok) * static_cast<uint32_t>(a.hs) * 4u;
+  const char* pbase = reinterpret_cast<const char*>(a.part + static_cast<int64_t>(blk.first) * a.hs);
+  for (int u = threadIdx.x; u < n_units; u += kThreads) {
+    const int j = u / R2;
+    const int r0 = (u - j * R2) * 2;
+    const uint32_t o0 = static_cast<uint32_t>(j * a.hs + r0) * 4u;
+    f32x2 sum = f32x2{0.f, 0.f};
+    for (int c0 = 0; c0 < nch; c0 += CB) {
+      f32x2 v[CB];
+      for (unsigned spins = 0;; ++spins) {
+        bool missing = false;
+#pragma unroll
+        for (int i = 0; i < CB; ++i) {
+          const int cc = min(c0 + i, nch - 1);
+          v[i] = __builtin_bit_cast(f32x2, coherent_load8(pbase + (o0 + static_cast<uint32_t>(cc) * cstride)));
+        }
+#pragma unroll
+        for (int i = 0; i < CB; ++i) missing = missing || is_empty(v[i][0]) || is_empty(v[i][1]);
+        if (!missing) break;
+        if (spins >= kSpinLimit) {
+          flag_error(a.plan.header, kErrSpin);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+#pragma unroll
+      for (int i = 0; i < CB; ++i)
+        if (c0 + i < nch) sum += v[i];
+    }
+    emit(j, r0, sum * alpha);
+  }
+}
+
 // Waits until every partial word the block's shrink workgroups write (count x
 // rank values of every d-range) holds a value, without using them.
 __device__ __forceinline__ void await_partials(const ApplyArgs& a, const Block& blk, int rank) {
@@ -710,7 +756,12 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
         if constexpr (ROLE == kFusedMulti) {
           collect_partials<4>(a, blk, RANK / 4, cur.res.alpha, to_lds);
         } else {
-          collect_partials<2>(a, blk, RANK / 4, cur.res.alpha, to_lds);
+          collect_partials2<4>(a, blk, RANK / 2, cur.res.alpha, [&](int j, int r0, f32x2 v) {
+            typename VecOf<T>::v2 o;
+            o[0] = static_cast<T>(v[0]);
+            o[1] = static_cast<T>(v[1]);
+            *reinterpret_cast<typename VecOf<T>::v2*>(s_h + j * HS + r0) = o;
+          });
         }
       }
     } else if (wrote > 0) {
