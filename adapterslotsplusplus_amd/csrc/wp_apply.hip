@@ -392,54 +392,15 @@ __device__ __forceinline__ bool wait_partials(const ApplyArgs& a, const Block& b
 // H of block b: rn(alpha * sum_c part[c]), each thread polling the partial
 // words it sums until they hold values (CB d-ranges per load batch), so the
 // loads that find a block's last partial also bring its data: once the gate
-// has opened there is no separate read.  A thread owns whole 4-wide units
-// and adds their d-ranges in increasing order, so every workgroup that
-// reduces the block gets the same bits.  (Sharing a unit between lanes and
-// combining with shuffles costs the single-slice kernel spills at its 7
-// waves per SIMD and measured slower.)  emit(j, r0, v4) receives each unit.
+// has opened there is no separate read.  A thread owns whole 2-wide units
+// (8-byte loads: half the registers per d-range in flight of 4-wide ones,
+// so more d-ranges go out per batch) and adds their d-ranges in increasing
+// order, so every workgroup that reduces the block gets the same bits.
+// (Sharing a unit between lanes and combining with shuffles cost the
+// single-slice kernel spills and measured slower.)  emit(j, r0, v2)
+// receives each unit.
 template <int CB, typename Emit>
-__device__ __forceinline__ void collect_partials(const ApplyArgs& a, const Block& blk, const int R4, float alpha,
-                                                 Emit emit) {
-  const int n_units = blk.count * R4;
-  const int nch = a.n_chunks;
-  const uint32_t cstride = static_cast<uint32_t>(a.ptok) * static_cast<uint32_t>(a.hs) * 4u;
-  const char* pbase = reinterpret_cast<const char*>(a.part + static_cast<int64_t>(blk.first) * a.hs);
-  for (int u = threadIdx.x; u < n_units; u += kThreads) {
-    const int j = u / R4;
-    const int r0 = (u - j * R4) * 4;
-    const uint32_t o0 = static_cast<uint32_t>(j * a.hs + r0) * 4u;
-    f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int c0 = 0; c0 < nch; c0 += CB) {
-      f32x4 v[CB];
-      for (unsigned spins = 0;; ++spins) {
-        bool missing = false;
-#pragma unroll
-        for (int i = 0; i < CB; ++i) {
-          const int cc = min(c0 + i, nch - 1);
-          v[i] = coherent_load_f4(reinterpret_cast<const float*>(pbase + (o0 + static_cast<uint32_t>(cc) * cstride)));
-        }
-#pragma unroll
-        for (int i = 0; i < CB; ++i) missing = missing || any_empty(v[i]);
-        if (!missing) break;
-        if (spins >= kSpinLimit) {
-          flag_error(a.plan.header, kErrSpin);
-          break;
-        }
-        __builtin_amdgcn_s_sleep(2);
-      }
-#pragma unroll
-      for (int i = 0; i < CB; ++i)
-        if (c0 + i < nch) sum += v[i];
-    }
-    emit(j, r0, sum * alpha);
-  }
-}
-
-// The same with 2-wide units (8-byte loads): half the registers per d-range
-// in flight, so the single-slice kernel, at its 7 waves per SIMD, takes four
-// d-ranges per batch.  emit(j, r0, v2).
-template <int CB, typename Emit>
-__device__ __forceinline__ void collect_partials2(const ApplyArgs& a, const Block& blk, const int R2, float alpha,
+__device__ __forceinline__ void collect_partials(const ApplyArgs& a, const Block& blk, const int R2, float alpha,
                                                   Emit emit) {
   const int n_units = blk.count * R2;
   const int nch = a.n_chunks;
@@ -750,18 +711,19 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
       // larger blocks and for the single-slice kernel (measured on MI355X).
       go = (ROLE == kFused || blk.count * wrote * a.n_chunks > 2048) ? wait_partials(a, blk, wrote, s_flag) : true;
       if (go) {
-        const auto to_lds = [&](int j, int r0, f32x4 v) {
-          *reinterpret_cast<typename VecOf<T>::v4*>(s_h + j * HS + r0) = round4<T>(v);
+        const auto to_lds = [&](int j, int r0, f32x2 v) {
+          typename VecOf<T>::v2 o;
+          o[0] = static_cast<T>(v[0]);
+          o[1] = static_cast<T>(v[1]);
+          *reinterpret_cast<typename VecOf<T>::v2*>(s_h + j * HS + r0) = o;
         };
+        // Batches of d-ranges: all eight of a multi-slice call's at once;
+        // four in the single-slice kernel (eight cost it a spill and
+        // measured slower).
         if constexpr (ROLE == kFusedMulti) {
-          collect_partials<4>(a, blk, RANK / 4, cur.res.alpha, to_lds);
+          collect_partials<8>(a, blk, RANK / 2, cur.res.alpha, to_lds);
         } else {
-          collect_partials2<4>(a, blk, RANK / 2, cur.res.alpha, [&](int j, int r0, f32x2 v) {
-            typename VecOf<T>::v2 o;
-            o[0] = static_cast<T>(v[0]);
-            o[1] = static_cast<T>(v[1]);
-            *reinterpret_cast<typename VecOf<T>::v2*>(s_h + j * HS + r0) = o;
-          });
+          collect_partials<4>(a, blk, RANK / 2, cur.res.alpha, to_lds);
         }
       }
     } else if (wrote > 0) {
@@ -818,8 +780,11 @@ __device__ __forceinline__ void reduce_to_h(const ApplyArgs& a, int b, const Blo
   if (blk.count * wrote * a.n_chunks > 2048) wait_partials(a, blk, wrote, s_flag);
   T* H = static_cast<T*>(a.h);
   const int32_t* toks = a.plan.bperm + static_cast<int64_t>(b) * kBlockTokens;
-  collect_partials<4>(a, blk, wrote / 4, res.alpha, [&](int j, int r0, f32x4 v) {
-    store4<T>(H + static_cast<int64_t>(toks[j]) * a.ldh + r0, v);
+  collect_partials<8>(a, blk, wrote / 2, res.alpha, [&](int j, int r0, f32x2 v) {
+    typename VecOf<T>::v2 o;
+    o[0] = static_cast<T>(v[0]);
+    o[1] = static_cast<T>(v[1]);
+    *reinterpret_cast<typename VecOf<T>::v2*>(H + static_cast<int64_t>(toks[j]) * a.ldh + r0) = o;
   });
   __syncthreads();
   clear_partials(a, blk, wrote, threadIdx.x, kThreads);
