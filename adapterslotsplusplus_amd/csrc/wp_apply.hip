@@ -17,15 +17,16 @@
 //                       d-range and reduce through LDS; the workgroup
 //                       stores its fp32 partial H coherently.
 //   expand workgroups   block b, 256 output columns (of each slice).  They
-//                       load their B rows and current Y, wait until the
-//                       block's partials hold values (the buffer holds the
-//                       NaN pattern kPartialEmpty between calls, which no
-//                       bf16/fp16 computation produces), sum them in a fixed
-//                       order (so every workgroup, and every run, gets the
-//                       same bits), apply alpha once and round H to the I/O
-//                       dtype in LDS (reference :129, :360), then run the
-//                       MFMAs and store Y = rn(Y + H.B^T) (reference :194).
-//                       The last one of the block empties its partials again.
+//                       load their B rows and current Y, poll the block's
+//                       partials until they hold values (the buffer holds
+//                       the NaN pattern kPartialEmpty between calls, which no
+//                       bf16/fp16 computation produces) -- the polling loads
+//                       are the reads -- sum them in a fixed order (so every
+//                       workgroup, and every run, gets the same bits), apply
+//                       alpha once and round H to the I/O dtype in LDS
+//                       (reference :129, :360), then run the MFMAs and store
+//                       Y = rn(Y + H.B^T) (reference :194).  The last one of
+//                       the block empties its partials again.
 //
 // Summing the partials in every expand workgroup re-reads a few KB per
 // workgroup but keeps the cross-workgroup chain to one hop: the partial
@@ -43,9 +44,10 @@
 // past the device block count exit at once.
 //
 // The expand-only variant serves expand() of the engine API and the expand
-// half of large-plan calls; shrink() has its own kernel (shrink_kernel),
-// which computes every rank row of a block per workgroup and streams the
-// d-range through LDS.
+// half of large-plan calls.  shrink() of decode-sized plans runs the shrink
+// side with one reducer workgroup per block (kShrinkOnly); larger plans use
+// shrink_kernel, which computes every rank row of a block per workgroup and
+// streams the d-range through LDS.
 #include <hip/hip_runtime.h>
 
 #include "wp_apply.h"
@@ -794,8 +796,9 @@ __device__ __forceinline__ void reduce_to_h(const ApplyArgs& a, int b, const Blo
 
 // Occupancy target (waves per SIMD), from the registers each variant needs
 // without spilling: the fused kernel holds B and Y across the partials'
-// reduction (two chunks of them in multi-chunk calls); expand() keeps four
-// token tiles in flight; rank 64 and mixed ranks hold twice the B fragments.
+// collection, the multi-slice one also two 16-row shrink tiles; expand()
+// keeps four token tiles in flight; rank 64 and mixed ranks hold twice the B
+// fragments.
 template <int RANK, int ROLE, int TILES>
 constexpr int waves_per_simd() {
   constexpr bool wide = RANK == 0 || RANK == 64;
