@@ -27,6 +27,11 @@
 namespace wp {
 namespace {
 
+// Workgroup barrier for LDS data: waits for this wave's LDS accesses, not
+// for its global stores (a __syncthreads would wait for those to be
+// acknowledged; nothing here reads back what it stored to global memory).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // Exclusive scan of one int per thread across the workgroup.  `scratch` holds
 // NT/64 ints.  Returns the thread's exclusive prefix; *total gets the sum.
 // Begins and ends with a workgroup barrier.
@@ -41,9 +46,9 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* scratch, int* to
     const int y = __shfl_up(x, off, 64);
     if (lane >= off) x += y;
   }
-  __syncthreads();
+  lds_barrier();
   if (lane == 63) scratch[wid] = x;
-  __syncthreads();
+  lds_barrier();
   if (wid == 0) {
     int w = lane < kWaves ? scratch[lane] : 0;
 #pragma unroll
@@ -53,10 +58,10 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* scratch, int* to
     }
     if (lane < kWaves) scratch[lane] = w;
   }
-  __syncthreads();
+  lds_barrier();
   const int base = wid > 0 ? scratch[wid - 1] : 0;
   *total = scratch[kWaves - 1];
-  __syncthreads();
+  lds_barrier();
   return base + x - v;
 }
 
@@ -75,6 +80,15 @@ __device__ __forceinline__ int upper_index(const int* a, int n, int q) {
   return lo;
 }
 
+// Runs sorted by counting (below) when there are at most kRankMax of them and
+// the waves' broadcast reads (keys x keys per thread x waves) stay within
+// kRankWork; past that, a bitonic sort.  Measured on MI355X: 256-token plans
+// 15.8 -> 12.7 us per build_seg_bounds; at 1024 threads the waves' reads
+// queue on the CU's LDS (2048 Zipf-routed tokens: 42 us bitonic, 96 us by
+// counting).
+constexpr int kRankMax = 1024;
+constexpr int kRankWork = 4096;
+
 template <int NT, int E>
 __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, int idx_is_int64, int T,
                                                   uint32_t* __restrict__ header, Segment* __restrict__ segments,
@@ -86,6 +100,7 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
   __shared__ int s_a[CAP + 1];  // run starts, later group adapter ids
   __shared__ int s_b[CAP + 1];  // per-run segment bases, later group offsets
   __shared__ int s_scan[NT / 64];
+  __shared__ unsigned long long s_sorted[kRankMax];  // sorted keys (counting path)
   long long* s_id = reinterpret_cast<long long*>(s_big);
 
   const int tid = threadIdx.x;
@@ -100,7 +115,7 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
     }
     s_id[i] = v;
   }
-  __syncthreads();
+  lds_barrier();
 
   // 2. Run starts in token order (reference :484): s_a[r] = first token of run r.
   bool is_start[E];
@@ -118,7 +133,7 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
     if (is_start[e]) s_a[rb++] = e0 + e;
   }
   if (tid == 0) s_a[n_runs] = T;
-  __syncthreads();
+  lds_barrier();
 
   // 3. Exported table.  Pieces per run: ceil(len/32) when id >= 0 (reference
   //    :485-489); slot bases by exclusive scan in token-start order (:494-503).
@@ -143,7 +158,7 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
     sb += pieces[e];
   }
   if (tid == 0) s_b[n_runs] = n_segs;
-  __syncthreads();
+  lds_barrier();
   const int seg_out = n_segs < seg_cap ? n_segs : seg_cap;
   for (int q = tid; q < seg_out; q += NT) {
     const int r = upper_index(s_b, n_runs, q);
@@ -181,25 +196,44 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
   for (int e = 0; e < E; ++e) {
     if (key[e] != ~0ull) s_big[vb++] = key[e];
   }
-  int P = 1;
-  while (P < n_vruns) P <<= 1;
-  for (int i = n_vruns + tid; i < P; i += NT) s_big[i] = ~0ull;
-  __syncthreads();
-  for (int k = 2; k <= P; k <<= 1) {
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int i = tid; i < P; i += NT) {
-        const int ixj = i ^ j;
-        if (ixj > i) {
-          const unsigned long long a = s_big[i];
-          const unsigned long long b = s_big[ixj];
-          const bool ascending = (i & k) == 0;
-          if ((a > b) == ascending) {
-            s_big[i] = b;
-            s_big[ixj] = a;
+  const unsigned long long* skey = s_big;  // the sorted keys
+  if (n_vruns <= kRankMax && n_vruns * E * (NT / 64) <= kRankWork) {
+    // Keys are distinct (the run index is in them): a key's position is
+    // the number of keys below it.  Every lane reads the same key at once
+    // (an LDS broadcast), with no barrier per step, unlike a bitonic sort's
+    // log^2 rounds (7 of the 16 us of a 256-token plan).
+    lds_barrier();
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      if (key[e] == ~0ull) continue;
+      int below = 0;
+#pragma unroll 8
+      for (int i = 0; i < n_vruns; ++i) below += s_big[i] < key[e] ? 1 : 0;
+      s_sorted[below] = key[e];
+    }
+    lds_barrier();
+    skey = s_sorted;
+  } else {
+    int P = 1;
+    while (P < n_vruns) P <<= 1;
+    for (int i = n_vruns + tid; i < P; i += NT) s_big[i] = ~0ull;
+    lds_barrier();
+    for (int k = 2; k <= P; k <<= 1) {
+      for (int j = k >> 1; j > 0; j >>= 1) {
+        for (int i = tid; i < P; i += NT) {
+          const int ixj = i ^ j;
+          if (ixj > i) {
+            const unsigned long long a = s_big[i];
+            const unsigned long long b = s_big[ixj];
+            const bool ascending = (i & k) == 0;
+            if ((a > b) == ascending) {
+              s_big[i] = b;
+              s_big[ixj] = a;
+            }
           }
         }
+        lds_barrier();
       }
-      __syncthreads();
     }
   }
 
@@ -218,12 +252,12 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
     gid_e[e] = 0;
     gstart[e] = false;
     if (p < n_vruns) {
-      const unsigned long long kk = s_big[p];
+      const unsigned long long kk = skey[p];
       const int r = static_cast<int>(kk & 0xffffffffull);
       start_e[e] = s_a[r];
       len_e[e] = s_a[r + 1] - s_a[r];
       gid_e[e] = static_cast<int>(kk >> 32);
-      gstart[e] = p == 0 || (s_big[p - 1] >> 32) != (kk >> 32);
+      gstart[e] = p == 0 || (skey[p - 1] >> 32) != (kk >> 32);
     }
     lsum += len_e[e];
     gcount += gstart[e] ? 1 : 0;
@@ -243,15 +277,30 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
     }
     ob += len_e[e];
   }
-  __syncthreads();
-  for (int q = tid; q < n_tok; q += NT) {
-    const int p = upper_index(s_roff, n_vruns, q);
-    perm[q] = s_rstart[p] + (q - s_roff[p]);
+  lds_barrier();
+  // perm[q] for q = tid + e*NT, kept in registers until the run tables are
+  // free, then in LDS for the block lists below.
+  int pv[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int q = tid + e * NT;
+    pv[e] = 0;
+    if (q < n_tok) {
+      const int p = upper_index(s_roff, n_vruns, q);
+      pv[e] = s_rstart[p] + (q - s_roff[p]);
+      perm[q] = pv[e];
+    }
   }
 
   // 6. Groups (one per adapter) and their blocks of bt tokens.
   int n_groups = 0;
   int gb = block_exclusive_scan<NT>(gcount, s_scan, &n_groups);  // ends every read of s_roff / s_rstart
+  int* s_perm = reinterpret_cast<int*>(s_big) + CAP;             // [CAP] perm (over s_rstart)
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int q = tid + e * NT;
+    if (q < n_tok) s_perm[q] = pv[e];
+  }
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     if (gstart[e]) {
@@ -261,7 +310,7 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
     }
   }
   if (tid == 0) s_b[n_groups] = n_tok;
-  __syncthreads();
+  lds_barrier();
   int nb[E];
   int bsum = 0;
 #pragma unroll
@@ -279,7 +328,7 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
     if (g < n_groups) s_bbase[g] = bb;
     bb += nb[e];
   }
-  __syncthreads();
+  lds_barrier();
   const int blk_out = n_blocks < block_cap ? n_blocks : block_cap;
   for (int q = tid; q < blk_out; q += NT) {
     const int g = upper_index(s_bbase, n_groups, q);
@@ -292,16 +341,14 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
     b.entry = s_a[g];
     blocks[q] = b;
   }
-  // Block-padded token lists, read back from perm (written above by this
-  // workgroup; the barrier makes those global writes visible to it).
-  __syncthreads();
+  // Block-padded token lists, from the LDS copy of perm.
   for (int u = tid; u < blk_out * bt; u += NT) {
     const int q = u / bt;
     const int j = u - q * bt;
     const int g = upper_index(s_bbase, n_groups, q);
     const int n = s_b[g + 1] - s_b[g];
     const int jj = (q - s_bbase[g]) * bt + j;  // position inside the group
-    if (jj < n) bperm[static_cast<int64_t>(q) * kBlockTokens + j] = perm[s_b[g] + jj];
+    if (jj < n) bperm[static_cast<int64_t>(q) * kBlockTokens + j] = s_perm[s_b[g] + jj];
   }
 
   if (tid == 0) {

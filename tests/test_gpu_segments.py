@@ -67,7 +67,7 @@ def test_default_capacity_and_empty(engine):
 @pytest.mark.parametrize("T", [1, 17, 64, 255, 256, 257, 1000, 2048, 2049, 5000, 8192])
 def test_random_routings_match_oracle(engine, T):
     rng = np.random.default_rng(T)
-    for trial in range(4):
+    for trial in range(5):
         if trial == 0:
             idx = rng.integers(-1, 64, size=T)
         elif trial == 1:  # long runs
@@ -75,8 +75,11 @@ def test_random_routings_match_oracle(engine, T):
         elif trial == 2:  # Zipf-like
             p = 1.0 / np.arange(1, 129) ** 1.1
             idx = rng.choice(128, size=T, p=p / p.sum())
-        else:             # large ids, sorted prefill-like runs
+        elif trial == 3:  # large ids, sorted prefill-like runs
             idx = np.sort(rng.integers(0, 1 << 20, size=T))
+        else:             # a dozen long runs, repeated ids (few runs: the plan's counting sort)
+            cuts = np.sort(rng.choice(np.arange(1, max(T, 2)), size=min(11, max(T - 1, 0)), replace=False))
+            idx = np.repeat(rng.integers(-1, 8, size=len(cuts) + 1), np.diff(np.concatenate([[0], cuts, [T]])))
         announce(f"seg_bounds random T={T} trial={trial}")
         t = torch.from_numpy(idx.astype(np.int64)).cuda()
         assert engine.build_seg_bounds(t)
