@@ -235,3 +235,39 @@ def test_evict_releases_slot():
     b = torch.zeros(O, R, dtype=torch.float16, device="cuda")
     engine.register_adapter(99, a, b, 1.0)
     assert engine.prefetch_adapter(99) >= 0
+
+
+def test_score_policy_keeps_top_adapters_staged():
+    """ScorePrefetchPolicy over host-resident adapters: after each update the
+    top-scored ones are staged and usable, the rest released; a step that
+    routes to the staged set matches the oracle."""
+    from adapterslotsplusplus_amd.prefetch_policy import ScorePrefetchPolicy
+
+    announce("score-driven staging")
+    engine, adapters = make_engine(10, seed=40, host=True)
+    policy = ScorePrefetchPolicy(engine, slots=4)
+    rng = random.Random(5)
+    for it in range(3):
+        scores = {a: rng.random() for a in range(10)}
+        must = [it]
+        policy.update(scores, must=must)
+        want = policy.ranking(scores, must)[:4]
+        assert sorted(policy.staged) == sorted(want)
+        for a in want:
+            assert wait_ready(engine, a)
+        T = 48
+        ids = [want[j % 4] for j in range(T)]
+        X = randn((T, D), 41 + it, torch.float16, 0.1)
+        Y0 = randn((T, O), 51 + it, torch.float16, 0.1)
+        assert engine.build_seg_bounds(torch.tensor(ids, device="cuda"))
+        H = engine.shrink(X.cuda(), D, R, T)
+        Y = Y0.cuda()
+        engine.expand(H, Y, O, R)
+        torch.cuda.synchronize()
+        segs = so.seg_bounds(ids).tolist()
+        H_ref = bgmv.shrink(X, segs, adapters, R, T)
+        assert_close(H, H_ref, f"H update {it}")
+        assert_close(Y, bgmv.expand(H_ref, Y0, segs, adapters), f"Y update {it}")
+        assert engine.device_errors() == 0
+    policy.release_all()
+    assert policy.staged == {}
