@@ -739,10 +739,39 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
     if (threadIdx.x == 0) consumed_prev = atomic_add_u(&a.consumed[b * kCounterStride], 1u);
   }
   if (go) {
-    if constexpr (ROLE == kFusedMulti) {
-      // Chunks after the first load when they are reached: a second set of
-      // B and Y registers (the next chunk loading while one is computed)
-      // costs a wave per SIMD, and measured slower (qkv 19.33 vs 19.08 us).
+    if constexpr (ROLE == kFusedMulti && RANK <= 32) {
+      // Chunks 1 and 2 (the k and v slices of a qkv call) load together
+      // once the partials are in, so their latency is paid once: qkv
+      // 18.55 -> 18.19 us at 4 waves per SIMD, measured on MI355X (holding
+      // them before the collection instead, with 5 waves, was slower).
+      OutChunk<T> cn[2];
+      V8 bfn[2][kOT][KS];
+      YRows yqn[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int oc = p + (j + 1) * n_owg;
+        cn[j].res.ptr = nullptr;
+        if (j + 1 < a.n_sub && oc < a.n_ochunks) {
+          cn[j] = out_chunk<T>(a, blk, oc);
+          if (cn[j].res.err != 0 && p == 0 && threadIdx.x == 0) flag_error(a.plan.header, cn[j].res.err);
+          if (cn[j].res.ptr != nullptr) load_chunk<T, RANK>(a, cn[j], tok0, bfn[j], yqn[j]);
+        }
+      }
+      if (cur.res.ptr != nullptr) compute_chunk<T, RANK, true, 1>(a, b, blk, tok0, cur, bf, yq, s_h, stage);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        if (cn[j].res.ptr != nullptr) compute_chunk<T, RANK, true, 1>(a, b, blk, tok0, cn[j], bfn[j], yqn[j], s_h, stage);
+      for (int i = 3; i < a.n_sub; ++i) {
+        const int oc = p + i * n_owg;
+        if (oc >= a.n_ochunks) break;
+        cur = out_chunk<T>(a, blk, oc);
+        if (cur.res.err != 0 && p == 0 && threadIdx.x == 0) flag_error(a.plan.header, cur.res.err);
+        load_chunk<T, RANK>(a, cur, tok0, bf, yq);
+        if (cur.res.ptr != nullptr) compute_chunk<T, RANK, true, 1>(a, b, blk, tok0, cur, bf, yq, s_h, stage);
+      }
+    } else if constexpr (ROLE == kFusedMulti) {
+      // Rank 64: chunks after the first load when they are reached (its
+      // doubled B fragments leave no room for more sets).
       for (int i = 0; i < a.n_sub; ++i) {
         const int oc = p + i * n_owg;
         if (oc >= a.n_ochunks) break;
@@ -803,7 +832,7 @@ template <int RANK, int ROLE, int TILES>
 constexpr int waves_per_simd() {
   constexpr bool wide = RANK == 0 || RANK == 64;
   if (ROLE == kFused) return wide ? 5 : 7;
-  if (ROLE == kFusedMulti) return wide ? 4 : 5;
+  if (ROLE == kFusedMulti) return 4;
   if (ROLE == kShrinkOnly) return 5;
   if (TILES == 1) return wide ? 5 : 8;
   return wide ? 3 : 5;
