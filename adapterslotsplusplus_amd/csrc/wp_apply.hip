@@ -383,7 +383,7 @@ __device__ __forceinline__ bool wait_partials(const ApplyArgs& a, const Block& b
         if (lane == 0) flag_error(a.plan.header, kErrSpin);
         break;
       }
-      __builtin_amdgcn_s_sleep(8);
+      __builtin_amdgcn_s_sleep(2);
     }
     if (lane == 0) *s_flag = ok;
   }
