@@ -29,13 +29,14 @@ DEVICE_ERR_ID_RANGE = 1
 DEVICE_ERR_UNREGISTERED = 2
 DEVICE_ERR_SHAPE = 4
 DEVICE_ERR_SPIN = 8
+DEVICE_ERR_CAPACITY = 16
 
 # Every entry point include/warppipe_mi355x.h declares.
 EXPORTED = (
     "wp_last_error", "wp_abi_version", "wp_rank_supported", "wp_block_tokens", "wp_create", "wp_destroy",
     "wp_register_adapter", "wp_evict_adapter", "wp_has_adapter", "wp_set_entry_offset", "wp_build_segments",
     "wp_build_seg_bounds", "wp_read_segments", "wp_read_plan", "wp_read_device_errors",
-    "wp_shrink", "wp_expand", "wp_add_lora", "wp_prefetch_adapter", "wp_is_prefetch_ready",
+    "wp_shrink", "wp_expand", "wp_shrink_expand", "wp_add_lora", "wp_prefetch_adapter", "wp_is_prefetch_ready",
     "wp_release_prefetch",
 )
 
@@ -78,6 +79,7 @@ def load():
         "wp_evict_adapter": ([p, i32, p], ctypes.c_int),
         "wp_has_adapter": ([p, i32], ctypes.c_int),
         "wp_set_entry_offset": ([p, i32, i32], ctypes.c_int),
+        "wp_shrink_expand": ([p, p, p, i32, i32, i32, i64, i64, i32, i32, p], ctypes.c_int),
         "wp_build_segments": ([p, p, i32, p, i32, p], ctypes.c_int),
         "wp_build_seg_bounds": ([p, p, i32, i64, p], ctypes.c_int),
         "wp_read_segments": ([p, p, i64, P(i64), p], ctypes.c_int),

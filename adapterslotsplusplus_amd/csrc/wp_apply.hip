@@ -887,10 +887,10 @@ void apply_kernel(const uint32_t* header, const Block* __restrict__ blocks,
   const Block blk = blocks[b];
   const int row = threadIdx.x & 15;
   const int32_t tok0 = bperm[static_cast<int64_t>(b) * kBlockTokens + row];
-  if constexpr (ROLE == kExpandOnly || ROLE == kShrinkOnly) {
-    if (b == a.n_slots - 1 && part == 0 && threadIdx.x == 0 && n_blocks > a.n_slots)
-      flag_error(a.plan.header, kErrCapacity);
-  }
+  // A plan with more blocks than the grid's slots (only routings that name
+  // ids the call cannot resolve produce one) is reported, not silently cut.
+  if (b == a.n_slots - 1 && part == 0 && threadIdx.x == 0 && n_blocks > a.n_slots)
+    flag_error(a.plan.header, kErrCapacity);
   if ((b >= n_blocks) | (blk.count <= 0) | (tok0 < -1)) return;
   const int32_t t0 = row < blk.count ? tok0 : -1;
 
@@ -1150,13 +1150,9 @@ hipError_t launch_rank(const ApplyArgs& a, hipStream_t stream) {
     apply_kernel<T, 0, ROLE, TILES><<<grid, kThreads, 0, stream>>>(WP_APPLY_ARGS);
   } else {
     switch (a.rank) {
-      case 0:  // mixed ranks: registered adapters only, which the fused calls do not take
-        if constexpr (ROLE == kExpandOnly) {
-          apply_kernel<T, 0, ROLE, TILES><<<grid, kThreads, 0, stream>>>(WP_APPLY_ARGS);
-          break;
-        } else {
-          return hipErrorInvalidValue;
-        }
+      case 0:  // mixed ranks (registered adapters): each block's adapter decides
+        apply_kernel<T, 0, ROLE, TILES><<<grid, kThreads, 0, stream>>>(WP_APPLY_ARGS);
+        break;
       case 8: apply_kernel<T, 8, ROLE, TILES><<<grid, kThreads, 0, stream>>>(WP_APPLY_ARGS); break;
       case 16: apply_kernel<T, 16, ROLE, TILES><<<grid, kThreads, 0, stream>>>(WP_APPLY_ARGS); break;
       case 32: apply_kernel<T, 32, ROLE, TILES><<<grid, kThreads, 0, stream>>>(WP_APPLY_ARGS); break;

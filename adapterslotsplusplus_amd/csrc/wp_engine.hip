@@ -1057,6 +1057,66 @@ int wp_add_lora(wp_engine* e, void* y, const void* x, const void* wa, int64_t wa
   return WP_OK;
 }
 
+int wp_shrink_expand(wp_engine* e, const void* X, void* Y, int32_t d_model, int32_t out_features, int32_t rank,
+                     int64_t T, int64_t y_row_stride, int32_t y_col_offset, int32_t dtype, void* stream_) {
+  if (!e) return fail(WP_ERR_INVALID, "shrink_expand: engine is NULL");
+  if (e->plan_kind == 0 || e->plan_T > kSmallPlanTokens) {
+    // Large plans: shrink() into the engine's H, then expand() from it (the
+    // same checks and errors as the two calls).
+    const int64_t hs = rank == 0 ? kMaxRank : rank;
+    int rc = wp_shrink(e, X, e->hbuf, d_model, rank, T, hs, dtype, stream_);
+    if (rc != WP_OK) return rc;
+    return wp_expand(e, e->hbuf, Y, out_features, rank, T, hs, y_row_stride, y_col_offset, dtype, stream_);
+  }
+  if (rank != 0 && !rank_ok(rank)) return fail(WP_ERR_INVALID, "shrink_expand: unsupported rank (only 8/16/32/64)");
+  int rc = check_io("shrink_expand", dtype, X, "X");
+  if (rc != WP_OK) return rc;
+  if (!aligned(Y, 8)) return fail(WP_ERR_INVALID, "shrink_expand: Y must be 8-byte aligned");
+  if (d_model <= 0 || d_model % 8 != 0) return fail(WP_ERR_INVALID, "shrink_expand: d_model must be a positive multiple of 8");
+  if (out_features <= 0 || out_features % 4 != 0)
+    return fail(WP_ERR_INVALID, "shrink_expand: out_features must be a positive multiple of 4");
+  if (y_col_offset < 0 || y_col_offset % 4 != 0 || y_row_stride % 4 != 0 || y_row_stride < y_col_offset + out_features)
+    return fail(WP_ERR_INVALID, "shrink_expand: Y window [%d, %d) does not fit row stride %lld with 4-element alignment",
+                y_col_offset, y_col_offset + out_features, (long long)y_row_stride);
+  if (e->plan_T > T)
+    return fail(WP_ERR_INVALID, "shrink_expand: segments reach token %lld but X has %lld rows", (long long)e->plan_T,
+                (long long)T);
+  if (e->plan_kind == 1) {
+    for (size_t i = 0; i < e->plan_entry_ids.size(); ++i) {
+      const Adapter& ad = e->adapters.at(e->plan_entry_ids[i]);
+      if (ad.d != d_model || ad.o != out_features || (rank != 0 && ad.rank != rank) || ad.dtype != dtype)
+        return fail(WP_ERR_INVALID, "shrink_expand: adapter %d is %d x %d, rank %d; the call is %d x %d, rank %d",
+                    e->plan_entry_ids[i], ad.d, ad.o, ad.rank, d_model, out_features, rank);
+    }
+  }
+  DeviceGuard g(e->device);
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  ApplyArgs a = base_args(e, rank);
+  a.x = X;
+  a.ldx = d_model;
+  a.y = Y;
+  a.ldy = y_row_stride;
+  a.d_model = d_model;
+  uint32_t mask = 0;
+  if ((rc = table_weights(e, stream, &a.w, &mask)) != WP_OK) return rc;
+  const int cols = expand_cols_per_workgroup();
+  a.w.n_slices = 1;
+  a.w.o_size[0] = out_features;
+  a.w.y_off[0] = y_col_offset;
+  a.w.oc_start[0] = 0;
+  a.w.oc_start[1] = static_cast<int32_t>(ceil_div(out_features, cols));
+  a.n_ochunks = a.w.oc_start[1];
+  a.n_sub = static_cast<int>(ceil_div(a.n_ochunks, kExpandWorkgroups));
+  a.n_slots = block_bound(e, static_cast<int64_t>(e->adapters.size()));
+  const int multi = a.n_sub > 1 ? 1 : 0;
+  shrink_split(d_model, rank, multi ? kShrinkRowsFused : kShrinkRows, a.n_slots, ceil_div(a.n_ochunks, a.n_sub),
+               multi ? 0 : static_cast<int64_t>(e->n_cu) * fused_waves_per_simd(rank, multi), &a);
+  WP_HIP(launch_fused(dtype == WP_DTYPE_BF16, a, stream));
+  if (e->plan_kind == 1) record_slot_uses(e, e->plan_entry_slot, stream);
+  else record_mask_uses(e, mask, stream);
+  return WP_OK;
+}
+
 int wp_prefetch_adapter(wp_engine* e, int32_t adapter_id, int32_t* slot_out) {
   if (!e || !slot_out) return fail(WP_ERR_INVALID, "prefetch_adapter: null argument");
   *slot_out = -1;

@@ -274,6 +274,27 @@ class WarpPipeEngine:
         _lib.check(self._lib.wp_expand(self._handle, _ptr(H), _ptr(Y), int(out_features), rank, T, int(H.size(-1)),
                                        int(Y.size(-1)), int(y_offset), dt, self._stream()), "expand")
 
+    def shrink_expand(self, X, Y, out_features, rank, y_offset: int = 0, layer=None):
+        """shrink() then expand() as one call (not in the reference):
+        Y[:, y_offset:y_offset+o] += rn(alpha * X . A^T) . B^T per segment, in
+        place.  Decode-sized plans run in one launch with no H round trip
+        (rank=0: mixed ranks); larger plans run the two halves through the
+        engine's own H."""
+        rank = int(rank or 0)
+        self._on_device(X, "X")
+        self._on_device(Y, "Y")
+        if X.dtype != Y.dtype:
+            raise RuntimeError("X/Y must have the same dtype")
+        dt = _dtype_code(Y, "Y")
+        if not (X.is_contiguous() and Y.is_contiguous()):
+            raise RuntimeError("X/Y must be contiguous")
+        if X.size(0) != Y.size(0):
+            raise RuntimeError("X and Y have different token counts")
+        self._select_layer(layer)
+        _lib.check(self._lib.wp_shrink_expand(self._handle, _ptr(X), _ptr(Y), int(X.size(-1)), int(out_features), rank,
+                                              int(Y.size(0)), int(Y.size(-1)), int(y_offset), dt, self._stream()),
+                   "shrink_expand")
+
     def add_lora_packed(self, y, x, wa_t_all, wb_t_all, scale, y_offset=None, y_slice_size=None) -> bool:
         """y += (scale * x . A[idx]^T) . B[idx]^T for the tokens of the last
         build_seg_bounds table (reference engine.py:56-62, bindings:195-234).

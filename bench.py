@@ -319,9 +319,18 @@ def run_cfg3(args):
         b = wl.algorithmic_bytes(T, d_in, d_out, tr)
         per[name] = {"us_per_call": round(u / len(sel), 2), "bytes_per_call": b,
                      "GB_s": round(b / (u / len(sel) * 1e-6) / 1e9, 1)}
+
+    # The same targets through shrink_expand(): both halves in one launch.
+    def fused_calls():
+        for t in targets:
+            t["eng"].shrink_expand(t["X"], t["Y"], t["d_out"], 0)
+
+    uf, _ = graph_us(fused_calls, max(5, args.steps))
     emit({"workload": f"cfg3: 13B mixed-rank decode, T=512, 128 adapters ({len(touched)} touched), ranks {{8,16,32,64}}, "
                       f"bf16, {n_layers} layers x (gate, up, down), shrink + expand per target",
-          "us_per_layer": round(us / n_layers, 2), "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1), "per_target": per})
+          "us_per_layer": round(us / n_layers, 2), "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1), "per_target": per,
+          "shrink_expand_one_launch": {"us_per_layer": round(uf / n_layers, 2),
+                                       "GB_s": round(nbytes / (uf * 1e-6) / 1e9, 1)}})
 
 
 def run_cfg4(args):

@@ -158,6 +158,16 @@ int wp_shrink(wp_engine* e, const void* X, void* H, int32_t d_model, int32_t ran
 int wp_expand(wp_engine* e, const void* H, void* Y, int32_t out_features, int32_t rank, int64_t T,
               int64_t h_row_stride, int64_t y_row_stride, int32_t y_col_offset, int32_t dtype, void* stream);
 
+/* shrink() followed by expand() over the adapter store, as one call: no
+ * counterpart in the reference (its callers run the two after each other,
+ * bindings:132-148).  Decode-sized plans (at most 512 tokens) run both halves
+ * in one launch with no H round trip (rank = 0: mixed ranks, each adapter's
+ * own); larger plans run shrink then expand through the engine's own H.  Results
+ * match the two calls within the fp tolerance (the d-range split, and so the
+ * fp32 summation order of H, can differ). */
+int wp_shrink_expand(wp_engine* e, const void* X, void* Y, int32_t d_model, int32_t out_features, int32_t rank,
+                     int64_t T, int64_t y_row_stride, int32_t y_col_offset, int32_t dtype, void* stream);
+
 /* Replaces WarpPipeExtension::add_lora_packed (bindings:195-234) and the DSAK
  * kernels (warp_pipe_r32.cu:280-423), generalised to ranks 8/16/32/64, bf16,
  * and n_slices (1..4) output slices sharing one H:

@@ -472,3 +472,49 @@ def test_registered_adapters_large_plan():
     assert_close(H, H_ref, "H")
     assert_close(Y, bgmv.expand(H_ref, Y0, segs, adapters), "Y")
     assert engine.device_errors() == 0
+
+
+@pytest.mark.parametrize("case", ["rank32_device_plan", "rank16_host_plan_window", "mixed", "large_plan"])
+def test_shrink_expand_matches_oracle(case):
+    """shrink_expand(): one launch for decode-sized single-rank plans, shrink +
+    expand through the engine's H otherwise; each against the oracle."""
+    announce(f"shrink_expand {case}")
+    dtype = torch.bfloat16
+    engine = WarpPipeEngine()
+    d, o = 2048, 1536
+    if case == "mixed":
+        rng = np.random.default_rng(8)
+        ranks = [8, 16, 32, 64, 16, 32]
+        ids = [4, 9, 1, 7, 3, 12]
+        adapters = {}
+        for i, (aid, r) in enumerate(zip(ids, ranks)):
+            A = randn((r, d), 300 + i, dtype, 0.02)
+            B = randn((o, r), 310 + i, dtype, 0.02)
+            engine.register_adapter(aid, A.cuda(), B.cuda(), 16.0 / r, rank=r)
+            adapters[aid] = (A, B, 16.0 / r)
+        rank = 0
+    else:
+        rank = 16 if case == "rank16_host_plan_window" else 32
+        ids = [4, 9, 1, 7, 3, 12]
+        adapters = register(engine, 6, rank, d, o, dtype, 320, 0.5, ids=ids)
+    T = 700 if case == "large_plan" else 200
+    X = randn((T, d), 330, dtype)
+    width, off = (o + 256, 128) if case == "rank16_host_plan_window" else (o, 0)
+    Y0 = randn((T, width), 331, dtype)
+    if case == "rank16_host_plan_window":
+        sorted_ids = [1, 3, 4, 7, 9, 12]
+        offsets = [0, 30, 55, 90, 140, 170, 200]
+        engine.build_segments(sorted_ids, offsets)
+        segs = so.segment_table(sorted_ids, offsets).tolist()
+    else:
+        idx = np.random.default_rng(T).choice(ids + [-1], size=T)
+        assert engine.build_seg_bounds(torch.from_numpy(idx).cuda())
+        segs = so.seg_bounds(idx).tolist()
+    Y = Y0.cuda()
+    engine.shrink_expand(X.cuda(), Y, o, rank, y_offset=off)
+    torch.cuda.synchronize()
+    H_ref = bgmv.shrink(X, segs, adapters, rank if rank else 64, T)
+    ref = Y0.clone()
+    ref[:, off:off + o] = bgmv.expand(H_ref, Y0[:, off:off + o].contiguous(), segs, adapters)
+    assert_close(Y, ref, "Y")
+    assert engine.device_errors() == 0
