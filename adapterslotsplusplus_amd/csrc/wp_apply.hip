@@ -843,7 +843,9 @@ template <typename T, int RANK>
 struct alignas(16) SharedMem {
   static constexpr int RR = RANK == 0 ? kMaxRank : RANK;
   static constexpr int kRed = kShrinkRowsFused / 16 * kWaves * 64;    // f32x4
-  static constexpr int kH = (kBlockTokens * (RR + 8) * 2 + 15) / 16;   // f32x4 worth of T
+  // H rows of one block: the fused roles run on plans of 16-token blocks
+  // (launch_fused checks); no other role keeps H in LDS.
+  static constexpr int kH = (16 * (RR + 8) * 2 + 15) / 16;              // f32x4 worth of T
   f32x4 buf[kRed > kH ? kRed : kH];
   T stage[kWaves * 16 * kStageStride];  // each wave's Y tile (expand)
 };
@@ -1187,6 +1189,8 @@ hipError_t launch_fused(int dtype_bf16, const ApplyArgs& a, hipStream_t stream) 
   // The kernels' shrink split is fixed per role; the grid and the readers
   // follow a.srows, so the two must agree.
   if (a.srows != (a.n_sub > 1 ? kShrinkRowsFused : kShrinkRows)) return hipErrorInvalidValue;
+  // The block's H rows live in LDS, sized for blocks of 16 tokens.
+  if (a.tiles != 1) return hipErrorInvalidValue;
   return a.n_sub > 1 ? launch_role<kFusedMulti>(dtype_bf16, a, stream) : launch_role<kFused>(dtype_bf16, a, stream);
 }
 hipError_t launch_shrink(int dtype_bf16, const ApplyArgs& a, hipStream_t stream) {
