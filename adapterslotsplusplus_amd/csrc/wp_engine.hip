@@ -406,6 +406,15 @@ int block_bound(const wp_engine* e, int64_t groups) {
   return static_cast<int>(std::min<int64_t>(T, T / e->plan_bt + g));
 }
 
+// Distinct ids an adapter-store call on a device-built plan can resolve: the
+// registered adapters, and no more than the ids of the selected layer window
+// (wp_set_entry_offset's count), so a multi-layer store is not bounded by
+// every layer's adapters.
+int64_t resolvable_ids(const wp_engine* e) {
+  const int64_t n = static_cast<int64_t>(e->adapters.size());
+  return e->entry_count > 0 ? std::min<int64_t>(n, e->entry_count) : n;
+}
+
 
 }  // namespace
 
@@ -908,7 +917,7 @@ int wp_shrink(wp_engine* e, const void* X, void* H, int32_t d_model, int32_t ran
   uint32_t mask = 0;
   if ((rc = table_weights(e, stream, &a.w, &mask)) != WP_OK) return rc;
   a.w.n_slices = 1;
-  a.n_slots = block_bound(e, static_cast<int64_t>(e->adapters.size()));
+  a.n_slots = block_bound(e, resolvable_ids(e));
   if (e->plan_T <= kSmallPlanTokens) {
     // Decode-sized plans: many small shrink workgroups and a reducer per
     // block (the fused calls' shrink side), not one workgroup per block and
@@ -969,7 +978,7 @@ int wp_expand(wp_engine* e, const void* H, void* Y, int32_t out_features, int32_
   a.w.oc_start[0] = 0;
   a.w.oc_start[1] = static_cast<int32_t>(ceil_div(out_features, cols));
   a.n_ochunks = a.w.oc_start[1];
-  a.n_slots = block_bound(e, static_cast<int64_t>(e->adapters.size()));
+  a.n_slots = block_bound(e, resolvable_ids(e));
   WP_HIP(launch_expand(dtype == WP_DTYPE_BF16, a, stream));
   if (e->plan_kind == 1) record_slot_uses(e, e->plan_entry_slot, stream);
   else record_mask_uses(e, mask, stream);
@@ -1107,7 +1116,7 @@ int wp_shrink_expand(wp_engine* e, const void* X, void* Y, int32_t d_model, int3
   a.w.oc_start[1] = static_cast<int32_t>(ceil_div(out_features, cols));
   a.n_ochunks = a.w.oc_start[1];
   a.n_sub = static_cast<int>(ceil_div(a.n_ochunks, kExpandWorkgroups));
-  a.n_slots = block_bound(e, static_cast<int64_t>(e->adapters.size()));
+  a.n_slots = block_bound(e, resolvable_ids(e));
   const int multi = a.n_sub > 1 ? 1 : 0;
   shrink_split(d_model, rank, multi ? kShrinkRowsFused : kShrinkRows, a.n_slots, ceil_div(a.n_ochunks, a.n_sub),
                multi ? 0 : static_cast<int64_t>(e->n_cu) * fused_waves_per_simd(rank, multi), &a);
