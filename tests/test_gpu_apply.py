@@ -474,15 +474,17 @@ def test_registered_adapters_large_plan():
     assert engine.device_errors() == 0
 
 
-@pytest.mark.parametrize("case", ["rank32_device_plan", "rank16_host_plan_window", "mixed", "large_plan"])
+@pytest.mark.parametrize("case", ["rank32_device_plan", "rank16_host_plan_window", "mixed", "mixed_wide", "large_plan"])
 def test_shrink_expand_matches_oracle(case):
     """shrink_expand(): one launch for decode-sized single-rank plans, shrink +
     expand through the engine's H otherwise; each against the oracle."""
     announce(f"shrink_expand {case}")
     dtype = torch.bfloat16
     engine = WarpPipeEngine()
-    d, o = 2048, 1536
-    if case == "mixed":
+    # mixed_wide: 19 output chunks of 256 (the last one 12 columns), more
+    # than one chunk per expand workgroup.
+    d, o = 2048, (4620 if case == "mixed_wide" else 1536)
+    if case in ("mixed", "mixed_wide"):
         rng = np.random.default_rng(8)
         ranks = [8, 16, 32, 64, 16, 32]
         ids = [4, 9, 1, 7, 3, 12]

@@ -84,7 +84,15 @@ def test_cfg3_mixed_rank_13b(layer):
     segs = so.seg_bounds(idx.numpy()).tolist()
     H_ref = bgmv.shrink(X, segs, adapters, 64, 512)
     assert_close(H, H_ref, f"cfg3 {layer} H")
-    assert_close(Y, bgmv.expand(H_ref, Y0, segs, adapters), f"cfg3 {layer} Y")
+    Y_ref = bgmv.expand(H_ref, Y0, segs, adapters)
+    assert_close(Y, Y_ref, f"cfg3 {layer} Y")
+    assert engine.device_errors() == 0
+    # The same call in one launch (mixed ranks; the gate's 13824 outputs take
+    # the multi-chunk expand workgroups).
+    Y1 = Y0.cuda()
+    engine.shrink_expand(X.cuda(), Y1, d_out, 0)
+    torch.cuda.synchronize()
+    assert_close(Y1, Y_ref, f"cfg3 {layer} Y, one launch")
     assert engine.device_errors() == 0
 
 
