@@ -520,3 +520,50 @@ def test_shrink_expand_matches_oracle(case):
     ref[:, off:off + o] = bgmv.expand(H_ref, Y0[:, off:off + o].contiguous(), segs, adapters)
     assert_close(Y, ref, "Y")
     assert engine.device_errors() == 0
+
+
+def _random_case(seed):
+    """Seeded add_lora shape: T across the 512-token switch between the
+    one-launch and the two-launch paths, 1-3 slices (one of them wider than
+    4096 columns in some cases), every rank, column offsets, runs of -1."""
+    rng = np.random.default_rng(1000 + seed)
+    T = int(rng.choice([1, 3, 16, 17, 100, 255, 256, 300, 511, 512, 513, 640]))
+    d = int(rng.choice([64, 520, 1024, 2056, 4096]))
+    rank = int(rng.choice([8, 16, 32, 64]))
+    L = int(rng.choice([1, 2, 7, 33]))
+    n_sl = int(rng.integers(1, 4))
+    if seed % 5 == 0:
+        widths = [4620]
+    else:
+        widths = [int(rng.integers(1, 1025)) * 4 for _ in range(n_sl)]
+    offs, col = [], int(rng.integers(0, 3)) * 4
+    for w in widths:
+        offs.append(col)
+        col += w + int(rng.integers(0, 3)) * 4
+    # Runs of equal ids (decode batches group by request), some -1.
+    idx = np.repeat(rng.integers(-1, L, size=T), rng.integers(1, 6, size=T))[:T]
+    dtype = DTYPES[seed % 2]
+    scale = float(rng.uniform(0.25, 2.0))
+    return T, d, rank, L, widths, offs, col, idx, dtype, scale
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_add_lora_random_shapes(seed):
+    T, d, rank, L, widths, offs, width, idx, dtype, scale = _random_case(seed)
+    announce(f"random add_lora seed {seed}: T={T} d={d} r={rank} L={L} slices={widths} offs={offs} {dtype}")
+    engine = WarpPipeEngine()
+    wa = randn((L, 1, rank, d), 2000 + seed, dtype, 0.02)
+    wbs = [randn((L, 1, o, rank), 2100 + 7 * seed + i, dtype, 0.02) for i, o in enumerate(widths)]
+    x = randn((T, d), 2200 + seed, dtype)
+    y0 = randn((T, width), 2300 + seed, dtype)
+    assert engine.build_seg_bounds(torch.from_numpy(idx).cuda())
+    y = y0.cuda()
+    if len(widths) == 1:
+        assert engine.add_lora_packed(y, x.cuda(), wa.cuda(), wbs[0].cuda(), scale, y_offset=offs[0],
+                                      y_slice_size=widths[0])
+    else:
+        assert engine.add_lora_slices(y, x.cuda(), wa.cuda(), [w.cuda() for w in wbs], scale, offs)
+    torch.cuda.synchronize()
+    segs = so.seg_bounds(idx).tolist()
+    assert_close(y, bgmv.add_lora(y0, x, wa, wbs, scale, segs, offs), f"seed {seed}")
+    assert engine.device_errors() == 0
