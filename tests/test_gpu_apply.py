@@ -567,3 +567,56 @@ def test_add_lora_random_shapes(seed):
     segs = so.seg_bounds(idx).tolist()
     assert_close(y, bgmv.add_lora(y0, x, wa, wbs, scale, segs, offs), f"seed {seed}")
     assert engine.device_errors() == 0
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_store_random_shapes(seed):
+    """Seeded adapter-store calls: registered adapters of random ranks (mixed,
+    rank=0, on device-built plans; one rank on host-built plans), random ids,
+    T across the 512-token switch; shrink + expand and shrink_expand against
+    the oracle."""
+    rng = np.random.default_rng(3000 + seed)
+    dtype = DTYPES[seed % 2]
+    host_plan = seed % 3 == 0
+    T = int(rng.choice([1, 40, 200, 512, 513, 700]))
+    d = int(rng.choice([64, 1032, 2048]))
+    o = int(rng.integers(1, 1300)) * 4
+    K = int(rng.integers(1, 12))
+    ids = sorted(int(v) for v in rng.choice(200, size=K, replace=False))
+    one_rank = int(rng.choice([8, 16, 32, 64]))
+    ranks = [one_rank] * K if host_plan else [int(rng.choice([8, 16, 32, 64])) for _ in ids]
+    announce(f"random store seed {seed}: T={T} d={d} o={o} K={K} ranks={ranks} host_plan={host_plan} {dtype}")
+    engine = WarpPipeEngine()
+    adapters = {}
+    for i, (aid, r) in enumerate(zip(ids, ranks)):
+        A = randn((r, d), 3100 + 10 * seed + i, dtype, 0.02)
+        B = randn((o, r), 3200 + 10 * seed + i, dtype, 0.02)
+        alpha = float(rng.uniform(0.25, 2.0))
+        engine.register_adapter(aid, A.cuda(), B.cuda(), alpha, rank=r)
+        adapters[aid] = (A, B, alpha)
+    if host_plan:
+        cuts = np.sort(rng.choice(np.arange(1, T), size=min(K - 1, T - 1), replace=False)) if T > 1 else []
+        offsets = [0] + [int(c) for c in cuts] + [T]
+        sorted_ids = ids[: len(offsets) - 1]
+        engine.build_segments(sorted_ids, offsets)
+        segs = so.segment_table(sorted_ids, offsets).tolist()
+        rank = one_rank
+    else:
+        idx = np.repeat(rng.choice(ids + [-1], size=T), rng.integers(1, 9, size=T))[:T]
+        assert engine.build_seg_bounds(torch.from_numpy(idx).cuda())
+        segs = so.seg_bounds(idx).tolist()
+        rank = 0
+    X = randn((T, d), 3300 + seed, dtype)
+    Y0 = randn((T, o), 3400 + seed, dtype)
+    H = engine.shrink(X.cuda(), d, rank, T)
+    Y = Y0.cuda()
+    engine.expand(H, Y, o, rank)
+    Y1 = Y0.cuda()
+    engine.shrink_expand(X.cuda(), Y1, o, rank)
+    torch.cuda.synchronize()
+    H_ref = bgmv.shrink(X, segs, adapters, rank if rank else 64, T)
+    Y_ref = bgmv.expand(H_ref, Y0, segs, adapters)
+    assert_close(H, H_ref, f"seed {seed} H")
+    assert_close(Y, Y_ref, f"seed {seed} Y")
+    assert_close(Y1, Y_ref, f"seed {seed} Y, shrink_expand")
+    assert engine.device_errors() == 0
