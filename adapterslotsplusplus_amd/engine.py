@@ -283,6 +283,8 @@ class WarpPipeEngine:
         rank = int(rank or 0)
         self._on_device(X, "X")
         self._on_device(Y, "Y")
+        if X.dim() != 2 or Y.dim() != 2:
+            raise RuntimeError("shrink_expand: X and Y must be 2-D ([T, d] and [T, width])")
         if X.dtype != Y.dtype:
             raise RuntimeError("X/Y must have the same dtype")
         dt = _dtype_code(Y, "Y")
