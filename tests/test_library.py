@@ -68,6 +68,8 @@ def test_null_engine_arguments_are_errors_not_crashes():
     assert lib.wp_build_seg_bounds(None, None, 1, 4, None) == _lib.WP_ERR_INVALID
     assert lib.wp_shrink(None, None, None, 64, 32, 1, 32, 1, None) == _lib.WP_ERR_INVALID
     assert lib.wp_has_adapter(None, 0) == 0
+    assert lib.wp_shrink_expand(None, None, None, 64, 64, 32, 1, 64, 0, 1, None) == _lib.WP_ERR_INVALID
+    assert lib.wp_set_entry_offset(None, 0, 0) == _lib.WP_ERR_INVALID
     slot = ctypes.c_int32(5)
     assert lib.wp_prefetch_adapter(None, 0, ctypes.byref(slot)) == _lib.WP_ERR_INVALID
     with pytest.raises(RuntimeError, match="engine is NULL"):
