@@ -47,6 +47,13 @@ def _ptr(t: torch.Tensor) -> ctypes.c_void_p:
     return ctypes.c_void_p(t.data_ptr())
 
 
+def _current_raw_stream(device_index: int) -> int:
+    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+    if raw is not None:
+        return int(raw(device_index))
+    return int(torch.cuda.current_stream(device_index).cuda_stream)
+
+
 class _Ext:
     """Stand-in for the reference's `engine._ext` extension object: exposes the
     free functions tests call on it (test_rank_variants.py:97-103)."""
@@ -70,6 +77,8 @@ class WarpPipeEngine:
                 raise RuntimeError("WarpPipeEngine: no GPU available (the apply runs only on the GPU)")
             dev = torch.cuda.current_device()
         self.device = torch.device("cuda", int(dev))
+        self._dev_index = int(dev)
+        self._ranks = {}  # rank -> the library's rank_supported answer
         cfg = _lib.WpConfig(int(dev), int(self.config.num_staging_slots), int(self.config.max_tokens), 64)
         _lib.check(self._lib.wp_create(ctypes.byref(cfg), ctypes.byref(self._handle)), "WarpPipeEngine")
         self._held = {}
@@ -115,12 +124,17 @@ class WarpPipeEngine:
             pass
 
     def _stream(self) -> ctypes.c_void_p:
-        return ctypes.c_void_p(torch.cuda.current_stream(self.device).cuda_stream)
+        # The raw handle of torch's current stream on the engine's device,
+        # without building a torch.cuda.Stream object per call.
+        return ctypes.c_void_p(_current_raw_stream(self._dev_index))
 
     def _on_device(self, t: torch.Tensor, what: str) -> None:
-        if not t.is_cuda:
-            raise RuntimeError(f"{what} must be a CUDA tensor")
-        if t.device != self.device:
+        # get_device() is an int (-1 on the CPU): cheaper per call than
+        # building and comparing torch.device objects.
+        dev = t.get_device()
+        if dev != self._dev_index:
+            if dev < 0:
+                raise RuntimeError(f"{what} must be a CUDA tensor")
             raise RuntimeError(f"{what} is on {t.device}, the engine on {self.device}")
 
     # ------------------------------------------------------- adapter store --
@@ -310,7 +324,10 @@ class WarpPipeEngine:
         """One shrink, several expands: each wb_t_alls[i] ([L, 1, o_i, r]) writes
         columns [y_offsets[i], y_offsets[i] + o_i) of y (packed q/k/v)."""
         rank = int(wb_t_alls[0].size(-1))
-        if not self._ext.rank_supported(rank):
+        ok = self._ranks.get(rank)
+        if ok is None:
+            ok = self._ranks[rank] = bool(self._ext.rank_supported(rank))
+        if not ok:
             return False
         self._on_device(x, "x")
         self._on_device(y, "y")
