@@ -620,3 +620,56 @@ def test_store_random_shapes(seed):
     assert_close(Y, Y_ref, f"seed {seed} Y")
     assert_close(Y1, Y_ref, f"seed {seed} Y, shrink_expand")
     assert engine.device_errors() == 0
+
+
+def test_shrink_expand_graph_replays_with_new_routing():
+    """The adapter-store path in a captured step: build_seg_bounds and a
+    mixed-rank shrink_expand captured once, replayed with other routings
+    copied into the captured index tensor; eager work and synchronisation
+    between the replays, every replay against the oracle."""
+    dtype = torch.bfloat16
+    T, d, o = 48, 1024, 768
+    engine = WarpPipeEngine()
+    ids, ranks = [3, 8, 5, 11], [16, 32, 64, 8]
+    adapters = {}
+    for i, (aid, r) in enumerate(zip(ids, ranks)):
+        A = randn((r, d), 400 + i, dtype, 0.02)
+        B = randn((o, r), 410 + i, dtype, 0.02)
+        engine.register_adapter(aid, A.cuda(), B.cuda(), 16.0 / r, rank=r)
+        adapters[aid] = (A, B, 16.0 / r)
+    X = randn((T, d), 420, dtype)
+    Y0 = randn((T, o), 421, dtype)
+    rng = np.random.default_rng(42)
+    routings = [rng.choice(ids + [-1], size=T) for _ in range(3)]
+    x_d, y0_d = X.cuda(), Y0.cuda()
+    idx_buf = torch.from_numpy(routings[0]).cuda()
+    y_buf = y0_d.clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            assert engine.build_seg_bounds(idx_buf)
+            y_buf.copy_(y0_d)
+            engine.shrink_expand(x_d, y_buf, o, 0)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    announce("shrink_expand graph capture")
+    with torch.cuda.graph(g):
+        engine.build_seg_bounds(idx_buf)
+        engine.shrink_expand(x_d, y_buf, o, 0)
+    torch.cuda.synchronize()
+    refs = []
+    for idx in routings:
+        segs = so.seg_bounds(idx).tolist()
+        refs.append(bgmv.expand(bgmv.shrink(X, segs, adapters, 64, T), Y0, segs, adapters))
+    for it, k in enumerate([1, 2, 0, 1]):
+        announce(f"shrink_expand graph replay {it}")
+        idx_buf.copy_(torch.from_numpy(routings[k]))
+        y_buf.copy_(y0_d)
+        _ = (x_d.float() * 2).sum()  # eager work between replays
+        g.replay()
+        torch.cuda.synchronize()
+        assert_close(y_buf, refs[k], f"replay {it} (routing {k})")
+    assert engine.device_errors() == 0
+    assert not torch.allclose(refs[1].float(), refs[2].float(), rtol=1e-2, atol=1e-3)
