@@ -120,3 +120,49 @@ def test_layer_arguments_are_checked():
     engine.build_segments([1], [0, 4])
     with pytest.raises(RuntimeError, match="build_seg_bounds"):
         engine.shrink(torch.zeros(4, 64, dtype=torch.float16, device="cuda"), 64, 16, 4, layer=3)
+
+
+def test_layers_in_one_captured_step():
+    """One graph holds build_seg_bounds and every layer's shrink_expand; each
+    call's layer offset is recorded with it, so replays with other routings
+    apply each layer's own adapters."""
+    dtype = torch.bfloat16
+    d, o, rank, T = 512, 384, 16, 40
+    engine = WarpPipeEngine(WarpPipeConfig(layer_stride=STRIDE))
+    per_layer = register_layers(engine, rank, d, o, dtype, 950)
+    X = randn((T, d), 960, dtype)
+    Y0 = randn((T, o), 961, dtype)
+    rng = np.random.default_rng(9)
+    routings = [rng.integers(-1, K, size=T) for _ in range(2)]
+    x_d, y0_d = X.cuda(), Y0.cuda()
+    idx_buf = torch.from_numpy(routings[0]).cuda()
+    ys = [y0_d.clone() for _ in range(LAYERS)]
+
+    def step():
+        engine.build_seg_bounds(idx_buf)
+        for lay in range(LAYERS):
+            engine.shrink_expand(x_d, ys[lay], o, rank, layer=lay)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    announce("layers graph capture")
+    with torch.cuda.graph(g):
+        step()
+    torch.cuda.synchronize()
+    for it, k in enumerate([1, 0, 1]):
+        announce(f"layers graph replay {it}")
+        idx_buf.copy_(torch.from_numpy(routings[k]))
+        for y in ys:
+            y.copy_(y0_d)
+        g.replay()
+        torch.cuda.synchronize()
+        segs = so.seg_bounds(routings[k]).tolist()
+        for lay in range(LAYERS):
+            ref = bgmv.expand(bgmv.shrink(X, segs, per_layer[lay], rank, T), Y0, segs, per_layer[lay])
+            assert_close(ys[lay], ref, f"replay {it} layer {lay}")
+    assert engine.device_errors() == 0
