@@ -673,3 +673,25 @@ def test_shrink_expand_graph_replays_with_new_routing():
         assert_close(y_buf, refs[k], f"replay {it} (routing {k})")
     assert engine.device_errors() == 0
     assert not torch.allclose(refs[1].float(), refs[2].float(), rtol=1e-2, atol=1e-3)
+
+
+def test_shrink_expand_shape_errors():
+    """A call whose out_features do not match the registered adapters: raised
+    on a host-built table (checked when enqueued); on a device-built plan the
+    blocks are skipped, Y is left as it was and the shape bit (4) is set."""
+    dtype = torch.float16
+    engine = WarpPipeEngine()
+    register(engine, 2, 16, 256, 512, dtype, 500, 1.0, ids=[1, 2])
+    X = randn((32, 256), 501, dtype).cuda()
+    Y = randn((32, 256), 502, dtype).cuda()
+    engine.build_segments([1, 2], [0, 10, 32])
+    with pytest.raises(RuntimeError, match="shrink_expand"):
+        engine.shrink_expand(X, Y, 256, 16)
+    assert engine.build_seg_bounds(torch.tensor([1] * 16 + [2] * 16).cuda())
+    before = Y.clone()
+    engine.shrink_expand(X, Y, 256, 16)
+    torch.cuda.synchronize()
+    assert torch.equal(Y, before)
+    assert engine.device_errors() & 4
+    with pytest.raises(RuntimeError, match="2-D"):
+        engine.shrink_expand(X.view(2, 16, 256), Y, 256, 16)
