@@ -55,6 +55,10 @@ hipError_t launch_shrink_small(int dtype_bf16, const ApplyArgs& a, hipStream_t s
 // expand(): expand from a caller-provided token-indexed H.
 hipError_t launch_expand(int dtype_bf16, const ApplyArgs& a, hipStream_t stream);
 
+// Sets n 32-bit words at p to v (vector stores; a kernel, so that a caller
+// may capture it in a graph).
+hipError_t launch_fill_u32(uint32_t* p, uint32_t v, size_t n, hipStream_t stream);
+
 // Output columns one expand workgroup produces.
 int expand_cols_per_workgroup();
 // Waves per SIMD the fused kernel for `rank` (0: mixed) runs at, single- or

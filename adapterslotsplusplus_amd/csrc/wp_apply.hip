@@ -50,6 +50,8 @@
 // streams the d-range through LDS.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "wp_apply.h"
 
 namespace wp {
@@ -1176,7 +1178,19 @@ hipError_t launch_role(int dtype_bf16, const ApplyArgs& a, hipStream_t stream) {
   return dtype_bf16 ? launch_rank<__bf16, ROLE, 1>(a, stream) : launch_rank<_Float16, ROLE, 1>(a, stream);
 }
 
+__global__ __launch_bounds__(kThreads) void fill_u32_kernel(uint32_t* __restrict__ p, uint32_t v, size_t n) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * kThreads;
+  for (size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; i < n; i += stride) p[i] = v;
+}
+
 }  // namespace
+
+hipError_t launch_fill_u32(uint32_t* p, uint32_t v, size_t n, hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  const size_t blocks = std::min<size_t>((n + kThreads - 1) / kThreads, 2048);
+  fill_u32_kernel<<<static_cast<unsigned>(blocks), kThreads, 0, stream>>>(p, v, n);
+  return hipGetLastError();
+}
 
 int expand_cols_per_workgroup() { return kOC; }
 int fused_waves_per_simd(int rank, int multi) {

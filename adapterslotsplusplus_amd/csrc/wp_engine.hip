@@ -691,6 +691,11 @@ int wp_build_segments(wp_engine* e, const int32_t* ids, int32_t K, const int32_t
   for (auto& r : ranges) n_tok += r.second;
   if (n_tok > e->tok_cap)
     return fail(WP_ERR_CAPACITY, "build_segments: %lld tokens exceed max_tokens %d", (long long)n_tok, e->tok_cap);
+  // Large-plan calls keep H in the engine's [max_tokens, 64] buffer by token
+  // row, so the last token row bounds the table as much as the token count.
+  if (max_end > e->tok_cap)
+    return fail(WP_ERR_CAPACITY, "build_segments: segments reach token %lld, beyond max_tokens %d",
+                (long long)max_end, e->tok_cap);
 
   // Wait until the previous upload left the pinned buffer.
   int rc = wait_event_host(e->upload_done, &e->upload_pending);
@@ -880,6 +885,76 @@ int table_weights(wp_engine* e, hipStream_t stream, Weights* w, uint32_t* mask) 
   return WP_OK;
 }
 
+// Validates an add_lora call on stacked weights (vLLM's wa_t_all /
+// wb_t_all) and fills the launch fields that do not depend on the plan or on
+// where the scratch buffers live.  WP_NOT_HANDLED for a rank without kernels
+// (reference: add_lora_packed returns False, bindings:197-198).
+int stacked_call_args(const char* who, void* y, const void* x, const void* wa, int64_t wa_stride0, int32_t num_loras,
+                      int32_t n_slices, const void* const* wb, const int64_t* wb_stride0, const int32_t* out_features,
+                      const int32_t* y_col_offsets, float scale, int32_t rank, int32_t d_model, int64_t y_row_stride,
+                      int32_t dtype, ApplyArgs* a) {
+  if (!rank_ok(rank)) return WP_NOT_HANDLED;
+  int rc = check_io(who, dtype, x, "x");
+  if (rc != WP_OK) return rc;
+  if ((rc = check_io(who, dtype, wa, "wa_t_all")) != WP_OK) return rc;
+  if (!y || !aligned(y, 8)) return fail(WP_ERR_INVALID, "%s: y must be 8-byte aligned", who);
+  if (d_model <= 0 || d_model % 8 != 0) return fail(WP_ERR_INVALID, "%s: d_model must be a positive multiple of 8", who);
+  if (num_loras <= 0) return fail(WP_ERR_INVALID, "%s: num_loras must be positive", who);
+  if (n_slices < 1 || n_slices > kMaxSlices || !wb || !wb_stride0 || !out_features || !y_col_offsets)
+    return fail(WP_ERR_INVALID, "%s: 1..%d output slices with their weights, strides, widths and offsets", who,
+                kMaxSlices);
+  if (wa_stride0 % 8 != 0) return fail(WP_ERR_INVALID, "%s: wa_t_all stride must be a multiple of 8", who);
+  if (y_row_stride % 4 != 0) return fail(WP_ERR_INVALID, "%s: y row stride must be a multiple of 4", who);
+  for (int s = 0; s < n_slices; ++s) {
+    if ((rc = check_io(who, dtype, wb[s], "wb_t_all")) != WP_OK) return rc;
+    if (wb_stride0[s] % 8 != 0) return fail(WP_ERR_INVALID, "%s: wb_t_all stride must be a multiple of 8", who);
+    if (out_features[s] <= 0 || out_features[s] % 4 != 0 || y_col_offsets[s] < 0 || y_col_offsets[s] % 4 != 0 ||
+        y_col_offsets[s] + out_features[s] > y_row_stride)
+      return fail(WP_ERR_INVALID, "%s: slice %d window [%d, %d) does not fit y (row stride %lld, 4-aligned)", who, s,
+                  y_col_offsets[s], y_col_offsets[s] + out_features[s], (long long)y_row_stride);
+  }
+  a->rank = rank;
+  a->n_sub = 1;
+  a->hs = rank;
+  a->x = x;
+  a->ldx = d_model;
+  a->y = y;
+  a->ldy = y_row_stride;
+  a->d_model = d_model;
+  a->w.mode = kStacked;
+  a->w.num_ids = num_loras;
+  a->w.a_base = wa;
+  a->w.a_stride = wa_stride0;
+  a->w.scale = scale;
+  a->w.n_slices = n_slices;
+  const int cols = expand_cols_per_workgroup();
+  int oc = 0;
+  for (int s = 0; s < n_slices; ++s) {
+    a->w.b_base[s] = wb[s];
+    a->w.b_stride[s] = wb_stride0[s];
+    a->w.o_size[s] = out_features[s];
+    a->w.y_off[s] = y_col_offsets[s];
+    a->w.oc_start[s] = oc;
+    oc += static_cast<int>(ceil_div(out_features[s], cols));
+  }
+  a->w.oc_start[n_slices] = oc;
+  a->n_ochunks = oc;
+  return WP_OK;
+}
+
+// Work split of a fused call (a->n_slots, the output chunks and the rank set):
+// about kExpandWorkgroups expand workgroups per block -- wider outputs (several
+// slices) give each workgroup several chunks, so that the block's partials are
+// summed fewer times -- and the shrink side in 32-row groups for those
+// multi-chunk calls (half the shrink workgroups, so more of the expand side is
+// resident from the start), 16-row groups otherwise.
+void fused_split(ApplyArgs* a, int rank, int d_model, int n_cu) {
+  a->n_sub = static_cast<int>(ceil_div(a->n_ochunks, kExpandWorkgroups));
+  const int multi = a->n_sub > 1 ? 1 : 0;
+  shrink_split(d_model, rank, multi ? kShrinkRowsFused : kShrinkRows, a->n_slots, ceil_div(a->n_ochunks, a->n_sub),
+               multi ? 0 : static_cast<int64_t>(n_cu) * fused_waves_per_simd(rank, multi), a);
+}
+
 }  // namespace
 
 int wp_shrink(wp_engine* e, const void* X, void* H, int32_t d_model, int32_t rank, int64_t T, int64_t h_row_stride,
@@ -990,69 +1065,26 @@ int wp_add_lora(wp_engine* e, void* y, const void* x, const void* wa, int64_t wa
                 const int32_t* y_col_offsets, float scale, int32_t rank, int32_t d_model, int64_t T,
                 int64_t y_row_stride, int32_t dtype, void* stream_) {
   if (!e) return fail(WP_ERR_INVALID, "add_lora: engine is NULL");
-  // Reference: add_lora_packed returns False for ranks its kernels lack (bindings:197-198).
-  if (!rank_ok(rank)) return WP_NOT_HANDLED;
-  int rc = check_io("add_lora", dtype, x, "x");
+  ApplyArgs a{};
+  int rc = stacked_call_args("add_lora", y, x, wa, wa_stride0, num_loras, n_slices, wb, wb_stride0, out_features,
+                             y_col_offsets, scale, rank, d_model, y_row_stride, dtype, &a);
   if (rc != WP_OK) return rc;
-  if ((rc = check_io("add_lora", dtype, wa, "wa_t_all")) != WP_OK) return rc;
-  if (!aligned(y, 8)) return fail(WP_ERR_INVALID, "add_lora: y must be 8-byte aligned");
-  if (d_model <= 0 || d_model % 8 != 0) return fail(WP_ERR_INVALID, "add_lora: d_model must be a positive multiple of 8");
-  if (num_loras <= 0) return fail(WP_ERR_INVALID, "add_lora: num_loras must be positive");
-  if (n_slices < 1 || n_slices > kMaxSlices) return fail(WP_ERR_INVALID, "add_lora: 1..%d output slices", kMaxSlices);
-  if (wa_stride0 % 8 != 0) return fail(WP_ERR_INVALID, "add_lora: wa_t_all stride must be a multiple of 8");
-  for (int s = 0; s < n_slices; ++s) {
-    if ((rc = check_io("add_lora", dtype, wb[s], "wb_t_all")) != WP_OK) return rc;
-    if (wb_stride0[s] % 8 != 0) return fail(WP_ERR_INVALID, "add_lora: wb_t_all stride must be a multiple of 8");
-    if (out_features[s] <= 0 || out_features[s] % 4 != 0 || y_col_offsets[s] < 0 || y_col_offsets[s] % 4 != 0 ||
-        y_col_offsets[s] + out_features[s] > y_row_stride)
-      return fail(WP_ERR_INVALID, "add_lora: slice %d window [%d, %d) does not fit y (row stride %lld, 4-aligned)", s,
-                  y_col_offsets[s], y_col_offsets[s] + out_features[s], (long long)y_row_stride);
-  }
-  if (y_row_stride % 4 != 0) return fail(WP_ERR_INVALID, "add_lora: y row stride must be a multiple of 4");
   if (e->plan_kind == 0) return fail(WP_ERR_STATE, "add_lora: no segment table (call build_seg_bounds first)");
   if (e->plan_T > T) return fail(WP_ERR_INVALID, "add_lora: segments reach token %lld but x has %lld rows", (long long)e->plan_T, (long long)T);
   DeviceGuard g(e->device);
   hipStream_t stream = static_cast<hipStream_t>(stream_);
-
-  ApplyArgs a = base_args(e, rank);
-  a.x = x;
-  a.ldx = d_model;
-  a.y = y;
-  a.ldy = y_row_stride;
-  a.d_model = d_model;
-  a.w.mode = kStacked;
-  a.w.num_ids = num_loras;
-  a.w.a_base = wa;
-  a.w.a_stride = wa_stride0;
-  a.w.scale = scale;
-  a.w.n_slices = n_slices;
-  const int cols = expand_cols_per_workgroup();
-  int oc = 0;
-  for (int s = 0; s < n_slices; ++s) {
-    a.w.b_base[s] = wb[s];
-    a.w.b_stride[s] = wb_stride0[s];
-    a.w.o_size[s] = out_features[s];
-    a.w.y_off[s] = y_col_offsets[s];
-    a.w.oc_start[s] = oc;
-    oc += static_cast<int>(ceil_div(out_features[s], cols));
-  }
-  a.w.oc_start[n_slices] = oc;
-  a.n_ochunks = oc;
-  // About kExpandWorkgroups expand workgroups per block; wider outputs (several
-  // slices) give each workgroup several chunks, so that the partials of the
-  // block are summed fewer times.
-  a.n_sub = static_cast<int>(ceil_div(oc, kExpandWorkgroups));
+  a.tiles = (e->plan_bt + 15) / 16;
+  a.ptok = e->tok_cap;
+  a.part = e->part;
+  a.consumed = e->consumed;
+  a.plan = plan_view(e);
   a.n_slots = block_bound(e, num_loras);
-  // Multi-chunk calls split the shrink in 32-row groups: half the shrink
-  // workgroups, so more of their expand workgroups are resident from the
-  // start.
-  const int multi = a.n_sub > 1 ? 1 : 0;
-  shrink_split(d_model, rank, multi ? kShrinkRowsFused : kShrinkRows, a.n_slots, ceil_div(oc, a.n_sub),
-               multi ? 0 : static_cast<int64_t>(e->n_cu) * fused_waves_per_simd(rank, multi), &a);
+  fused_split(&a, rank, d_model, e->n_cu);
   if (e->plan_bt > 16) {
     // Large plans (prefill-sized, 64-token blocks): shrink into the engine's
     // H, then expand from it.  Each launch keeps several token tiles in
     // flight per workgroup; the kernel boundary replaces the in-kernel wait.
+    if (e->plan_T > e->tok_cap) return fail(WP_ERR_CAPACITY, "add_lora: table reaches past the engine's H rows");
     a.h = e->hbuf;
     a.ldh = a.hs;
     a.n_sub = 1;
@@ -1115,11 +1147,8 @@ int wp_shrink_expand(wp_engine* e, const void* X, void* Y, int32_t d_model, int3
   a.w.oc_start[0] = 0;
   a.w.oc_start[1] = static_cast<int32_t>(ceil_div(out_features, cols));
   a.n_ochunks = a.w.oc_start[1];
-  a.n_sub = static_cast<int>(ceil_div(a.n_ochunks, kExpandWorkgroups));
   a.n_slots = block_bound(e, resolvable_ids(e));
-  const int multi = a.n_sub > 1 ? 1 : 0;
-  shrink_split(d_model, rank, multi ? kShrinkRowsFused : kShrinkRows, a.n_slots, ceil_div(a.n_ochunks, a.n_sub),
-               multi ? 0 : static_cast<int64_t>(e->n_cu) * fused_waves_per_simd(rank, multi), &a);
+  fused_split(&a, rank, d_model, e->n_cu);
   WP_HIP(launch_fused(dtype == WP_DTYPE_BF16, a, stream));
   if (e->plan_kind == 1) record_slot_uses(e, e->plan_entry_slot, stream);
   else record_mask_uses(e, mask, stream);

@@ -283,7 +283,13 @@ class WarpPipeEngine:
         dt = _dtype_code(Y, "Y")
         if not (H.is_contiguous() and Y.is_contiguous()):
             raise RuntimeError("H/Y must be contiguous")
+        if H.dim() != 2 or Y.dim() != 2:
+            raise RuntimeError("expand: H and Y must be 2-D ([T, rank] and [T, width])")
         T = int(Y.size(0))
+        # The library checks the table against Y's rows; H is read at the same
+        # token rows, so it needs at least as many.
+        if int(H.size(0)) < T:
+            raise RuntimeError(f"expand: H has {int(H.size(0))} rows, Y has {T}")
         self._select_layer(layer)
         _lib.check(self._lib.wp_expand(self._handle, _ptr(H), _ptr(Y), int(out_features), rank, T, int(H.size(-1)),
                                        int(Y.size(-1)), int(y_offset), dt, self._stream()), "expand")

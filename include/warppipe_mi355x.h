@@ -103,7 +103,7 @@ int wp_evict_adapter(wp_engine* e, int32_t adapter_id, void* stream);
 int wp_has_adapter(wp_engine* e, int32_t adapter_id);
 
 /* Multi-layer adapter store (no counterpart in the reference, whose store
- * holds one (A, B) per id, csrc/bridge/adapter_store.h:12-19): a layer's
+ * holds one (A, B) per id, csrc/memory/adapter_store.h:12-19): a layer's
  * adapters are registered under ids offset by layer * stride.  After this
  * call, the per-token ids of a build_seg_bounds plan select the adapters
  * registered under offset + id in the shrink / expand calls that
