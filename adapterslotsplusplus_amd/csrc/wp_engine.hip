@@ -27,6 +27,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <unordered_map>
 #include <vector>
@@ -1152,6 +1153,124 @@ int wp_shrink_expand(wp_engine* e, const void* X, void* Y, int32_t d_model, int3
   WP_HIP(launch_fused(dtype == WP_DTYPE_BF16, a, stream));
   if (e->plan_kind == 1) record_slot_uses(e, e->plan_entry_slot, stream);
   else record_mask_uses(e, mask, stream);
+  return WP_OK;
+}
+
+}  // extern "C"
+
+// ============================================================================
+// No-allocation entry point: build_seg_bounds + add_lora in one call, with the
+// plan, the fp32 partials and the per-block counters in this library's static
+// device array `scratch` (each GPU holds its own copy until the process ends).
+// ============================================================================
+
+namespace {
+
+constexpr size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+// Tokens per call: the reference's build_seg_bounds limit (bindings:165-166).
+constexpr int kStaticTokens = kRefMaxSegments;
+// Segments and blocks each hold at least one token.
+constexpr int kStaticSegCap = kStaticTokens;
+constexpr int kStaticBlockCap = kStaticTokens;
+constexpr size_t kSOffHdr = 0;
+constexpr size_t kSOffSeg = align256(kSOffHdr + sizeof(uint32_t) * kHdrWords);
+constexpr size_t kSOffBlk = align256(kSOffSeg + sizeof(Segment) * kStaticSegCap);
+constexpr size_t kSOffPerm = align256(kSOffBlk + sizeof(Block) * kStaticBlockCap);
+constexpr size_t kSOffBperm = align256(kSOffPerm + sizeof(int32_t) * kStaticTokens);
+constexpr size_t kSOffCons = align256(kSOffBperm + sizeof(int32_t) * kStaticBlockCap * kBlockTokens);
+constexpr size_t kSOffPart = align256(kSOffCons + sizeof(uint32_t) * kStaticBlockCap * kCounterStride);
+constexpr size_t kStaticBytes = align256(kSOffPart + sizeof(float) * kMaxChunks * kStaticTokens * kMaxRank);
+static_assert(kStaticBytes == WP_STATIC_SCRATCH_BYTES, "WP_STATIC_SCRATCH_BYTES in the C header");
+
+}  // namespace
+
+// In host code this name is a host-side stand-in, not the device address:
+// host code uses the per-device pointer from hipGetSymbolAddress only.
+static __device__ __align__(256) unsigned char scratch[kStaticBytes];
+
+namespace {
+
+constexpr int kStaticMaxDevices = 64;
+
+struct StaticDevice {
+  char* ptr = nullptr;  // this device's copy of `scratch`
+  int n_cu = 256;
+};
+
+std::mutex g_static_mu;
+StaticDevice g_static[kStaticMaxDevices];
+
+// The current device's scratch, set up on its first use: the symbol's device
+// address, then the counters and plan header cleared and the partials filled
+// with kPartialEmpty (the state every call leaves behind), synchronously.
+int static_scratch(int dev, hipStream_t stream, StaticDevice** out) {
+  std::lock_guard<std::mutex> lock(g_static_mu);
+  StaticDevice& sd = g_static[dev];
+  if (sd.ptr == nullptr) {
+    if (stream_capturing(stream))
+      return fail(WP_ERR_STATE, "add_lora_static: the first call on a device sets up its scratch and cannot be "
+                                "captured; call it once before capturing");
+    void* p = nullptr;
+    WP_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    char* base = static_cast<char*>(p);
+    WP_HIP(launch_fill_u32(reinterpret_cast<uint32_t*>(base), 0u, kSOffPart / 4, stream));
+    WP_HIP(launch_fill_u32(reinterpret_cast<uint32_t*>(base + kSOffPart), kPartialEmpty, (kStaticBytes - kSOffPart) / 4,
+                           stream));
+    WP_HIP(hipStreamSynchronize(stream));
+    int n_cu = 0;
+    if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n_cu > 0)
+      sd.n_cu = n_cu;
+    sd.ptr = base;
+  }
+  *out = &sd;
+  return WP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int wp_add_lora_static(void* y, const void* x, const void* idx, int32_t idx_is_int64, int64_t T, const void* wa,
+                       int64_t wa_stride0, int32_t num_loras, int32_t n_slices, const void* const* wb,
+                       const int64_t* wb_stride0, const int32_t* out_features, const int32_t* y_col_offsets,
+                       float scale, int32_t rank, int32_t d_model, int64_t y_row_stride, int32_t dtype,
+                       void* stream_) {
+  ApplyArgs a{};
+  int rc = stacked_call_args("add_lora_static", y, x, wa, wa_stride0, num_loras, n_slices, wb, wb_stride0,
+                             out_features, y_col_offsets, scale, rank, d_model, y_row_stride, dtype, &a);
+  if (rc != WP_OK) return rc;
+  if (T < 0) return fail(WP_ERR_INVALID, "add_lora_static: negative token count");
+  if (T > kStaticTokens)
+    return fail(WP_ERR_CAPACITY, "add_lora_static: %lld tokens exceed the static scratch's %d", (long long)T,
+                kStaticTokens);
+  if (T == 0) return WP_OK;
+  if (!idx) return fail(WP_ERR_INVALID, "add_lora_static: null indices");
+  int dev = 0;
+  WP_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kStaticMaxDevices) return fail(WP_ERR_NO_DEVICE, "add_lora_static: device %d out of range", dev);
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  StaticDevice* sd = nullptr;
+  if ((rc = static_scratch(dev, stream, &sd)) != WP_OK) return rc;
+  char* base = sd->ptr;
+  PlanView v;
+  v.header = reinterpret_cast<uint32_t*>(base + kSOffHdr);
+  v.segments = reinterpret_cast<const Segment*>(base + kSOffSeg);
+  v.blocks = reinterpret_cast<const Block*>(base + kSOffBlk);
+  v.perm = reinterpret_cast<const int32_t*>(base + kSOffPerm);
+  v.bperm = reinterpret_cast<const int32_t*>(base + kSOffBperm);
+  const int bt = plan_block_tokens(T);
+  WP_HIP(launch_plan(idx, idx_is_int64 ? 1 : 0, static_cast<int>(T), v.header, reinterpret_cast<Segment*>(base + kSOffSeg),
+                     reinterpret_cast<Block*>(base + kSOffBlk), reinterpret_cast<int32_t*>(base + kSOffPerm),
+                     reinterpret_cast<int32_t*>(base + kSOffBperm), kStaticSegCap, kStaticBlockCap, bt, stream));
+  a.tiles = 1;
+  a.ptok = kStaticTokens;
+  a.part = reinterpret_cast<float*>(base + kSOffPart);
+  a.consumed = reinterpret_cast<uint32_t*>(base + kSOffCons);
+  a.plan = v;
+  // Blocks: sum over adapters of ceil(n / 16) <= T / 16 + adapters, and <= T.
+  a.n_slots = static_cast<int>(std::min<int64_t>(T, T / bt + std::min<int64_t>(num_loras, T)));
+  fused_split(&a, rank, d_model, sd->n_cu);
+  WP_HIP(launch_fused(dtype == WP_DTYPE_BF16, a, stream));
   return WP_OK;
 }
 

@@ -180,6 +180,25 @@ int wp_add_lora(wp_engine* e, void* y, const void* x, const void* wa, int64_t wa
                 const int32_t* y_col_offsets, float scale, int32_t rank, int32_t d_model, int64_t T,
                 int64_t y_row_stride, int32_t dtype, void* stream);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops or harnesses that forbid
+ * hipMalloc): wp_build_seg_bounds followed by wp_add_lora as one call, with no
+ * engine.  The step plan, the fp32 partials and the per-block counters live in
+ * a static device array of this library, WP_STATIC_SCRATCH_BYTES per GPU, held
+ * until the process ends; the call allocates and frees nothing.  Arguments and
+ * results are wp_add_lora's on a table built from idx (T token -> adapter ids,
+ * int64 if idx_is_int64, else int32).  Limits: T <= 256 (WP_ERR_CAPACITY
+ * above), rank 8/16/32/64 (WP_NOT_HANDLED otherwise), 1..4 slices.  The first
+ * call on a device sets its scratch up synchronously and must not be under
+ * graph capture; later calls enqueue two kernels on `stream` and may be
+ * captured.  Every call on a GPU shares that GPU's scratch: calls that overlap
+ * (other streams, other threads) race and must be serialised by the caller. */
+#define WP_STATIC_SCRATCH_BYTES 1189120
+int wp_add_lora_static(void* y, const void* x, const void* idx, int32_t idx_is_int64, int64_t T, const void* wa,
+                       int64_t wa_stride0, int32_t num_loras, int32_t n_slices, const void* const* wb,
+                       const int64_t* wb_stride0, const int32_t* out_features, const int32_t* y_col_offsets,
+                       float scale, int32_t rank, int32_t d_model, int64_t y_row_stride, int32_t dtype, void* stream);
+
 /* ---- staging / prefetch ---------------------------------------------------- */
 
 /* Replaces WarpPipeExtension::prefetch_adapter (bindings:46-57): copies the
