@@ -112,3 +112,17 @@ def test_host_table_known_answers(engine, golden_dir):
         engine.build_segments([9999], [0, 4])
     for i in range(257):
         engine.evict_adapter(i)
+
+
+def test_host_table_past_max_tokens_is_rejected():
+    """A host table whose token rows reach past max_tokens is refused before
+    any launch: large-plan calls index the engine's H scratch by token row."""
+    announce("build_segments past max_tokens")
+    eng = WarpPipeEngine(WarpPipeConfig(max_tokens=256))
+    A = torch.zeros(32, 64, dtype=torch.float16, device="cuda")
+    B = torch.zeros(64, 32, dtype=torch.float16, device="cuda")
+    eng.register_adapter(0, A, B, 1.0, rank=32)
+    with pytest.raises(RuntimeError, match="beyond max_tokens"):
+        eng.build_segments([0], [500, 600])
+    eng.build_segments([0], [200, 256])
+    assert eng.read_segments() == [(0, 200, 56)]
