@@ -27,3 +27,7 @@ class WarpPipeConfig:
     # shrink / expand(..., layer=l) on a build_seg_bounds table apply layer
     # l's weights to each token's adapter id.  0: one layer, plain ids.
     layer_stride: int = 0
+    # Size of the device adapter table: ids (layer * layer_stride + id with a
+    # multi-layer store) in [0, max_adapter_ids) are usable with
+    # build_seg_bounds tables; others through build_segments only.
+    max_adapter_ids: int = 65536

@@ -30,14 +30,38 @@ struct ApplyArgs {
   float* part;        // fp32 partial H by plan position: [n_chunks][ptok][hs], kPartialEmpty between calls
   uint32_t* consumed; // per block (stride kCounterStride): fused calls count expand workgroups done reading,
                       // shrink() counts d-range workgroups done; zero between calls
+  uint32_t spin_limit; // polls before a wait on partials gives up (kDefaultSpinLimit)
   PlanView plan;
   Weights w;
 };
 
+// Bound of a wait on partials: polls of ~1 us each, so about 0.1 s.
+constexpr uint32_t kDefaultSpinLimit = 1u << 17;
+
 // Builds the step plan from token_lora_indices (wp_plan.hip).
-// Blocks hold at most bt (<= kBlockTokens) tokens.
+// Blocks hold at most bt (<= kBlockTokens) tokens.  The same launch first
+// does what `m` asks (publications into the adapter table; the partial
+// buffer's repair after a give-up); m may be null.
 hipError_t launch_plan(const void* idx, int idx_is_int64, int T, uint32_t* header, Segment* segments, Block* blocks,
-                       int32_t* perm, int32_t* bperm, int seg_cap, int block_cap, int bt, hipStream_t stream);
+                       int32_t* perm, int32_t* bperm, int seg_cap, int block_cap, int bt, const Maint* m,
+                       hipStream_t stream);
+// The plan build's maintenance alone (one workgroup), for eager calls that
+// run between plan builds.
+hipError_t launch_maintain(uint32_t* header, const Maint& m, hipStream_t stream);
+
+// Tiny writes of adapter-table entries and of one slot publication, in stream
+// order (one wave): pub (if not null) gets (pub_id, pub_entry) under its
+// sequence lock, then dst[i] = val[i] for i < n.
+constexpr int kMaxEntryWrites = 4;
+struct EntryWrites {
+  int32_t n;
+  int32_t pub_id;
+  SlotPub* pub;
+  Entry pub_entry;
+  Entry* dst[kMaxEntryWrites];
+  Entry val[kMaxEntryWrites];
+};
+hipError_t launch_entry_writes(const EntryWrites& w, hipStream_t stream);
 
 // shrink(): a workgroup streams its d-range (a.dc, a multiple of
 // kShrinkSlices * 128 columns) in groups of kShrinkSlices 128-column slices.

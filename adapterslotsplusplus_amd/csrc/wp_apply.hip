@@ -92,8 +92,6 @@ constexpr int kShrinkKSteps = 4;        // 32-wide K-steps per wave per load bat
 // large plans); the fused kernel, which decode-sized plans use, works one
 // tile at a time to keep its registers for occupancy.
 constexpr int kTilesInFlight = kBlockTokens / 16;
-// Bound of the partials wait: polls of ~1 us each, so about 0.1 s.
-constexpr unsigned kSpinLimit = 1u << 17;
 constexpr int kShrinkWavesPerSimd = 4;
 
 // kFusedMulti: fused, with several output chunks per expand workgroup.
@@ -184,6 +182,17 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 
 __device__ __forceinline__ void flag_error(uint32_t* header, uint32_t bits) { atomicOr(&header[kHdrErrors], bits); }
 
+// A wait on partials that reached its bound: flagged (kErrSpin), and the
+// partial buffer marked poisoned (kHdrPoison).  A shrink workgroup that was
+// late may yet write its partial after the block's readers emptied the
+// buffer, so later calls skip their work until the next plan build has
+// refilled the buffer (nothing reads such a word as data).
+__device__ __forceinline__ void give_up(uint32_t* header) {
+  flag_error(header, kErrSpin);
+  atomic_store_u(&header[kHdrPoison], 1u);
+}
+__device__ __forceinline__ bool poisoned(const uint32_t* header) { return atomic_load_u(&header[kHdrPoison]) != 0u; }
+
 // A block's weights as the kernels see them.
 // The adapter-table entry as two 16-byte loads (field by field, with a test
 // between, the compiler issued three dependent loads).
@@ -194,11 +203,20 @@ __device__ __forceinline__ Entry load_entry(const Entry* p) {
   e.a_ptr = static_cast<uint64_t>(lo[0]) | (static_cast<uint64_t>(lo[1]) << 32);
   e.b_ptr = static_cast<uint64_t>(lo[2]) | (static_cast<uint64_t>(lo[3]) << 32);
   e.alpha = __builtin_bit_cast(float, hi[0]);
-  e.rank = static_cast<int32_t>(hi[1]);
+  e.rank_dtype = static_cast<int32_t>(hi[1]);
   e.d_model = static_cast<int32_t>(hi[2]);
   e.out_features = static_cast<int32_t>(hi[3]);
   return e;
 }
+
+// wp_dtype code of the kernels' element type (adapter-table entries carry
+// the dtype their weights were registered with).
+template <typename T>
+constexpr int32_t dtype_code();
+template <>
+constexpr int32_t dtype_code<_Float16>() { return 0; }
+template <>
+constexpr int32_t dtype_code<__bf16>() { return 1; }
 
 template <typename T>
 struct Resolved {
@@ -226,18 +244,19 @@ __device__ __forceinline__ Resolved<T> resolve_a(const ApplyArgs& a, const Block
     return r;
   }
   const Entry en = load_entry(a.w.entries + blk.entry);
+  const int32_t rank = entry_rank(en.rank_dtype);
   // One test over both halves, so that both loads go out before the wait.
-  if ((en.a_ptr == 0) | (en.b_ptr == 0) | (en.rank <= 0)) {
+  if ((en.a_ptr == 0) | (en.b_ptr == 0) | (rank <= 0)) {
     r.err = kErrUnregistered;
     return r;
   }
-  if (en.d_model != a.d_model || (a.rank != 0 && en.rank != a.rank)) {
+  if (en.d_model != a.d_model || (a.rank != 0 && rank != a.rank) || entry_dtype(en.rank_dtype) != dtype_code<T>()) {
     r.err = kErrShape;
     return r;
   }
   r.ptr = reinterpret_cast<const T*>(en.a_ptr);
   r.alpha = en.alpha;
-  r.rank = en.rank;
+  r.rank = rank;
   return r;
 }
 
@@ -259,19 +278,20 @@ __device__ __forceinline__ Resolved<T> resolve_b(const ApplyArgs& a, const Block
     return r;
   }
   const Entry en = load_entry(a.w.entries + blk.entry);
+  const int32_t rank = entry_rank(en.rank_dtype);
   // One test over both halves, so that both loads go out before the wait.
-  if ((en.a_ptr == 0) | (en.b_ptr == 0) | (en.rank <= 0)) {
+  if ((en.a_ptr == 0) | (en.b_ptr == 0) | (rank <= 0)) {
     r.err = kErrUnregistered;
     return r;
   }
-  if (en.out_features != a.w.o_size[0] || (a.rank != 0 && en.rank != a.rank) ||
-      (a.d_model != 0 && en.d_model != a.d_model)) {
+  if (en.out_features != a.w.o_size[0] || (a.rank != 0 && rank != a.rank) ||
+      (a.d_model != 0 && en.d_model != a.d_model) || entry_dtype(en.rank_dtype) != dtype_code<T>()) {
     r.err = kErrShape;
     return r;
   }
   r.ptr = reinterpret_cast<const T*>(en.b_ptr);
   r.alpha = en.alpha;
-  r.rank = en.rank;
+  r.rank = rank;
   return r;
 }
 
@@ -377,14 +397,16 @@ __device__ __forceinline__ bool wait_partials(const ApplyArgs& a, const Block& b
     }
     int ok = 1;
     for (unsigned spins = 0;; ++spins) {
+      // Both tests are uniform over the wave.  After the bound, or once
+      // another wait of the call gave up, the block is abandoned.
+      if (spins >= a.spin_limit || (spins > 0 && poisoned(a.plan.header))) {
+        ok = 0;
+        if (lane == 0 && spins >= a.spin_limit) give_up(a.plan.header);
+        break;
+      }
       const bool here = probe == nullptr || !is_empty(__builtin_bit_cast(float, atomic_load_u(
                                                 reinterpret_cast<const uint32_t*>(probe))));
       if (__all(here)) break;
-      if (spins >= kSpinLimit) {
-        ok = 0;
-        if (lane == 0) flag_error(a.plan.header, kErrSpin);
-        break;
-      }
       __builtin_amdgcn_s_sleep(2);
     }
     if (lane == 0) *s_flag = ok;
@@ -418,6 +440,12 @@ __device__ __forceinline__ void collect_partials(const ApplyArgs& a, const Block
     for (int c0 = 0; c0 < nch; c0 += CB) {
       f32x2 v[CB];
       for (unsigned spins = 0;; ++spins) {
+        if (spins >= a.spin_limit || (spins > 0 && poisoned(a.plan.header))) {
+          if (spins >= a.spin_limit) give_up(a.plan.header);
+#pragma unroll
+          for (int i = 0; i < CB; ++i) v[i] = f32x2{0.f, 0.f};
+          break;
+        }
         bool missing = false;
 #pragma unroll
         for (int i = 0; i < CB; ++i) {
@@ -427,10 +455,6 @@ __device__ __forceinline__ void collect_partials(const ApplyArgs& a, const Block
 #pragma unroll
         for (int i = 0; i < CB; ++i) missing = missing || is_empty(v[i][0]) || is_empty(v[i][1]);
         if (!missing) break;
-        if (spins >= kSpinLimit) {
-          flag_error(a.plan.header, kErrSpin);
-          break;
-        }
         __builtin_amdgcn_s_sleep(2);
       }
 #pragma unroll
@@ -453,11 +477,12 @@ __device__ __forceinline__ void await_partials(const ApplyArgs& a, const Block& 
     const int j = q / r4;
     const int r0 = (q - j * r4) * 4;
     const float* p = a.part + (static_cast<int64_t>(c) * a.ptok + blk.first + j) * a.hs + r0;
-    for (unsigned spins = 0; any_empty(coherent_load_f4(p)); ++spins) {
-      if (spins >= kSpinLimit) {
-        flag_error(a.plan.header, kErrSpin);
+    for (unsigned spins = 0;; ++spins) {
+      if (spins >= a.spin_limit || (spins > 0 && poisoned(a.plan.header))) {
+        if (spins >= a.spin_limit) give_up(a.plan.header);
         break;
       }
+      if (!any_empty(coherent_load_f4(p))) break;
       __builtin_amdgcn_s_sleep(4);
     }
   }
@@ -888,6 +913,8 @@ void apply_kernel(const uint32_t* header, const Block* __restrict__ blocks,
   // tested on the count alone, the compiler would load the descriptor and the
   // token only after the count had arrived.
   const int n_blocks = static_cast<int>(header[kHdrNumBlocks]);
+  // Roles that use the partial buffer do nothing while it is poisoned.
+  const uint32_t poison = ROLE == kExpandOnly ? 0u : header[kHdrPoison];
   const Block blk = blocks[b];
   const int row = threadIdx.x & 15;
   const int32_t tok0 = bperm[static_cast<int64_t>(b) * kBlockTokens + row];
@@ -895,7 +922,7 @@ void apply_kernel(const uint32_t* header, const Block* __restrict__ blocks,
   // ids the call cannot resolve produce one) is reported, not silently cut.
   if (b == a.n_slots - 1 && part == 0 && threadIdx.x == 0 && n_blocks > a.n_slots)
     flag_error(a.plan.header, kErrCapacity);
-  if ((b >= n_blocks) | (blk.count <= 0) | (tok0 < -1)) return;
+  if ((b >= n_blocks) | (blk.count <= 0) | (tok0 < -1) | (poison != 0u)) return;
   const int32_t t0 = row < blk.count ? tok0 : -1;
 
   if (shrink_role) {

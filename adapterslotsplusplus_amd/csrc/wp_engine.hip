@@ -77,23 +77,30 @@ inline bool rank_ok(int r) { return r == 8 || r == 16 || r == 32 || r == 64; }
 struct Adapter {
   int32_t rank = 0, d = 0, o = 0, dtype = 0;
   float alpha = 0.f;
-  void* dA = nullptr;  // device copies (pool)
+  void* dA = nullptr;    // device copies (pool)
   void* dB = nullptr;
-  void* hA = nullptr;  // pinned host copies (host-resident adapters)
+  void* host = nullptr;  // host-resident adapters: one pinned allocation, A then B
+  void* hA = nullptr;
   void* hB = nullptr;
   size_t a_bytes = 0, b_bytes = 0;
   hipEvent_t copied = nullptr;  // recorded after the registration copy
 };
 
+// A staging slot.  Kernels reach its buffers only through the adapter table:
+// once the copy has landed, the prefetch stream publishes the slot's entry
+// (SlotPub); the next plan build -- or an eager call that finds the slot ready
+// -- writes it into the table; a release writes the adapter's registered
+// entry back on the caller's stream, and the slot's next copy waits for that.
 struct Slot {
   int32_t adapter = -1;
   void* A = nullptr;
   void* B = nullptr;
   size_t cap_a = 0, cap_b = 0;
-  hipEvent_t ready = nullptr;     // prefetch stream, after the copy
-  hipEvent_t last_use = nullptr;  // compute stream, after kernels that read the slot
+  hipEvent_t ready = nullptr;     // prefetch stream: copy and publication done
+  hipEvent_t released = nullptr;  // caller's stream: the registered entry is back
   bool issued = false;
-  bool used = false;
+  bool release_pending = false;   // `released` recorded and not yet waited for by a copy
+  bool applied = false;           // an eager call has enqueued the table write of the publication
 };
 
 // Expand workgroups per block a fused call aims for.
@@ -157,6 +164,15 @@ inline void shrink_range_split(int d, ApplyArgs* a) {
 
 }  // namespace
 
+// Pinned upload buffers of host-built plans, used in turn: a plan upload
+// waits (on the host) only for the one issued kUploadRing builds before it.
+constexpr int kUploadRing = 4;
+// Adapter-table size when the configuration gives none.
+constexpr int32_t kDefaultTableIds = 1 << 16;
+constexpr int32_t kMaxTableIds = 1 << 22;
+// Staging slots an engine may have (publications are applied by one thread each).
+constexpr int kMaxStagingSlots = 256;
+
 struct wp_engine {
   int device = 0;
   wp_config cfg{};
@@ -164,6 +180,9 @@ struct wp_engine {
   hipMemPool_t pool = nullptr;
   std::unordered_map<int32_t, Adapter> adapters;
   std::vector<Slot> slots;
+  // Pinned host copies of evicted adapters, freed once the prefetch stream
+  // has passed the recorded event (a copy may still read them).
+  std::vector<std::pair<void*, hipEvent_t>> host_graveyard;
 
   // Workspace (one allocation).
   char* ws = nullptr;
@@ -172,33 +191,27 @@ struct wp_engine {
   Block* blocks = nullptr;
   int32_t* perm = nullptr;
   int32_t* bperm = nullptr;     // [block_cap][kBlockTokens]
-  uint32_t* consumed = nullptr; // [block_cap]
+  uint32_t* consumed = nullptr; // [block_cap][kCounterStride]
   Entry* plan_entries = nullptr;
-  float* part = nullptr;        // [kMaxChunks][tok_cap][kMaxRank] fp32 partial H of fused calls (kPartialEmpty between calls)
-  float* spart = nullptr;       // same shape, d-range partials of shrink() launches (no invariant between calls)
+  float* part = nullptr;        // [kMaxChunks][ptok][kMaxRank] fp32 partial H of fused calls (kPartialEmpty between calls)
+  float* spart = nullptr;       // [kMaxChunks][tok_cap][kMaxRank] d-range partials of shrink() launches (no invariant)
   void* hbuf = nullptr;         // [tok_cap][kMaxRank] 2-byte H of large-plan add_lora calls
+  SlotPub* pubs = nullptr;      // [num_staging_slots] staging publications
+  Entry* dtable = nullptr;      // [table_cap] id-indexed adapter table of build_seg_bounds plans
+  int table_cap = 0;
   int seg_cap = 0, block_cap = 0, tok_cap = 0, entry_cap = 0;
+  int ptok = 0;                 // plan positions of `part`: fused calls run on plans of <= kSmallPlanTokens
+  uint64_t part_words = 0, consumed_words = 0;
   int n_cu = 256;  // compute units of the device
   int32_t entry_offset = 0;  // table-mode calls on device-built plans read dtable + entry_offset
   int32_t entry_count = 0;   // ... and at most this many entries (0: to the table's end)
+  uint32_t spin_limit = kDefaultSpinLimit;
 
-  // Id-indexed adapter table for table-mode kernels on device-built plans.
-  Entry* dtable = nullptr;
-  int dtable_cap = 0;
-  std::vector<Entry> htable;
-  bool table_dirty = true;
-  uint32_t table_staged_mask = 0;
-  char* pinned_table = nullptr;
-  size_t pinned_table_bytes = 0;
-  hipEvent_t table_done = nullptr;
-  bool table_done_pending = false;
-
-  // Pinned upload buffer for host-built plans.
-  char* pinned = nullptr;
+  char* pinned[kUploadRing] = {};
+  hipEvent_t upload_done[kUploadRing] = {};
+  bool upload_pending[kUploadRing] = {};
+  int upload_next = 0;
   size_t pinned_bytes = 0;
-  hipEvent_t upload_done = nullptr;
-  bool upload_pending = false;
-  uint32_t* pinned_zero = nullptr;
 
   // Host view of the current plan.
   int plan_kind = 0;          // 0 none, 1 host-built (build_segments), 2 device-built (build_seg_bounds)
@@ -226,88 +239,90 @@ bool stream_capturing(hipStream_t s) {
   return st != hipStreamCaptureStatusNone;
 }
 
-int wait_event_host(hipEvent_t ev, bool* pending) {
-  if (*pending) {
-    WP_HIP(hipEventSynchronize(ev));
-    *pending = false;
-  }
-  return WP_OK;
-}
-
-Entry entry_for(const wp_engine* e, int32_t id, const Adapter& ad, int* slot_used) {
+// The adapter's table entry as registered: its device copies, or no weights
+// (a host-resident adapter is usable only through a staging slot).
+Entry registered_entry(const Adapter& ad) {
   Entry en{};
+  en.a_ptr = reinterpret_cast<uint64_t>(ad.dA);
+  en.b_ptr = reinterpret_cast<uint64_t>(ad.dB);
   en.alpha = ad.alpha;
-  en.rank = ad.rank;
+  en.rank_dtype = pack_rank_dtype(ad.rank, ad.dtype);
   en.d_model = ad.d;
   en.out_features = ad.o;
-  *slot_used = -1;
-  const int s = find_slot(e, id);
-  if (s >= 0 && slot_ready(e->slots[s])) {
-    en.a_ptr = reinterpret_cast<uint64_t>(e->slots[s].A);
-    en.b_ptr = reinterpret_cast<uint64_t>(e->slots[s].B);
-    *slot_used = s;
-  } else {
-    en.a_ptr = reinterpret_cast<uint64_t>(ad.dA);
-    en.b_ptr = reinterpret_cast<uint64_t>(ad.dB);
-  }
   return en;
 }
 
-// Refreshes the device adapter table (stream-ordered) when registrations or
-// staging readiness changed.  Returns the staged-slot mask in use.
-int sync_table(wp_engine* e, hipStream_t stream, uint32_t* mask_out) {
-  if (stream_capturing(stream)) {
-    // Event queries are not allowed while a graph is being captured: the
-    // table must already be current (the uncaptured warm-up call made it so).
-    *mask_out = e->table_staged_mask;
-    if (e->table_dirty)
-      return fail(WP_ERR_STATE, "adapter table changed before graph capture; run the call once before capturing");
-    return WP_OK;
+Entry staged_entry(const Adapter& ad, const Slot& sl) {
+  Entry en = registered_entry(ad);
+  en.a_ptr = reinterpret_cast<uint64_t>(sl.A);
+  en.b_ptr = reinterpret_cast<uint64_t>(sl.B);
+  return en;
+}
+
+// Entry of a host-built plan: the staged copy once its slot is ready, else
+// the registered one.
+Entry entry_for(const wp_engine* e, int32_t id, const Adapter& ad, int* slot_used) {
+  *slot_used = -1;
+  const int s = find_slot(e, id);
+  if (s >= 0 && slot_ready(e->slots[s])) {
+    *slot_used = s;
+    return staged_entry(ad, e->slots[s]);
   }
-  uint32_t mask = 0;
-  for (size_t i = 0; i < e->slots.size(); ++i)
-    if (slot_ready(e->slots[i]) && e->adapters.count(e->slots[i].adapter)) mask |= 1u << i;
-  *mask_out = mask;
-  if (!e->table_dirty && mask == e->table_staged_mask) return WP_OK;
-  if (e->dtable_cap == 0) return WP_OK;
-  std::fill(e->htable.begin(), e->htable.end(), Entry{});
-  for (const auto& kv : e->adapters) {
-    if (kv.first < 0 || kv.first >= e->dtable_cap) continue;
-    int su = -1;
-    e->htable[kv.first] = entry_for(e, kv.first, kv.second, &su);
-  }
-  const size_t bytes = sizeof(Entry) * static_cast<size_t>(e->dtable_cap);
-  int rc = wait_event_host(e->table_done, &e->table_done_pending);
-  if (rc != WP_OK) return rc;
-  if (e->pinned_table_bytes < bytes) {
-    if (e->pinned_table) WP_HIP(hipHostFree(e->pinned_table));
-    e->pinned_table = nullptr;
-    WP_HIP(hipHostMalloc(reinterpret_cast<void**>(&e->pinned_table), bytes, hipHostMallocDefault));
-    e->pinned_table_bytes = bytes;
-  }
-  std::memcpy(e->pinned_table, e->htable.data(), bytes);
-  WP_HIP(hipMemcpyAsync(e->dtable, e->pinned_table, bytes, hipMemcpyHostToDevice, stream));
-  WP_HIP(hipEventRecord(e->table_done, stream));
-  e->table_done_pending = true;
-  e->table_dirty = false;
-  e->table_staged_mask = mask;
+  return registered_entry(ad);
+}
+
+Maint maint_view(const wp_engine* e) {
+  Maint m{};
+  m.part = e->part;
+  m.part_words = e->part_words;
+  m.consumed = e->consumed;
+  m.consumed_words = e->consumed_words;
+  m.pubs = e->pubs;
+  m.n_pubs = static_cast<int32_t>(e->slots.size());
+  m.table_cap = e->table_cap;
+  m.table = e->dtable;
+  return m;
+}
+
+// Table entry `id` = en, in stream order (ids outside the table are reached
+// through build_segments tables only).
+int table_write(wp_engine* e, int32_t id, const Entry& en, hipStream_t stream) {
+  if (id < 0 || id >= e->table_cap) return WP_OK;
+  EntryWrites w{};
+  w.n = 1;
+  w.dst[0] = e->dtable + id;
+  w.val[0] = en;
+  WP_HIP(launch_entry_writes(w, stream));
   return WP_OK;
 }
 
-int grow_table(wp_engine* e, int32_t id, hipStream_t stream) {
-  if (id < 0 || id < e->dtable_cap) return WP_OK;
-  constexpr int32_t kMaxTableIds = 1 << 20;
-  if (id >= kMaxTableIds) return WP_OK;  // usable through build_segments only
-  int cap = std::max(256, e->dtable_cap);
-  while (cap <= id) cap *= 2;
-  Entry* nt = nullptr;
-  WP_HIP(hipMallocFromPoolAsync(reinterpret_cast<void**>(&nt), sizeof(Entry) * cap, e->pool, stream));
-  if (e->dtable) WP_HIP(hipFreeAsync(e->dtable, stream));
-  e->dtable = nt;
-  e->dtable_cap = cap;
-  e->htable.assign(cap, Entry{});
-  e->table_dirty = true;
+// Eager calls on a build_seg_bounds plan: a slot whose copy has landed since
+// the plan was built is written into the table before the call (the plan
+// build writes every ready publication, so captured steps need no such launch).
+int apply_ready_slots(wp_engine* e, hipStream_t stream) {
+  bool any = false;
+  for (auto& sl : e->slots)
+    if (sl.issued && !sl.applied && hipEventQuery(sl.ready) == hipSuccess) {
+      sl.applied = true;
+      any = true;
+    }
+  if (any) WP_HIP(launch_maintain(e->header, maint_view(e), stream));
   return WP_OK;
+}
+
+void sweep_graveyard(wp_engine* e, bool wait) {
+  for (size_t i = 0; i < e->host_graveyard.size();) {
+    auto& g = e->host_graveyard[i];
+    if (wait || hipEventQuery(g.second) == hipSuccess) {
+      if (wait) (void)hipEventSynchronize(g.second);
+      (void)hipHostFree(g.first);
+      (void)hipEventDestroy(g.second);
+      g = e->host_graveyard.back();
+      e->host_graveyard.pop_back();
+    } else {
+      ++i;
+    }
+  }
 }
 
 void invalidate_host_plan_for(wp_engine* e, int32_t id) {
@@ -319,52 +334,67 @@ void invalidate_host_plan_for(wp_engine* e, int32_t id) {
     }
 }
 
-int release_slot(wp_engine* e, int s) {
+// Frees slot s, on `stream`: once its copy has landed, the publication is
+// emptied and the adapter's registered entry written back into the table and
+// into the current host-built plan, so kernels enqueued after this never read
+// the slot; `released` marks that point for the slot's next copy.  Kernels
+// enqueued before it on `stream` (graph replays included) finish first.
+int release_slot_on(wp_engine* e, int s, hipStream_t stream) {
   if (s < 0) return WP_OK;
-  e->slots[s].adapter = -1;
-  e->slots[s].issued = false;
-  e->table_dirty = true;
+  Slot& sl = e->slots[s];
+  if (sl.adapter < 0) return WP_OK;
+  if (sl.issued) WP_HIP(hipStreamWaitEvent(stream, sl.ready, 0));
+  EntryWrites w{};
+  w.pub = e->pubs + s;
+  w.pub_id = -1;
+  Entry reg{};
+  auto it = e->adapters.find(sl.adapter);
+  if (it != e->adapters.end()) reg = registered_entry(it->second);
+  if (sl.adapter < e->table_cap) {
+    w.dst[w.n] = e->dtable + sl.adapter;
+    w.val[w.n++] = reg;
+  }
+  if (e->plan_kind == 1)
+    for (size_t k = 0; k < e->plan_entry_slot.size(); ++k)
+      if (e->plan_entry_slot[k] == s) {
+        // A slot holds one adapter, which a host-built plan lists once.
+        if (w.n < kMaxEntryWrites) {
+          w.dst[w.n] = e->plan_entries + k;
+          w.val[w.n++] = reg;
+        }
+        e->plan_entry_slot[k] = -1;
+      }
+  WP_HIP(launch_entry_writes(w, stream));
+  WP_HIP(hipEventRecord(sl.released, stream));
+  sl.release_pending = true;
+  sl.adapter = -1;
+  sl.issued = false;
+  sl.applied = false;
   return WP_OK;
 }
 
 int evict_impl(wp_engine* e, int32_t id, hipStream_t stream) {
   auto it = e->adapters.find(id);
   if (it == e->adapters.end()) return WP_OK;
+  int rc = release_slot_on(e, find_slot(e, id), stream);
+  if (rc != WP_OK) return rc;
   Adapter& ad = it->second;
-  const int s = find_slot(e, id);
-  if (s >= 0) {
-    // The slot copy may still read the pinned host copy.
-    if (e->slots[s].issued) WP_HIP(hipEventSynchronize(e->slots[s].ready));
-    release_slot(e, s);
-  }
+  // Kernels enqueued from here on find no weights for the id; those enqueued
+  // before finish before the stream-ordered frees.
+  if ((rc = table_write(e, id, Entry{}, stream)) != WP_OK) return rc;
   if (ad.dA) WP_HIP(hipFreeAsync(ad.dA, stream));
   if (ad.dB) WP_HIP(hipFreeAsync(ad.dB, stream));
-  if (ad.hA) WP_HIP(hipHostFree(ad.hA));
-  if (ad.hB) WP_HIP(hipHostFree(ad.hB));
+  if (ad.host) {
+    hipEvent_t ev = nullptr;
+    WP_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+    WP_HIP(hipEventRecord(ev, e->pstream));
+    e->host_graveyard.emplace_back(ad.host, ev);
+  }
   if (ad.copied) WP_HIP(hipEventDestroy(ad.copied));
   e->adapters.erase(it);
-  if (id >= 0 && id < e->dtable_cap) e->table_dirty = true;
   invalidate_host_plan_for(e, id);
+  sweep_graveyard(e, false);
   return WP_OK;
-}
-
-// Slot reads are tracked for eager launches; inside a graph capture an event
-// record would become a graph node, so staged slots must not be recycled
-// while such a graph is still replayed.
-void record_slot_uses(wp_engine* e, const std::vector<int>& slot_ids, hipStream_t stream) {
-  if (stream_capturing(stream)) return;
-  for (int s : slot_ids) {
-    if (s < 0) continue;
-    if (hipEventRecord(e->slots[s].last_use, stream) == hipSuccess) e->slots[s].used = true;
-  }
-}
-
-void record_mask_uses(wp_engine* e, uint32_t mask, hipStream_t stream) {
-  if (stream_capturing(stream)) return;
-  for (size_t i = 0; i < e->slots.size(); ++i)
-    if (mask & (1u << i)) {
-      if (hipEventRecord(e->slots[i].last_use, stream) == hipSuccess) e->slots[i].used = true;
-    }
 }
 
 PlanView plan_view(const wp_engine* e) {
@@ -384,9 +414,10 @@ ApplyArgs base_args(const wp_engine* e, int rank) {
   a.n_sub = 1;
   a.tiles = (e->plan_bt + 15) / 16;
   a.hs = rank == 0 ? kMaxRank : rank;
-  a.ptok = e->tok_cap;
+  a.ptok = e->ptok;
   a.part = e->part;
   a.consumed = e->consumed;
+  a.spin_limit = e->spin_limit;
   a.plan = plan_view(e);
   return a;
 }
@@ -441,11 +472,15 @@ int wp_create(const wp_config* cfg_in, wp_engine** out) {
   cfg.num_staging_slots = 8;
   cfg.max_tokens = kPlanMaxTokens;
   cfg.max_rank = kMaxRank;
+  cfg.max_adapter_ids = kDefaultTableIds;
   if (cfg_in) cfg = *cfg_in;
+  if (cfg.max_adapter_ids == 0) cfg.max_adapter_ids = kDefaultTableIds;
   if (cfg.max_tokens <= 0 || cfg.max_tokens > kPlanMaxTokens)
     return fail(WP_ERR_INVALID, "wp_create: max_tokens must be in [1, %d]", kPlanMaxTokens);
-  if (cfg.num_staging_slots < 0 || cfg.num_staging_slots > 32)
-    return fail(WP_ERR_INVALID, "wp_create: num_staging_slots must be in [0, 32]");
+  if (cfg.num_staging_slots < 0 || cfg.num_staging_slots > kMaxStagingSlots)
+    return fail(WP_ERR_INVALID, "wp_create: num_staging_slots must be in [0, %d]", kMaxStagingSlots);
+  if (cfg.max_adapter_ids < 0 || cfg.max_adapter_ids > kMaxTableIds)
+    return fail(WP_ERR_INVALID, "wp_create: max_adapter_ids must be in [0, %d]", kMaxTableIds);
   int ndev = 0;
   const hipError_t ce = hipGetDeviceCount(&ndev);
   if (ce != hipSuccess || ndev <= 0)
@@ -478,6 +513,10 @@ int wp_create(const wp_config* cfg_in, wp_engine** out) {
   e->seg_cap = std::max(cfg.max_tokens, kRefMaxSegments);
   e->block_cap = cfg.max_tokens + kRefMaxSegments;
   e->entry_cap = kRefMaxSegments;
+  e->table_cap = cfg.max_adapter_ids;
+  e->ptok = std::min(cfg.max_tokens, kSmallPlanTokens);
+  e->part_words = static_cast<uint64_t>(kMaxChunks) * e->ptok * kMaxRank;
+  e->consumed_words = static_cast<uint64_t>(e->block_cap) * kCounterStride;
   size_t off = 0;
   auto carve = [&](size_t bytes) {
     const size_t at = off;
@@ -489,19 +528,16 @@ int wp_create(const wp_config* cfg_in, wp_engine** out) {
   const size_t o_blk = carve(sizeof(Block) * e->block_cap);
   const size_t o_perm = carve(sizeof(int32_t) * e->tok_cap);
   const size_t o_bperm = carve(sizeof(int32_t) * static_cast<size_t>(e->block_cap) * kBlockTokens);
-  const size_t o_cons = carve(sizeof(uint32_t) * e->block_cap * kCounterStride);
+  const size_t o_cons = carve(sizeof(uint32_t) * e->consumed_words);
   const size_t o_ent = carve(sizeof(Entry) * e->entry_cap);
-  const size_t o_part = carve(sizeof(float) * kMaxChunks * static_cast<size_t>(e->tok_cap) * kMaxRank);
+  const size_t o_pub = carve(sizeof(SlotPub) * std::max(cfg.num_staging_slots, 1));
+  const size_t o_tab = carve(sizeof(Entry) * std::max(e->table_cap, 1));
   const size_t o_spart = carve(sizeof(float) * kMaxChunks * static_cast<size_t>(e->tok_cap) * kMaxRank);
   const size_t hbuf_bytes = sizeof(uint16_t) * static_cast<size_t>(e->tok_cap) * kMaxRank;
   const size_t o_hbuf = carve(hbuf_bytes);
+  const size_t o_part = carve(sizeof(float) * e->part_words);
   if (hipMalloc(reinterpret_cast<void**>(&e->ws), off) != hipSuccess)
     return bail(fail(WP_ERR_HIP, "wp_create: workspace allocation (%zu bytes) failed", off));
-  if (hipMemset(e->ws, 0, off) != hipSuccess) return bail(fail(WP_ERR_HIP, "wp_create: workspace clear failed"));
-  if (hipMemsetD32(reinterpret_cast<hipDeviceptr_t>(e->ws + o_part), static_cast<int>(kPartialEmpty),
-                   kMaxChunks * static_cast<size_t>(e->tok_cap) * kMaxRank) != hipSuccess ||
-      hipDeviceSynchronize() != hipSuccess)
-    return bail(fail(WP_ERR_HIP, "wp_create: partial buffer fill failed"));
   e->header = reinterpret_cast<uint32_t*>(e->ws + o_hdr);
   e->segs = reinterpret_cast<Segment*>(e->ws + o_seg);
   e->blocks = reinterpret_cast<Block*>(e->ws + o_blk);
@@ -509,21 +545,33 @@ int wp_create(const wp_config* cfg_in, wp_engine** out) {
   e->bperm = reinterpret_cast<int32_t*>(e->ws + o_bperm);
   e->consumed = reinterpret_cast<uint32_t*>(e->ws + o_cons);
   e->plan_entries = reinterpret_cast<Entry*>(e->ws + o_ent);
-  e->part = reinterpret_cast<float*>(e->ws + o_part);
+  e->pubs = reinterpret_cast<SlotPub*>(e->ws + o_pub);
+  e->dtable = reinterpret_cast<Entry*>(e->ws + o_tab);
   e->spart = reinterpret_cast<float*>(e->ws + o_spart);
   e->hbuf = e->ws + o_hbuf;
+  e->part = reinterpret_cast<float*>(e->ws + o_part);
+  // Everything starts at zero except the partials (kPartialEmpty) and the
+  // publications' ids (-1: nothing published); filled by kernels, then waited for.
+  if (launch_fill_u32(reinterpret_cast<uint32_t*>(e->ws), 0u, o_part / 4, nullptr) != hipSuccess ||
+      launch_fill_u32(reinterpret_cast<uint32_t*>(e->part), kPartialEmpty, e->part_words, nullptr) != hipSuccess)
+    return bail(fail(WP_ERR_HIP, "wp_create: workspace fill failed"));
+  for (int i = 0; i < cfg.num_staging_slots; ++i) {
+    EntryWrites w{};
+    w.pub = e->pubs + i;
+    w.pub_id = -1;
+    if (launch_entry_writes(w, nullptr) != hipSuccess) return bail(fail(WP_ERR_HIP, "wp_create: slot setup failed"));
+  }
+  if (hipDeviceSynchronize() != hipSuccess) return bail(fail(WP_ERR_HIP, "wp_create: workspace setup failed"));
 
   e->pinned_bytes = sizeof(uint32_t) * kHdrWords + sizeof(Segment) * e->seg_cap + sizeof(Block) * e->block_cap +
                     sizeof(int32_t) * e->tok_cap + sizeof(int32_t) * static_cast<size_t>(e->block_cap) * kBlockTokens +
                     sizeof(Entry) * e->entry_cap + 1024;
-  if (hipHostMalloc(reinterpret_cast<void**>(&e->pinned), e->pinned_bytes, hipHostMallocDefault) != hipSuccess)
-    return bail(fail(WP_ERR_HIP, "wp_create: pinned upload buffer failed"));
-  if (hipHostMalloc(reinterpret_cast<void**>(&e->pinned_zero), 64, hipHostMallocDefault) != hipSuccess)
-    return bail(fail(WP_ERR_HIP, "wp_create: pinned zero word failed"));
-  std::memset(e->pinned_zero, 0, 64);
-  if (hipEventCreateWithFlags(&e->upload_done, hipEventDisableTiming) != hipSuccess ||
-      hipEventCreateWithFlags(&e->table_done, hipEventDisableTiming) != hipSuccess)
-    return bail(fail(WP_ERR_HIP, "wp_create: event creation failed"));
+  for (int i = 0; i < kUploadRing; ++i) {
+    if (hipHostMalloc(reinterpret_cast<void**>(&e->pinned[i]), e->pinned_bytes, hipHostMallocDefault) != hipSuccess)
+      return bail(fail(WP_ERR_HIP, "wp_create: pinned upload buffer failed"));
+    if (hipEventCreateWithFlags(&e->upload_done[i], hipEventDisableTiming) != hipSuccess)
+      return bail(fail(WP_ERR_HIP, "wp_create: event creation failed"));
+  }
   // The prefetch engine's own stream, default priority, never synchronising
   // with the null stream (reference: bindings:32).
   if (hipStreamCreateWithFlags(&e->pstream, hipStreamNonBlocking) != hipSuccess)
@@ -531,14 +579,14 @@ int wp_create(const wp_config* cfg_in, wp_engine** out) {
   // The first host-to-device copy on a new stream sets up its copy queue
   // (~5 ms on MI355X, with the host blocked): pay it here, not in the first
   // prefetch_adapter of a serving loop.  hbuf is scratch with no contents yet.
-  if (hipMemcpyAsync(e->hbuf, e->pinned, std::min(e->pinned_bytes, hbuf_bytes), hipMemcpyHostToDevice,
+  if (hipMemcpyAsync(e->hbuf, e->pinned[0], std::min(e->pinned_bytes, hbuf_bytes), hipMemcpyHostToDevice,
                      e->pstream) != hipSuccess ||
       hipStreamSynchronize(e->pstream) != hipSuccess)
     return bail(fail(WP_ERR_HIP, "wp_create: prefetch stream warm-up copy failed"));
   e->slots.resize(cfg.num_staging_slots);
   for (auto& s : e->slots) {
     if (hipEventCreateWithFlags(&s.ready, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&s.last_use, hipEventDisableTiming) != hipSuccess)
+        hipEventCreateWithFlags(&s.released, hipEventDisableTiming) != hipSuccess)
       return bail(fail(WP_ERR_HIP, "wp_create: slot event creation failed"));
   }
   *out = e;
@@ -553,23 +601,21 @@ int wp_destroy(wp_engine* e) {
     Adapter& ad = kv.second;
     if (ad.dA) (void)hipFree(ad.dA);
     if (ad.dB) (void)hipFree(ad.dB);
-    if (ad.hA) (void)hipHostFree(ad.hA);
-    if (ad.hB) (void)hipHostFree(ad.hB);
+    if (ad.host) (void)hipHostFree(ad.host);
     if (ad.copied) (void)hipEventDestroy(ad.copied);
   }
+  sweep_graveyard(e, true);
   for (auto& s : e->slots) {
     if (s.A) (void)hipFree(s.A);
     if (s.B) (void)hipFree(s.B);
     if (s.ready) (void)hipEventDestroy(s.ready);
-    if (s.last_use) (void)hipEventDestroy(s.last_use);
+    if (s.released) (void)hipEventDestroy(s.released);
   }
-  if (e->dtable) (void)hipFree(e->dtable);
   if (e->ws) (void)hipFree(e->ws);
-  if (e->pinned) (void)hipHostFree(e->pinned);
-  if (e->pinned_zero) (void)hipHostFree(e->pinned_zero);
-  if (e->pinned_table) (void)hipHostFree(e->pinned_table);
-  if (e->upload_done) (void)hipEventDestroy(e->upload_done);
-  if (e->table_done) (void)hipEventDestroy(e->table_done);
+  for (int i = 0; i < kUploadRing; ++i) {
+    if (e->pinned[i]) (void)hipHostFree(e->pinned[i]);
+    if (e->upload_done[i]) (void)hipEventDestroy(e->upload_done[i]);
+  }
   if (e->pstream) (void)hipStreamDestroy(e->pstream);
   if (e->pool) (void)hipMemPoolDestroy(e->pool);
   delete e;
@@ -591,6 +637,7 @@ int wp_register_adapter(wp_engine* e, int32_t adapter_id, const void* A, const v
     return fail(WP_ERR_INVALID, "AdapterStore::register_adapter: A/B pointer not 16-byte aligned");
   DeviceGuard g(e->device);
   hipStream_t stream = static_cast<hipStream_t>(stream_);
+  if (stream_capturing(stream)) return fail(WP_ERR_STATE, "register_adapter cannot run during graph capture");
   int rc = evict_impl(e, adapter_id, stream);
   if (rc != WP_OK) return rc;
   Adapter ad;
@@ -602,8 +649,10 @@ int wp_register_adapter(wp_engine* e, int32_t adapter_id, const void* A, const v
   ad.a_bytes = sizeof(uint16_t) * static_cast<size_t>(rank) * d_model;
   ad.b_bytes = sizeof(uint16_t) * static_cast<size_t>(out_features) * rank;
   if (host_resident) {
-    WP_HIP(hipHostMalloc(&ad.hA, ad.a_bytes, hipHostMallocDefault));
-    WP_HIP(hipHostMalloc(&ad.hB, ad.b_bytes, hipHostMallocDefault));
+    const size_t a_span = (ad.a_bytes + 255) & ~size_t(255);
+    WP_HIP(hipHostMalloc(&ad.host, a_span + ad.b_bytes, hipHostMallocDefault));
+    ad.hA = ad.host;
+    ad.hB = static_cast<char*>(ad.host) + a_span;
     std::memcpy(ad.hA, A, ad.a_bytes);
     std::memcpy(ad.hB, B, ad.b_bytes);
   } else {
@@ -614,16 +663,15 @@ int wp_register_adapter(wp_engine* e, int32_t adapter_id, const void* A, const v
     WP_HIP(hipEventCreateWithFlags(&ad.copied, hipEventDisableTiming));
     WP_HIP(hipEventRecord(ad.copied, stream));
   }
-  rc = grow_table(e, adapter_id, stream);
-  if (rc != WP_OK) return rc;
   e->adapters[adapter_id] = ad;
-  if (adapter_id >= 0 && adapter_id < e->dtable_cap) e->table_dirty = true;
-  return WP_OK;
+  return table_write(e, adapter_id, registered_entry(ad), stream);
 }
 
 int wp_evict_adapter(wp_engine* e, int32_t adapter_id, void* stream) {
   if (!e) return fail(WP_ERR_INVALID, "evict_adapter: engine is NULL");
   DeviceGuard g(e->device);
+  if (stream_capturing(static_cast<hipStream_t>(stream)))
+    return fail(WP_ERR_STATE, "evict_adapter cannot run during graph capture");
   return evict_impl(e, adapter_id, static_cast<hipStream_t>(stream));
 }
 
@@ -698,10 +746,15 @@ int wp_build_segments(wp_engine* e, const int32_t* ids, int32_t K, const int32_t
     return fail(WP_ERR_CAPACITY, "build_segments: segments reach token %lld, beyond max_tokens %d",
                 (long long)max_end, e->tok_cap);
 
-  // Wait until the previous upload left the pinned buffer.
-  int rc = wait_event_host(e->upload_done, &e->upload_pending);
-  if (rc != WP_OK) return rc;
-  char* p = e->pinned;
+  // The ring's next pinned buffer: only the upload issued kUploadRing builds
+  // ago can still be reading it.
+  const int ring = e->upload_next;
+  e->upload_next = (ring + 1) % kUploadRing;
+  if (e->upload_pending[ring]) {
+    WP_HIP(hipEventSynchronize(e->upload_done[ring]));
+    e->upload_pending[ring] = false;
+  }
+  char* p = e->pinned[ring];
   uint32_t* hdr = reinterpret_cast<uint32_t*>(p);
   Segment* hsegs = reinterpret_cast<Segment*>(p + 256);
   Block* hblocks = reinterpret_cast<Block*>(reinterpret_cast<char*>(hsegs) + sizeof(Segment) * std::max(K, 1));
@@ -761,8 +814,11 @@ int wp_build_segments(wp_engine* e, const int32_t* ids, int32_t K, const int32_t
                           stream));
   if (!entries.empty())
     WP_HIP(hipMemcpyAsync(e->plan_entries, hent, sizeof(Entry) * entries.size(), hipMemcpyHostToDevice, stream));
-  WP_HIP(hipEventRecord(e->upload_done, stream));
-  e->upload_pending = true;
+  WP_HIP(hipEventRecord(e->upload_done[ring], stream));
+  e->upload_pending[ring] = true;
+  // What a device plan build does first: ready publications into the table,
+  // the partial buffer's repair after a give-up.
+  WP_HIP(launch_maintain(e->header, maint_view(e), stream));
 
   e->plan_kind = 1;
   e->plan_T = max_end;
@@ -783,8 +839,14 @@ int wp_build_seg_bounds(wp_engine* e, const void* idx, int32_t idx_is_int64, int
   DeviceGuard g(e->device);
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   const int bt = plan_block_tokens(T);
+  const Maint m = maint_view(e);
   WP_HIP(launch_plan(idx, idx_is_int64 ? 1 : 0, static_cast<int>(T), e->header, e->segs, e->blocks, e->perm,
-                     e->bperm, e->seg_cap, e->block_cap, bt, stream));
+                     e->bperm, e->seg_cap, e->block_cap, bt, &m, stream));
+  // Slots whose copy had landed are in the table once this build has run
+  // (event queries are not allowed while a graph is being captured).
+  if (!stream_capturing(stream))
+    for (auto& sl : e->slots)
+      if (sl.issued && !sl.applied && hipEventQuery(sl.ready) == hipSuccess) sl.applied = true;
   e->plan_kind = 2;
   e->plan_T = T;
   e->plan_bt = bt;
@@ -840,18 +902,14 @@ int wp_read_device_errors(wp_engine* e, uint32_t* flags, void* stream_) {
   if (!e || !flags) return fail(WP_ERR_INVALID, "read_device_errors: null argument");
   DeviceGuard g(e->device);
   hipStream_t stream = static_cast<hipStream_t>(stream_);
+  if (stream_capturing(stream)) return fail(WP_ERR_STATE, "read_device_errors cannot run during graph capture");
   uint32_t v = 0;
   WP_HIP(hipMemcpyAsync(&v, e->header + kHdrErrors, sizeof(v), hipMemcpyDeviceToHost, stream));
-  WP_HIP(hipMemcpyAsync(e->header + kHdrErrors, e->pinned_zero, sizeof(v), hipMemcpyHostToDevice, stream));
   WP_HIP(hipStreamSynchronize(stream));
-  if (v & kErrSpin) {
-    // A wait that gave up leaves the partial buffer and the per-block
-    // counters undefined: empty and clear them.
-    WP_HIP(hipMemsetD32Async(reinterpret_cast<hipDeviceptr_t>(e->part), static_cast<int>(kPartialEmpty),
-                             kMaxChunks * static_cast<size_t>(e->tok_cap) * kMaxRank, stream));
-    WP_HIP(hipMemsetAsync(e->consumed, 0, sizeof(uint32_t) * e->block_cap * kCounterStride, stream));
-    WP_HIP(hipStreamSynchronize(stream));
-  }
+  WP_HIP(launch_fill_u32(e->header + kHdrErrors, 0u, 1, stream));
+  // After a give-up the buffer is repaired here too, not only at the next plan build.
+  if (v & kErrSpin) WP_HIP(launch_maintain(e->header, maint_view(e), stream));
+  WP_HIP(hipStreamSynchronize(stream));
   *flags = v;
   return WP_OK;
 }
@@ -865,8 +923,7 @@ int check_io(const char* who, int32_t dtype, const void* p16, const char* name) 
 }
 
 // Table-mode weights for the current plan.
-int table_weights(wp_engine* e, hipStream_t stream, Weights* w, uint32_t* mask) {
-  *mask = 0;
+int table_weights(wp_engine* e, hipStream_t stream, Weights* w) {
   w->mode = kTable;
   if (e->plan_kind == 1) {
     if (e->entry_offset != 0)
@@ -876,12 +933,14 @@ int table_weights(wp_engine* e, hipStream_t stream, Weights* w, uint32_t* mask) 
     w->num_ids = static_cast<int32_t>(e->plan_entry_ids.size());
     return WP_OK;
   }
-  int rc = sync_table(e, stream, mask);
-  if (rc != WP_OK) return rc;
+  if (!stream_capturing(stream)) {
+    const int rc = apply_ready_slots(e, stream);
+    if (rc != WP_OK) return rc;
+  }
   // A layer's adapters sit at ids offset by layer * stride: the plan's
   // per-token ids index the table from that offset.
-  w->entries = e->dtable + std::min(e->entry_offset, e->dtable_cap);
-  w->num_ids = std::max(0, e->dtable_cap - e->entry_offset);
+  w->entries = e->dtable + std::min(e->entry_offset, e->table_cap);
+  w->num_ids = std::max(0, e->table_cap - e->entry_offset);
   if (e->entry_count > 0) w->num_ids = std::min(w->num_ids, e->entry_count);
   return WP_OK;
 }
@@ -940,6 +999,7 @@ int stacked_call_args(const char* who, void* y, const void* x, const void* wa, i
   }
   a->w.oc_start[n_slices] = oc;
   a->n_ochunks = oc;
+  a->spin_limit = kDefaultSpinLimit;
   return WP_OK;
 }
 
@@ -990,8 +1050,7 @@ int wp_shrink(wp_engine* e, const void* X, void* H, int32_t d_model, int32_t ran
   a.h = H;
   a.ldh = h_row_stride;
   a.d_model = d_model;
-  uint32_t mask = 0;
-  if ((rc = table_weights(e, stream, &a.w, &mask)) != WP_OK) return rc;
+  if ((rc = table_weights(e, stream, &a.w)) != WP_OK) return rc;
   a.w.n_slices = 1;
   a.n_slots = block_bound(e, resolvable_ids(e));
   if (e->plan_T <= kSmallPlanTokens) {
@@ -1003,10 +1062,9 @@ int wp_shrink(wp_engine* e, const void* X, void* H, int32_t d_model, int32_t ran
   } else {
     shrink_range_split(d_model, &a);
     a.part = e->spart;
+    a.ptok = e->tok_cap;
     WP_HIP(launch_shrink(dtype == WP_DTYPE_BF16, a, stream));
   }
-  if (e->plan_kind == 1) record_slot_uses(e, e->plan_entry_slot, stream);
-  else record_mask_uses(e, mask, stream);
   return WP_OK;
 }
 
@@ -1045,8 +1103,7 @@ int wp_expand(wp_engine* e, const void* H, void* Y, int32_t out_features, int32_
   a.ldh = h_row_stride;
   a.y = Y;
   a.ldy = y_row_stride;
-  uint32_t mask = 0;
-  if ((rc = table_weights(e, stream, &a.w, &mask)) != WP_OK) return rc;
+  if ((rc = table_weights(e, stream, &a.w)) != WP_OK) return rc;
   const int cols = expand_cols_per_workgroup();
   a.w.n_slices = 1;
   a.w.o_size[0] = out_features;
@@ -1056,8 +1113,6 @@ int wp_expand(wp_engine* e, const void* H, void* Y, int32_t out_features, int32_
   a.n_ochunks = a.w.oc_start[1];
   a.n_slots = block_bound(e, resolvable_ids(e));
   WP_HIP(launch_expand(dtype == WP_DTYPE_BF16, a, stream));
-  if (e->plan_kind == 1) record_slot_uses(e, e->plan_entry_slot, stream);
-  else record_mask_uses(e, mask, stream);
   return WP_OK;
 }
 
@@ -1075,9 +1130,10 @@ int wp_add_lora(wp_engine* e, void* y, const void* x, const void* wa, int64_t wa
   DeviceGuard g(e->device);
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   a.tiles = (e->plan_bt + 15) / 16;
-  a.ptok = e->tok_cap;
+  a.ptok = e->ptok;
   a.part = e->part;
   a.consumed = e->consumed;
+  a.spin_limit = e->spin_limit;
   a.plan = plan_view(e);
   a.n_slots = block_bound(e, num_loras);
   fused_split(&a, rank, d_model, e->n_cu);
@@ -1091,6 +1147,7 @@ int wp_add_lora(wp_engine* e, void* y, const void* x, const void* wa, int64_t wa
     a.n_sub = 1;
     shrink_range_split(d_model, &a);
     a.part = e->spart;
+    a.ptok = e->tok_cap;
     WP_HIP(launch_shrink(dtype == WP_DTYPE_BF16, a, stream));
     WP_HIP(launch_expand(dtype == WP_DTYPE_BF16, a, stream));
     return WP_OK;
@@ -1139,8 +1196,7 @@ int wp_shrink_expand(wp_engine* e, const void* X, void* Y, int32_t d_model, int3
   a.y = Y;
   a.ldy = y_row_stride;
   a.d_model = d_model;
-  uint32_t mask = 0;
-  if ((rc = table_weights(e, stream, &a.w, &mask)) != WP_OK) return rc;
+  if ((rc = table_weights(e, stream, &a.w)) != WP_OK) return rc;
   const int cols = expand_cols_per_workgroup();
   a.w.n_slices = 1;
   a.w.o_size[0] = out_features;
@@ -1151,8 +1207,6 @@ int wp_shrink_expand(wp_engine* e, const void* X, void* Y, int32_t d_model, int3
   a.n_slots = block_bound(e, resolvable_ids(e));
   fused_split(&a, rank, d_model, e->n_cu);
   WP_HIP(launch_fused(dtype == WP_DTYPE_BF16, a, stream));
-  if (e->plan_kind == 1) record_slot_uses(e, e->plan_entry_slot, stream);
-  else record_mask_uses(e, mask, stream);
   return WP_OK;
 }
 
@@ -1259,9 +1313,15 @@ int wp_add_lora_static(void* y, const void* x, const void* idx, int32_t idx_is_i
   v.perm = reinterpret_cast<const int32_t*>(base + kSOffPerm);
   v.bperm = reinterpret_cast<const int32_t*>(base + kSOffBperm);
   const int bt = plan_block_tokens(T);
+  // The plan build repairs the partials after a give-up, as an engine's does.
+  Maint m{};
+  m.part = reinterpret_cast<float*>(base + kSOffPart);
+  m.part_words = (kStaticBytes - kSOffPart) / 4;
+  m.consumed = reinterpret_cast<uint32_t*>(base + kSOffCons);
+  m.consumed_words = (kSOffPart - kSOffCons) / 4;
   WP_HIP(launch_plan(idx, idx_is_int64 ? 1 : 0, static_cast<int>(T), v.header, reinterpret_cast<Segment*>(base + kSOffSeg),
                      reinterpret_cast<Block*>(base + kSOffBlk), reinterpret_cast<int32_t*>(base + kSOffPerm),
-                     reinterpret_cast<int32_t*>(base + kSOffBperm), kStaticSegCap, kStaticBlockCap, bt, stream));
+                     reinterpret_cast<int32_t*>(base + kSOffBperm), kStaticSegCap, kStaticBlockCap, bt, &m, stream));
   a.tiles = 1;
   a.ptok = kStaticTokens;
   a.part = reinterpret_cast<float*>(base + kSOffPart);
@@ -1280,21 +1340,29 @@ int wp_prefetch_adapter(wp_engine* e, int32_t adapter_id, int32_t* slot_out) {
   auto it = e->adapters.find(adapter_id);
   if (it == e->adapters.end()) return WP_OK;
   // Existing slot for the id, else the first free one, else none
-  // (reference: StagingBufferPool::acquire_slot, staging_buffer.h:62-73).
+  // (reference: StagingBufferPool::acquire_slot, staging_buffer.h:62-73).  A
+  // slot that already holds the id holds its current weights (registering
+  // the id again releases the slot), so nothing is copied again.
   int s = find_slot(e, adapter_id);
-  if (s < 0) {
-    for (size_t i = 0; i < e->slots.size(); ++i)
-      if (e->slots[i].adapter < 0) {
-        s = static_cast<int>(i);
-        break;
-      }
+  if (s >= 0) {
+    *slot_out = s;
+    return WP_OK;
   }
+  for (size_t i = 0; i < e->slots.size(); ++i)
+    if (e->slots[i].adapter < 0) {
+      s = static_cast<int>(i);
+      break;
+    }
   if (s < 0) return WP_OK;
   DeviceGuard g(e->device);
   Slot& sl = e->slots[s];
   const Adapter& ad = it->second;
-  // Never overwrite buffers that queued kernels may still read.
-  if (sl.used) WP_HIP(hipStreamWaitEvent(e->pstream, sl.last_use, 0));
+  // The slot's last release (and with it every kernel enqueued before it on
+  // the releasing stream) comes first; so does the registration copy.
+  if (sl.release_pending) {
+    WP_HIP(hipStreamWaitEvent(e->pstream, sl.released, 0));
+    sl.release_pending = false;
+  }
   if (ad.copied) WP_HIP(hipStreamWaitEvent(e->pstream, ad.copied, 0));
   if (sl.cap_a < ad.a_bytes) {
     if (sl.A) WP_HIP(hipFreeAsync(sl.A, e->pstream));
@@ -1313,11 +1381,19 @@ int wp_prefetch_adapter(wp_engine* e, int32_t adapter_id, int32_t* slot_out) {
   const hipMemcpyKind kind = ad.hA ? hipMemcpyHostToDevice : hipMemcpyDeviceToDevice;
   WP_HIP(hipMemcpyAsync(sl.A, srcA, ad.a_bytes, kind, e->pstream));
   WP_HIP(hipMemcpyAsync(sl.B, srcB, ad.b_bytes, kind, e->pstream));
+  // Published behind the copy, in stream order: the next plan build writes it
+  // into the table.
+  EntryWrites w{};
+  w.pub = e->pubs + s;
+  w.pub_id = adapter_id;
+  w.pub_entry = staged_entry(ad, sl);
+  WP_HIP(launch_entry_writes(w, e->pstream));
   WP_HIP(hipEventRecord(sl.ready, e->pstream));
   sl.adapter = adapter_id;
   sl.issued = true;
-  e->table_dirty = true;
+  sl.applied = false;
   *slot_out = s;
+  sweep_graveyard(e, false);
   return WP_OK;
 }
 
@@ -1328,9 +1404,31 @@ int wp_is_prefetch_ready(wp_engine* e, int32_t adapter_id, int32_t* ready) {
   return WP_OK;
 }
 
-int wp_release_prefetch(wp_engine* e, int32_t adapter_id) {
+int wp_release_prefetch(wp_engine* e, int32_t adapter_id, void* stream_) {
   if (!e) return fail(WP_ERR_INVALID, "release_prefetch: engine is NULL");
-  return release_slot(e, find_slot(e, adapter_id));
+  const int s = find_slot(e, adapter_id);
+  if (s < 0) return WP_OK;
+  DeviceGuard g(e->device);
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  if (stream_capturing(stream)) return fail(WP_ERR_STATE, "release_prefetch cannot run during graph capture");
+  return release_slot_on(e, s, stream);
+}
+
+int wp_wait_prefetch(wp_engine* e, int32_t adapter_id, void* stream_) {
+  if (!e) return fail(WP_ERR_INVALID, "wait_prefetch: engine is NULL");
+  const int s = find_slot(e, adapter_id);
+  if (s < 0 || !e->slots[s].issued) return WP_NOT_HANDLED;
+  DeviceGuard g(e->device);
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  if (stream_capturing(stream)) return fail(WP_ERR_STATE, "wait_prefetch cannot run during graph capture");
+  WP_HIP(hipStreamWaitEvent(stream, e->slots[s].ready, 0));
+  return WP_OK;
+}
+
+int wp_set_spin_limit(wp_engine* e, uint32_t polls) {
+  if (!e) return fail(WP_ERR_INVALID, "set_spin_limit: engine is NULL");
+  e->spin_limit = polls == 0xFFFFFFFFu ? kDefaultSpinLimit : polls;
+  return WP_OK;
 }
 
 }  // extern "C"

@@ -22,7 +22,7 @@
 // over the scanned offsets), and capacities of 256 / 2048 / 8192 tokens.
 #include <hip/hip_runtime.h>
 
-#include "wp_types.h"
+#include "wp_apply.h"
 
 namespace wp {
 namespace {
@@ -80,6 +80,82 @@ __device__ __forceinline__ int upper_index(const int* a, int n, int q) {
   return lo;
 }
 
+// ---------------------------------------------------------- maintenance ----
+
+__device__ __forceinline__ uint64_t agent_load64(const void* p) {
+  return __hip_atomic_load(static_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void agent_store64(void* p, uint64_t v) {
+  __hip_atomic_store(static_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// What a plan build does first (every thread of the workgroup takes part):
+//   * each ready staging-slot publication is written into the adapter table,
+//     so that every kernel of the step that follows sees the same table (a
+//     publication read while its writer is at work -- odd or changed sequence
+//     -- is left for the next build);
+//   * after a give-up (kHdrPoison), the partial buffer is refilled with
+//     kPartialEmpty and the per-block counters cleared, then the word reset.
+// Ends with a workgroup barrier.
+__device__ void maintain(uint32_t* header, const Maint& m, int* s_flag) {
+  const int tid = threadIdx.x;
+  if (m.table != nullptr && tid < m.n_pubs) {
+    const SlotPub* p = m.pubs + tid;
+    const uint32_t s1 = __hip_atomic_load(&p->seq, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+    if ((s1 & 1u) == 0u) {
+      const int32_t id = __hip_atomic_load(&p->id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      uint64_t w[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) w[i] = agent_load64(reinterpret_cast<const uint64_t*>(&p->entry) + i);
+      // The payload loads complete before the sequence is read again.
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      const uint32_t s2 = __hip_atomic_load(&p->seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (s1 == s2 && id >= 0 && id < m.table_cap) {
+        uint64_t* dst = reinterpret_cast<uint64_t*>(m.table + id);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[i] = w[i];
+      }
+    }
+  }
+  if (tid == 0) *s_flag = m.part != nullptr ? static_cast<int>(
+                              __hip_atomic_load(&header[kHdrPoison], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) : 0;
+  __syncthreads();
+  if (*s_flag != 0) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 e = u32x4{kPartialEmpty, kPartialEmpty, kPartialEmpty, kPartialEmpty};
+    u32x4* part4 = reinterpret_cast<u32x4*>(m.part);
+    for (uint64_t i = tid; i < m.part_words / 4; i += blockDim.x) part4[i] = e;
+    for (uint64_t i = tid; i < m.consumed_words; i += blockDim.x) m.consumed[i] = 0u;
+    __syncthreads();
+    if (tid == 0) __hip_atomic_store(&header[kHdrPoison], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+__global__ __launch_bounds__(256) void maintain_kernel(uint32_t* header, Maint m) {
+  __shared__ int s_flag;
+  maintain(header, m, &s_flag);
+}
+
+// One wave; thread 0 writes.  The publication follows the sequence-lock
+// protocol: odd sequence, payload, even sequence, with agent-scope release
+// fences between, so a reader that saw the same even value before and after
+// its payload loads has a whole payload.
+__global__ __launch_bounds__(64) void entry_writes_kernel(EntryWrites w) {
+  if (threadIdx.x != 0) return;
+  if (w.pub != nullptr) {
+    const uint32_t base = __hip_atomic_load(&w.pub->seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & ~1u;
+    __hip_atomic_store(&w.pub->seq, base + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __hip_atomic_store(&w.pub->id, w.pub_id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      agent_store64(reinterpret_cast<uint64_t*>(&w.pub->entry) + i, reinterpret_cast<const uint64_t*>(&w.pub_entry)[i]);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __hip_atomic_store(&w.pub->seq, base + 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  for (int i = 0; i < w.n; ++i) *w.dst[i] = w.val[i];
+}
+
 // Runs sorted by counting (below) when there are at most kRankMax of them and
 // the waves' broadcast reads (keys x keys per thread x waves) stay within
 // kRankWork; past that, a bitonic sort.  Measured on MI355X: 256-token plans
@@ -93,7 +169,8 @@ template <int NT, int E>
 __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, int idx_is_int64, int T,
                                                   uint32_t* __restrict__ header, Segment* __restrict__ segments,
                                                   Block* __restrict__ blocks, int32_t* __restrict__ perm,
-                                                  int32_t* __restrict__ bperm, int seg_cap, int block_cap, int bt) {
+                                                  int32_t* __restrict__ bperm, int seg_cap, int block_cap, int bt,
+                                                  Maint m) {
   constexpr int CAP = NT * E;
   // s_big: the ids (int64) first, then the sort keys, then per-run offsets.
   __shared__ unsigned long long s_big[CAP];
@@ -105,6 +182,9 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
 
   const int tid = threadIdx.x;
   const int e0 = tid * E;
+
+  // 0. Publications into the adapter table; the partial buffer's repair.
+  maintain(header, m, s_scan);
 
   // 1. ids -> LDS.
   for (int i = tid; i < CAP; i += NT) {
@@ -365,20 +445,37 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
 
 // Host launcher: the smallest capacity variant that holds T.
 hipError_t launch_plan(const void* idx, int idx_is_int64, int T, uint32_t* header, Segment* segments, Block* blocks,
-                       int32_t* perm, int32_t* bperm, int seg_cap, int block_cap, int bt, hipStream_t stream) {
+                       int32_t* perm, int32_t* bperm, int seg_cap, int block_cap, int bt, const Maint* m,
+                       hipStream_t stream) {
   if (T < 0 || bt < 1 || bt > kBlockTokens) return hipErrorInvalidValue;
+  Maint mm{};
+  if (m != nullptr) mm = *m;
+  // Publications are applied by threads 0..n_pubs-1 of the smallest variant.
+  if (mm.n_pubs < 0 || mm.n_pubs > 256) return hipErrorInvalidValue;
   if (T <= 256) {
     plan_kernel<256, 1><<<1, 256, 0, stream>>>(idx, idx_is_int64, T, header, segments, blocks, perm, bperm,
-                                               seg_cap, block_cap, bt);
+                                               seg_cap, block_cap, bt, mm);
   } else if (T <= 2048) {
     plan_kernel<1024, 2><<<1, 1024, 0, stream>>>(idx, idx_is_int64, T, header, segments, blocks, perm, bperm,
-                                                 seg_cap, block_cap, bt);
+                                                 seg_cap, block_cap, bt, mm);
   } else if (T <= kPlanMaxTokens) {
     plan_kernel<1024, 8><<<1, 1024, 0, stream>>>(idx, idx_is_int64, T, header, segments, blocks, perm, bperm,
-                                                 seg_cap, block_cap, bt);
+                                                 seg_cap, block_cap, bt, mm);
   } else {
     return hipErrorInvalidValue;
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_maintain(uint32_t* header, const Maint& m, hipStream_t stream) {
+  if (m.n_pubs < 0 || m.n_pubs > 256) return hipErrorInvalidValue;
+  maintain_kernel<<<1, 256, 0, stream>>>(header, m);
+  return hipGetLastError();
+}
+
+hipError_t launch_entry_writes(const EntryWrites& w, hipStream_t stream) {
+  if (w.n < 0 || w.n > kMaxEntryWrites) return hipErrorInvalidValue;
+  entry_writes_kernel<<<1, 64, 0, stream>>>(w);
   return hipGetLastError();
 }
 

@@ -16,6 +16,7 @@
 // and is written either by the plan kernel or by a stream-ordered upload.
 #pragma once
 
+#include <hip/hip_runtime.h>
 #include <stdint.h>
 
 namespace wp {
@@ -75,6 +76,12 @@ enum HeaderWord : int {
   kHdrT = 4,
   kHdrErrors = 5,
   kHdrBlockTokens = 6,
+  // Non-zero once a wait on partials gave up (kErrSpin): the partial buffer may
+  // hold words a late shrink workgroup wrote after its block's readers
+  // emptied it.  Kernels that use the buffer skip their work while it is set;
+  // the next plan build (or wp_read_device_errors) refills the buffer with
+  // kPartialEmpty, clears the counters and resets the word.
+  kHdrPoison = 7,
   kHdrWords = 16
 };
 
@@ -83,7 +90,7 @@ enum DeviceError : uint32_t {
   kErrIdRange = 1u,       // stacked weights: adapter id >= num_loras
   kErrUnregistered = 2u,  // adapter table: id not registered / not resident
   kErrShape = 4u,         // adapter rank / d / o differs from the call's
-  kErrSpin = 8u,          // a fused call's expand side gave up waiting
+  kErrSpin = 8u,          // a fused call's expand side gave up waiting (later calls skip until the next plan)
   kErrCapacity = 16u      // shrink() / expand(): the plan has more blocks than the call's grid
                           // (the routing names adapter ids that are not registered)
 };
@@ -106,9 +113,26 @@ struct Entry {  // 32 B: one registered adapter as the kernels see it
   uint64_t a_ptr;  // [rank, d] (0: not usable)
   uint64_t b_ptr;  // [o, rank]
   float alpha;
-  int32_t rank;
+  int32_t rank_dtype;  // rank in bits 0..15, the weights' dtype (wp_dtype) in bits 16..23
   int32_t d_model;
   int32_t out_features;
+};
+inline constexpr int32_t pack_rank_dtype(int32_t rank, int32_t dtype) { return rank | (dtype << 16); }
+__host__ __device__ inline constexpr int32_t entry_rank(int32_t rank_dtype) { return rank_dtype & 0xffff; }
+__host__ __device__ inline constexpr int32_t entry_dtype(int32_t rank_dtype) { return (rank_dtype >> 16) & 0xff; }
+
+// A staging slot's publication, written by the prefetch stream once the
+// slot's copy has landed, and read by the plan kernel at the start of every
+// step (which then writes `entry` into the adapter table at `id`, so that
+// every kernel of the step sees one table).  A sequence lock guards it: the
+// writer makes `seq` odd, writes id and entry, then makes it even again; a
+// reader uses what it read only if it saw the same even `seq` before and
+// after.  id < 0: the slot publishes nothing.
+struct SlotPub {  // 48 B
+  uint32_t seq;
+  int32_t id;
+  uint32_t pad[2];
+  Entry entry;
 };
 
 static_assert(sizeof(Segment) == 16, "Segment layout");
@@ -134,6 +158,21 @@ struct Weights {
   int64_t b_stride[kMaxSlices];
   int32_t o_size[kMaxSlices];
   int32_t y_off[kMaxSlices];
+};
+
+// What a plan build (or the engine's maintenance launch) keeps in order
+// besides the plan: it writes every ready slot publication into the adapter
+// table, and after a give-up (kHdrPoison) it refills the partial buffer with
+// kPartialEmpty and clears the per-block counters.
+struct Maint {
+  float* part;           // fused calls' partial buffer
+  uint64_t part_words;
+  uint32_t* consumed;    // per-block counters
+  uint64_t consumed_words;
+  const SlotPub* pubs;   // staging slot publications (n_pubs of them)
+  int32_t n_pubs;
+  int32_t table_cap;     // entries in `table`
+  Entry* table;          // id-indexed adapter table
 };
 
 struct PlanView {

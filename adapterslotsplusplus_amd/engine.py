@@ -79,7 +79,8 @@ class WarpPipeEngine:
         self.device = torch.device("cuda", int(dev))
         self._dev_index = int(dev)
         self._ranks = {}  # rank -> the library's rank_supported answer
-        cfg = _lib.WpConfig(int(dev), int(self.config.num_staging_slots), int(self.config.max_tokens), 64)
+        cfg = _lib.WpConfig(int(dev), int(self.config.num_staging_slots), int(self.config.max_tokens), 64,
+                            int(self.config.max_adapter_ids))
         _lib.check(self._lib.wp_create(ctypes.byref(cfg), ctypes.byref(self._handle)), "WarpPipeEngine")
         self._held = {}
         self._layers = {}  # adapter id -> layers registered under it (multi-layer store)
@@ -392,4 +393,25 @@ class WarpPipeEngine:
         return bool(r.value)
 
     def release_prefetch(self, adapter_id, layer=None):
-        _lib.check(self._lib.wp_release_prefetch(self._handle, self._store_id(adapter_id, layer)), "release_prefetch")
+        """Frees the id's slot in stream order on torch's current stream: work
+        already enqueued there (graph replays included) still reads the slot,
+        work enqueued after it does not, and the slot's next copy waits for
+        that point (reference bindings:64 frees it at once)."""
+        _lib.check(self._lib.wp_release_prefetch(self._handle, self._store_id(adapter_id, layer), self._stream()),
+                   "release_prefetch")
+
+    def wait_prefetch(self, adapter_id, layer=None) -> bool:
+        """Makes torch's current stream wait (on the device) until the id's
+        prefetch copy has landed; False when the id holds no slot.  A
+        build_seg_bounds enqueued after it (captured or not) uses the staged
+        copy."""
+        rc = _lib.check(self._lib.wp_wait_prefetch(self._handle, self._store_id(adapter_id, layer), self._stream()),
+                        "wait_prefetch")
+        return rc == _lib.WP_OK
+
+    def set_spin_limit(self, polls: Optional[int] = None) -> None:
+        """Test and debug: polls before a wait on partials gives up (None: the
+        default, about 0.1 s).  After a give-up (device error 8), calls that use
+        the partial buffer skip their work until the next plan build repairs it."""
+        _lib.check(self._lib.wp_set_spin_limit(self._handle, 0xFFFFFFFF if polls is None else int(polls)),
+                   "set_spin_limit")

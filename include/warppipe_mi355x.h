@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define WP_ABI_VERSION 1
+#define WP_ABI_VERSION 2
 
 enum wp_status {
   WP_OK = 0,
@@ -52,6 +52,9 @@ typedef struct wp_config {
   int32_t num_staging_slots;  /* reference: WP_MAX_STAGING = 8 (warp_pipe_metadata.h:11) */
   int32_t max_tokens;         /* largest T accepted by build_seg_bounds (reference: 256) */
   int32_t max_rank;           /* largest adapter rank (64) */
+  int32_t max_adapter_ids;    /* adapter table size: ids in [0, n) are usable with build_seg_bounds tables
+                                 (others through build_segments only); 0 = 65536.  The table is sized once,
+                                 so captured graphs never see it move. */
 } wp_config;
 
 /* ---- library ---------------------------------------------------------- */
@@ -204,15 +207,34 @@ int wp_add_lora_static(void* y, const void* x, const void* idx, int32_t idx_is_i
 /* Replaces WarpPipeExtension::prefetch_adapter (bindings:46-57): copies the
  * adapter's A and B into a staging slot on the engine's prefetch stream (H2D
  * from the pinned host store, or D2D).  Writes the slot index, or -1 when the
- * id is unknown or every slot is taken (*slot_out). */
+ * id is unknown or every slot is taken (*slot_out).  Once the copy has landed
+ * the slot is published on the device; the next build_seg_bounds (captured or
+ * not) puts it into the adapter table, and an eager call on a table built
+ * before that picks it up when it finds the copy complete. */
 int wp_prefetch_adapter(wp_engine* e, int32_t adapter_id, int32_t* slot_out);
 
 /* Replaces is_prefetch_ready (bindings:59-62): *ready = 1 once the copy completed. */
 int wp_is_prefetch_ready(wp_engine* e, int32_t adapter_id, int32_t* ready);
 
 /* Replaces release_prefetch (bindings:64): frees the id's slot (no-op without one).
- * The slot's buffers are not overwritten before kernels that read them finished. */
-int wp_release_prefetch(wp_engine* e, int32_t adapter_id);
+ * In stream order on `stream`: kernels enqueued on it before the release
+ * (graph replays included) still read the slot; kernels enqueued after it use
+ * the adapter's registered weights (or skip a host-resident adapter), and the
+ * slot's next copy waits for this point.  The reference frees the slot at
+ * once (staging_buffer.h:75-79). */
+int wp_release_prefetch(wp_engine* e, int32_t adapter_id, void* stream);
+
+/* No reference counterpart: makes `stream` wait (on the device, no host
+ * wait) until the id's prefetch copy has landed, so that a plan built next on
+ * it uses the staged copy.  WP_NOT_HANDLED when the id holds no slot. */
+int wp_wait_prefetch(wp_engine* e, int32_t adapter_id, void* stream);
+
+/* Test and debug: polls a wait on partials makes before it gives up (device
+ * error 8, kErrSpin); 0xFFFFFFFF restores the default (131072, about 0.1 s).
+ * After a give-up, calls that use the partial buffer skip their work until
+ * the next build_seg_bounds / build_segments (or wp_read_device_errors) has
+ * repaired the buffer. */
+int wp_set_spin_limit(wp_engine* e, uint32_t polls);
 
 #ifdef __cplusplus
 }

@@ -31,7 +31,7 @@ def test_library_loads_and_exports_every_declared_symbol():
 
 def test_abi_version_and_rank_table():
     lib = _lib.load()
-    assert lib.wp_abi_version() == 1
+    assert lib.wp_abi_version() == 2
     # reference: test_rank_variants.py:97-103
     for r in (8, 16, 32, 64):
         assert lib.wp_rank_supported(r) == 1
