@@ -25,7 +25,8 @@ struct ApplyArgs {
   int32_t n_sub;      // output chunks per expand workgroup (fused), else 1
   int32_t tiles;      // most 16-token tiles per block of the plan (1 or 4)
   int32_t n_slots;    // block slots of the grid (>= the plan's block count)
-  int32_t hs;         // elements per H row: rank, or 64 for mixed ranks
+  int32_t hs;         // elements per H / partial row: n_a x hs1
+  int32_t hs1;        // elements of one A slice's H in a row: rank, or 64 for mixed ranks
   int32_t ptok;       // rows per chunk of `part` (plan positions)
   float* part;        // fp32 partial H by plan position: [n_chunks][ptok][hs], kPartialEmpty between calls
   uint32_t* consumed; // per block (stride kCounterStride): fused calls count expand workgroups done reading,

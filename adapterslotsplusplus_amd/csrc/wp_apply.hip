@@ -226,15 +226,16 @@ struct Resolved {
   uint32_t err = 0;
 };
 
+// A of A-slice sa (0 when every output slice shares one A).
 template <typename T>
-__device__ __forceinline__ Resolved<T> resolve_a(const ApplyArgs& a, const Block& blk) {
+__device__ __forceinline__ Resolved<T> resolve_a(const ApplyArgs& a, const Block& blk, int sa = 0) {
   Resolved<T> r;
   if (a.w.mode == kStacked) {
     if (blk.adapter_id < 0 || blk.adapter_id >= a.w.num_ids) {
       r.err = kErrIdRange;
       return r;
     }
-    r.ptr = static_cast<const T*>(a.w.a_base) + static_cast<int64_t>(blk.adapter_id) * a.w.a_stride;
+    r.ptr = static_cast<const T*>(a.w.a_base[sa]) + static_cast<int64_t>(blk.adapter_id) * a.w.a_stride[sa];
     r.alpha = a.w.scale;
     r.rank = a.rank;
     return r;
@@ -311,7 +312,7 @@ __device__ __forceinline__ int32_t block_token(const ApplyArgs& a, int b, int tl
 // the publication: the partial buffer holds kPartialEmpty between calls, and
 // the readers poll for real values (no acknowledgement wait, no counter).
 template <typename T, int MT>
-__device__ __forceinline__ void shrink_body(const ApplyArgs& a, int b, int c, int r_begin, const Block& blk,
+__device__ __forceinline__ void shrink_body(const ApplyArgs& a, int b, int c, int sa, int r_begin, const Block& blk,
                                             int32_t tok0, const Resolved<T>& res, f32x4* s_red) {
   using V8 = typename VecOf<T>::v8;
   constexpr int KB = kShrinkKSteps;
@@ -332,7 +333,7 @@ __device__ __forceinline__ void shrink_body(const ApplyArgs& a, int b, int c, in
 #pragma unroll
   for (int m = 0; m < MT; ++m)
     ar[m] = m * 16 + row < n_rows ? res.ptr + static_cast<int64_t>(r_begin + m * 16 + row) * d : nullptr;
-  float* prow = a.part + (static_cast<int64_t>(c) * a.ptok + blk.first) * a.hs + r_begin;
+  float* prow = a.part + (static_cast<int64_t>(c) * a.ptok + blk.first) * a.hs + sa * a.hs1 + r_begin;
   for (int tt = 0; tt < ntt; ++tt) {
     const int32_t tok = tt == 0 ? tok0 : block_token(a, b, tt * 16 + row, blk.count);
     const T* xr = tok >= 0 ? X + static_cast<int64_t>(tok) * a.ldx : nullptr;
@@ -383,17 +384,33 @@ __device__ __forceinline__ bool any_empty(f32x4 v) { return is_empty(v[0]) || is
 
 // Waits (wave 0 polls, bounded) until one probe word of every shrink
 // workgroup's partial of block b holds a value: a cheap gate before the full
-// read, which validates every word itself.  Returns false after kErrSpin.
+// read, which validates every word itself.  Shrink workgroups are (d-range,
+// rank group, A slice); a lane probes up to kProbesPerLane of them.  Returns
+// false after a give-up.
+// PA: one A per slice (more shrink workgroups than one probe per lane).
+constexpr int kProbesPerLane = 4;
+template <bool PA>
 __device__ __forceinline__ bool wait_partials(const ApplyArgs& a, const Block& blk, int rank, int* s_flag) {
+  constexpr int kProbes = PA ? kProbesPerLane : 1;
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
     const int n_rg = (rank + a.srows - 1) / a.srows;
-    const int n_probe = a.n_chunks * n_rg;
-    const float* probe = nullptr;
-    if (lane < n_probe) {
-      const int rg = lane / a.n_chunks;
-      const int kc = lane - rg * a.n_chunks;
-      probe = a.part + (static_cast<int64_t>(kc) * a.ptok + blk.first) * a.hs + rg * a.srows;
+    const int per_a = a.n_chunks * n_rg;
+    const int n_probe = PA ? per_a * a.w.n_a : per_a;
+    // Word offsets into the partial buffer (at most 16 x 512 x 256 words).
+    constexpr uint32_t kNone = 0xFFFFFFFFu;
+    uint32_t probe[kProbes];
+#pragma unroll
+    for (int q = 0; q < kProbes; ++q) {
+      const int i = lane + 64 * q;
+      probe[q] = kNone;
+      if (i < n_probe) {
+        const int sa = PA ? i / per_a : 0;
+        const int k = i - sa * per_a;
+        const int rg = k / a.n_chunks;
+        const int kc = k - rg * a.n_chunks;
+        probe[q] = static_cast<uint32_t>((kc * a.ptok + blk.first) * a.hs + sa * a.hs1 + rg * a.srows);
+      }
     }
     int ok = 1;
     for (unsigned spins = 0;; ++spins) {
@@ -404,8 +421,11 @@ __device__ __forceinline__ bool wait_partials(const ApplyArgs& a, const Block& b
         if (lane == 0 && spins >= a.spin_limit) give_up(a.plan.header);
         break;
       }
-      const bool here = probe == nullptr || !is_empty(__builtin_bit_cast(float, atomic_load_u(
-                                                reinterpret_cast<const uint32_t*>(probe))));
+      bool here = true;
+#pragma unroll
+      for (int q = 0; q < kProbes; ++q)
+        here = here && (probe[q] == kNone || !is_empty(__builtin_bit_cast(
+                                                 float, atomic_load_u(reinterpret_cast<const uint32_t*>(a.part) + probe[q]))));
       if (__all(here)) break;
       __builtin_amdgcn_s_sleep(2);
     }
@@ -520,9 +540,12 @@ struct OutChunk {
   int o_first = 0;  // first output column inside the slice
   int o_size = 0;   // the slice's output columns
   int y_off = 0;    // the slice's first column in Y
+  int h_col = 0;    // the slice's first column in an H row (its A slice's H)
 };
 
-template <typename T>
+// kSliceH: a slice may have its own H (one A per slice, or expand() of such
+// a call's H); otherwise every slice reads H from column 0.
+template <typename T, bool kSliceH>
 __device__ __forceinline__ OutChunk<T> out_chunk(const ApplyArgs& a, const Block& blk, int oc) {
   int s = 0;
   while (s + 1 < a.w.n_slices && oc >= a.w.oc_start[s + 1]) ++s;
@@ -531,6 +554,7 @@ __device__ __forceinline__ OutChunk<T> out_chunk(const ApplyArgs& a, const Block
   c.o_first = (oc - a.w.oc_start[s]) * kOC;
   c.o_size = a.w.o_size[s];
   c.y_off = a.w.y_off[s];
+  c.h_col = (kSliceH && a.w.n_a > 1) ? s * a.hs1 : 0;
   return c;
 }
 
@@ -637,18 +661,18 @@ __device__ __forceinline__ void load_chunk(const ApplyArgs& a, const OutChunk<T>
 }
 
 // Y[tokens, chunk columns] = rn(Y + H.B^T) for every token tile of the block;
-// H comes from LDS (fused) or from the caller's token-indexed H (expand()).
-// MAXT tiles are in flight at once: their Y (and H) loads are issued
-// together before the MFMAs; y0 holds tile 0's Y, already loaded.  `stage`
-// is this wave's 16 x kStageStride LDS tile.
+// H comes from LDS (fused; rows of hsl elements) or from the caller's
+// token-indexed H (expand()), at the chunk's column c.h_col.  MAXT tiles are
+// in flight at once: their Y (and H) loads are issued together before the
+// MFMAs; y0 holds tile 0's Y, already loaded.  `stage` is this wave's
+// 16 x kStageStride LDS tile.
 template <typename T, int RANK, bool kHFromLds, int MAXT>
 __device__ __forceinline__ void compute_chunk(const ApplyArgs& a, int b, const Block& blk, int32_t tok0,
                                               const OutChunk<T>& c,
                                               const typename VecOf<T>::v8 (&bf)[kOT][(RANK + 31) / 32],
-                                              const YRows& y0, const T* s_h, T* stage) {
+                                              const YRows& y0, const T* s_h, int hsl, T* stage) {
   using V8 = typename VecOf<T>::v8;
   constexpr int KS = (RANK + 31) / 32;
-  constexpr int HS = RANK + 8;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int row = lane & 15;
@@ -678,9 +702,9 @@ __device__ __forceinline__ void compute_chunk(const ApplyArgs& a, int b, const B
         if (tok_row[i] < 0 || k >= RANK) {
           hf[i][ks] = zero8<T>();
         } else if constexpr (kHFromLds) {
-          hf[i][ks] = __builtin_bit_cast(V8, *reinterpret_cast<const u32x4*>(s_h + (tt * 16 + row) * HS + k));
+          hf[i][ks] = __builtin_bit_cast(V8, *reinterpret_cast<const u32x4*>(s_h + (tt * 16 + row) * hsl + c.h_col + k));
         } else {
-          hf[i][ks] = load8(static_cast<const T*>(a.h) + static_cast<int64_t>(tok_row[i]) * a.ldh + k);
+          hf[i][ks] = load8(static_cast<const T*>(a.h) + static_cast<int64_t>(tok_row[i]) * a.ldh + c.h_col + k);
         }
       }
     }
@@ -712,20 +736,25 @@ __device__ __forceinline__ void compute_chunk(const ApplyArgs& a, int b, const B
 // Expand workgroup `p` of block b: output chunks p, p + n_owg, ... (at most
 // n_sub of them; with several slices of equal width, one chunk per slice).
 // Chunk 0's B and Y are loaded before the wait.
-template <typename T, int RANK, int ROLE, int TILES>
+template <typename T, int RANK, int ROLE, int TILES, bool PA>
 __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, const Block& blk, int32_t tok0,
                                             T* s_h, T* s_stage, int* s_flag) {
   using V8 = typename VecOf<T>::v8;
   constexpr int KS = (RANK + 31) / 32;
   constexpr bool kFusedRole = ROLE == kFused || ROLE == kFusedMulti;
-  constexpr int HS = RANK + 8;
+  // LDS row of the block's H: every A slice's H side by side, plus 8
+  // elements to spread banks.
+  const int hsl = PA ? a.w.n_a * RANK + 8 : RANK + 8;
+  constexpr bool kSliceH = PA || ROLE == kExpandOnly;
   const int n_owg = (a.n_ochunks + a.n_sub - 1) / a.n_sub;
   T* stage = s_stage + (threadIdx.x >> 6) * 16 * kStageStride;
-  OutChunk<T> cur = out_chunk<T>(a, blk, p);
+  OutChunk<T> cur = out_chunk<T, kSliceH>(a, blk, p);
   if (cur.res.err != 0 && p == 0 && threadIdx.x == 0) flag_error(a.plan.header, cur.res.err);
   // Rank rows the block's shrink side writes (0: it could not resolve the
   // adapter and writes nothing).
   const int wrote = kFusedRole ? resolve_a<T>(a, blk).rank : 0;
+  // Partial words per token: every A slice's rank rows.
+  const int wrote_all = PA ? wrote * a.w.n_a : wrote;
   V8 bf[kOT][KS];
   YRows yq;
   load_chunk<T, RANK>(a, cur, tok0, bf, yq);
@@ -738,27 +767,28 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
       // Multi-slice workgroups of small blocks (at most 2048 partial words)
       // poll the data straight away; the probe gate in front pays off for
       // larger blocks and for the single-slice kernel (measured on MI355X).
-      go = (ROLE == kFused || blk.count * wrote * a.n_chunks > 2048) ? wait_partials(a, blk, wrote, s_flag) : true;
+      go = (ROLE == kFused || blk.count * wrote_all * a.n_chunks > 2048) ? wait_partials<PA>(a, blk, wrote, s_flag)
+                                                                          : true;
       if (go) {
         const auto to_lds = [&](int j, int r0, f32x2 v) {
           typename VecOf<T>::v2 o;
           o[0] = static_cast<T>(v[0]);
           o[1] = static_cast<T>(v[1]);
-          *reinterpret_cast<typename VecOf<T>::v2*>(s_h + j * HS + r0) = o;
+          *reinterpret_cast<typename VecOf<T>::v2*>(s_h + j * hsl + r0) = o;
         };
         // Batches of d-ranges: all eight of a multi-slice call's at once;
         // four in the single-slice kernel (eight cost it a spill and
         // measured slower).
         if constexpr (ROLE == kFusedMulti) {
-          collect_partials<8>(a, blk, RANK / 2, cur.res.alpha, to_lds);
+          collect_partials<8>(a, blk, (PA ? a.w.n_a : 1) * RANK / 2, cur.res.alpha, to_lds);
         } else {
-          collect_partials<4>(a, blk, RANK / 2, cur.res.alpha, to_lds);
+          collect_partials<4>(a, blk, (PA ? a.w.n_a : 1) * RANK / 2, cur.res.alpha, to_lds);
         }
       }
     } else if (wrote > 0) {
       // Nothing to compute, but this may be the workgroup that empties the
       // partials: every store must have landed first.
-      await_partials(a, blk, wrote);
+      await_partials(a, blk, wrote_all);
     }
     __syncthreads();
     // This workgroup has read everything it needs from the partials; the
@@ -779,22 +809,22 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
         const int oc = p + (j + 1) * n_owg;
         cn[j].res.ptr = nullptr;
         if (j + 1 < a.n_sub && oc < a.n_ochunks) {
-          cn[j] = out_chunk<T>(a, blk, oc);
+          cn[j] = out_chunk<T, kSliceH>(a, blk, oc);
           if (cn[j].res.err != 0 && p == 0 && threadIdx.x == 0) flag_error(a.plan.header, cn[j].res.err);
           if (cn[j].res.ptr != nullptr) load_chunk<T, RANK>(a, cn[j], tok0, bfn[j], yqn[j]);
         }
       }
-      if (cur.res.ptr != nullptr) compute_chunk<T, RANK, true, 1>(a, b, blk, tok0, cur, bf, yq, s_h, stage);
+      if (cur.res.ptr != nullptr) compute_chunk<T, RANK, true, 1>(a, b, blk, tok0, cur, bf, yq, s_h, hsl, stage);
 #pragma unroll
       for (int j = 0; j < 2; ++j)
-        if (cn[j].res.ptr != nullptr) compute_chunk<T, RANK, true, 1>(a, b, blk, tok0, cn[j], bfn[j], yqn[j], s_h, stage);
+        if (cn[j].res.ptr != nullptr) compute_chunk<T, RANK, true, 1>(a, b, blk, tok0, cn[j], bfn[j], yqn[j], s_h, hsl, stage);
       for (int i = 3; i < a.n_sub; ++i) {
         const int oc = p + i * n_owg;
         if (oc >= a.n_ochunks) break;
-        cur = out_chunk<T>(a, blk, oc);
+        cur = out_chunk<T, kSliceH>(a, blk, oc);
         if (cur.res.err != 0 && p == 0 && threadIdx.x == 0) flag_error(a.plan.header, cur.res.err);
         load_chunk<T, RANK>(a, cur, tok0, bf, yq);
-        if (cur.res.ptr != nullptr) compute_chunk<T, RANK, true, 1>(a, b, blk, tok0, cur, bf, yq, s_h, stage);
+        if (cur.res.ptr != nullptr) compute_chunk<T, RANK, true, 1>(a, b, blk, tok0, cur, bf, yq, s_h, hsl, stage);
       }
     } else if constexpr (ROLE == kFusedMulti) {
       // Rank 64: chunks after the first load when they are reached (its
@@ -803,14 +833,14 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
         const int oc = p + i * n_owg;
         if (oc >= a.n_ochunks) break;
         if (i > 0) {
-          cur = out_chunk<T>(a, blk, oc);
+          cur = out_chunk<T, kSliceH>(a, blk, oc);
           if (cur.res.err != 0 && p == 0 && threadIdx.x == 0) flag_error(a.plan.header, cur.res.err);
           load_chunk<T, RANK>(a, cur, tok0, bf, yq);
         }
-        if (cur.res.ptr != nullptr) compute_chunk<T, RANK, true, 1>(a, b, blk, tok0, cur, bf, yq, s_h, stage);
+        if (cur.res.ptr != nullptr) compute_chunk<T, RANK, true, 1>(a, b, blk, tok0, cur, bf, yq, s_h, hsl, stage);
       }
     } else {
-      compute_chunk<T, RANK, kFusedRole, kFusedRole ? 1 : TILES>(a, b, blk, tok0, cur, bf, yq, s_h, stage);
+      compute_chunk<T, RANK, kFusedRole, kFusedRole ? 1 : TILES>(a, b, blk, tok0, cur, bf, yq, s_h, hsl, stage);
     }
   }
 
@@ -821,7 +851,7 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
     __syncthreads();
     if (*s_flag != 0) {
       if (threadIdx.x == 0) atomic_store_u(&a.consumed[b * kCounterStride], 0u);
-      if (wrote > 0) clear_partials(a, blk, wrote, threadIdx.x, kThreads);
+      if (wrote > 0) clear_partials(a, blk, wrote_all, threadIdx.x, kThreads);
     }
   }
 }
@@ -835,7 +865,7 @@ __device__ __forceinline__ void reduce_to_h(const ApplyArgs& a, int b, const Blo
   // Rank rows the shrink side wrote (none if it could not resolve the adapter).
   const int wrote = res.ptr != nullptr ? res.rank : 0;
   if (wrote <= 0) return;
-  if (blk.count * wrote * a.n_chunks > 2048) wait_partials(a, blk, wrote, s_flag);
+  if (blk.count * wrote * a.n_chunks > 2048) wait_partials<false>(a, blk, wrote, s_flag);
   T* H = static_cast<T*>(a.h);
   const int32_t* toks = a.plan.bperm + static_cast<int64_t>(b) * kBlockTokens;
   collect_partials<8>(a, blk, wrote / 2, res.alpha, [&](int j, int r0, f32x2 v) {
@@ -872,7 +902,7 @@ struct alignas(16) SharedMem {
   static constexpr int kRed = kShrinkRowsFused / 16 * kWaves * 64;    // f32x4
   // H rows of one block: the fused roles run on plans of 16-token blocks
   // (launch_fused checks); no other role keeps H in LDS.
-  static constexpr int kH = (16 * (RR + 8) * 2 + 15) / 16;              // f32x4 worth of T
+  static constexpr int kH = (16 * (kMaxSlices * RR + 8) * 2 + 15) / 16;  // f32x4 worth of T
   f32x4 buf[kRed > kH ? kRed : kH];
   T stage[kWaves * 16 * kStageStride];  // each wave's Y tile (expand)
 };
@@ -885,7 +915,7 @@ struct alignas(16) SharedMem {
 // grid's split into roles).  The library is built with kernarg preloading
 // (-amdgpu-kernarg-preload-count), so these arrive in SGPRs at wave launch
 // and the plan loads go out without a kernel-argument load ahead of them.
-template <typename T, int RANK, int ROLE, int TILES>
+template <typename T, int RANK, int ROLE, int TILES, bool PA>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(waves_per_simd<RANK, ROLE, TILES>())))
 void apply_kernel(const uint32_t* header, const Block* __restrict__ blocks,
                   const int32_t* __restrict__ bperm, int32_t per_shrink, int32_t n_shrink, int32_t per_block,
@@ -926,28 +956,33 @@ void apply_kernel(const uint32_t* header, const Block* __restrict__ blocks,
   const int32_t t0 = row < blk.count ? tok0 : -1;
 
   if (shrink_role) {
-    const Resolved<T> res = resolve_a<T>(a, blk);
+    // part = (A slice, rank group, d-range), d-range fastest.
+    const int per_a = a.n_chunks * a.n_rgroups;
+    const int sa = PA ? part / per_a : 0;
+    const int k = part - sa * per_a;
+    const int rg = k / a.n_chunks;
+    const int c = k - rg * a.n_chunks;
+    const Resolved<T> res = resolve_a<T>(a, blk, sa);
     if (res.err != 0 && part == 0 && threadIdx.x == 0) flag_error(a.plan.header, res.err);
-    const int rg = part / a.n_chunks;
     if constexpr (ROLE == kFusedMulti || ROLE == kShrinkOnly) {
-      shrink_body<T, kShrinkRowsFused / 16>(a, b, part - rg * a.n_chunks, rg * kShrinkRowsFused, blk, t0, res, s_red);
+      shrink_body<T, kShrinkRowsFused / 16>(a, b, c, sa, rg * kShrinkRowsFused, blk, t0, res, s_red);
     } else {
-      shrink_body<T, 1>(a, b, part - rg * a.n_chunks, rg * kShrinkRows, blk, t0, res, s_red);
+      shrink_body<T, 1>(a, b, c, sa, rg * kShrinkRows, blk, t0, res, s_red);
     }
     return;
   }
   if constexpr (ROLE == kShrinkOnly) {
     reduce_to_h<T>(a, b, blk, &s_flag);
   } else if constexpr (RANK != 0) {
-    expand_body<T, RANK, ROLE, TILES>(a, b, part, blk, t0, s_h, smem.stage, &s_flag);
+    expand_body<T, RANK, ROLE, TILES, PA>(a, b, part, blk, t0, s_h, smem.stage, &s_flag);
   } else {
     // Mixed ranks: the block's adapter decides (resolved again inside).
     const Resolved<T> r0 = resolve_b<T>(a, blk, 0);
     switch (r0.rank) {
-      case 16: expand_body<T, 16, ROLE, TILES>(a, b, part, blk, t0, s_h, smem.stage, &s_flag); break;
-      case 32: expand_body<T, 32, ROLE, TILES>(a, b, part, blk, t0, s_h, smem.stage, &s_flag); break;
-      case 64: expand_body<T, 64, ROLE, TILES>(a, b, part, blk, t0, s_h, smem.stage, &s_flag); break;
-      default: expand_body<T, 8, ROLE, TILES>(a, b, part, blk, t0, s_h, smem.stage, &s_flag); break;
+      case 16: expand_body<T, 16, ROLE, TILES, PA>(a, b, part, blk, t0, s_h, smem.stage, &s_flag); break;
+      case 32: expand_body<T, 32, ROLE, TILES, PA>(a, b, part, blk, t0, s_h, smem.stage, &s_flag); break;
+      case 64: expand_body<T, 64, ROLE, TILES, PA>(a, b, part, blk, t0, s_h, smem.stage, &s_flag); break;
+      default: expand_body<T, 8, ROLE, TILES, PA>(a, b, part, blk, t0, s_h, smem.stage, &s_flag); break;
     }
   }
 }
@@ -1165,33 +1200,48 @@ hipError_t launch_shrink_t(const ApplyArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
+template <typename T, int RANK, int ROLE, int TILES>
+void launch_kernel(const ApplyArgs& a, dim3 grid, int32_t per_shrink, int32_t n_shrink, int32_t per_block,
+                   hipStream_t stream) {
+  // One A per slice only in the fused roles; a separate instantiation, so the
+  // shared-A kernels keep their constant indexing and single-probe gate.
+  if constexpr (ROLE == kFused || ROLE == kFusedMulti) {
+    if (a.w.n_a > 1) {
+      apply_kernel<T, RANK, ROLE, TILES, true><<<grid, kThreads, 0, stream>>>(
+          a.plan.header, a.plan.blocks, a.plan.bperm, per_shrink, n_shrink, per_block, a);
+      return;
+    }
+  }
+  apply_kernel<T, RANK, ROLE, TILES, false><<<grid, kThreads, 0, stream>>>(a.plan.header, a.plan.blocks, a.plan.bperm,
+                                                                          per_shrink, n_shrink, per_block, a);
+}
+
 template <typename T, int ROLE, int TILES>
 hipError_t launch_rank(const ApplyArgs& a, hipStream_t stream) {
-  const int64_t S = ROLE == kExpandOnly ? 0 : static_cast<int64_t>(a.n_slots) * a.n_chunks * a.n_rgroups;
+  const int64_t S = ROLE == kExpandOnly ? 0 : static_cast<int64_t>(a.n_slots) * a.n_chunks * a.n_rgroups * a.w.n_a;
   const int64_t E = static_cast<int64_t>(a.n_slots) *
                     ((a.n_ochunks + a.n_sub - 1) / a.n_sub);
   const int64_t n = S + E;
   if (n <= 0) return hipSuccess;
   const dim3 grid(static_cast<unsigned>(n));
-  const int32_t per_shrink = a.n_chunks * a.n_rgroups;
+  const int32_t per_shrink = a.n_chunks * a.n_rgroups * a.w.n_a;
   const int32_t per_block = (a.n_ochunks + a.n_sub - 1) / a.n_sub;
-#define WP_APPLY_ARGS a.plan.header, a.plan.blocks, a.plan.bperm, per_shrink, static_cast<int32_t>(S), per_block, a
+  const int32_t ns = static_cast<int32_t>(S);
   if constexpr (ROLE == kShrinkOnly) {
     // Its shrink side takes the rank from each block's adapter.
-    apply_kernel<T, 0, ROLE, TILES><<<grid, kThreads, 0, stream>>>(WP_APPLY_ARGS);
+    launch_kernel<T, 0, ROLE, TILES>(a, grid, per_shrink, ns, per_block, stream);
   } else {
     switch (a.rank) {
       case 0:  // mixed ranks (registered adapters): each block's adapter decides
-        apply_kernel<T, 0, ROLE, TILES><<<grid, kThreads, 0, stream>>>(WP_APPLY_ARGS);
+        launch_kernel<T, 0, ROLE, TILES>(a, grid, per_shrink, ns, per_block, stream);
         break;
-      case 8: apply_kernel<T, 8, ROLE, TILES><<<grid, kThreads, 0, stream>>>(WP_APPLY_ARGS); break;
-      case 16: apply_kernel<T, 16, ROLE, TILES><<<grid, kThreads, 0, stream>>>(WP_APPLY_ARGS); break;
-      case 32: apply_kernel<T, 32, ROLE, TILES><<<grid, kThreads, 0, stream>>>(WP_APPLY_ARGS); break;
-      case 64: apply_kernel<T, 64, ROLE, TILES><<<grid, kThreads, 0, stream>>>(WP_APPLY_ARGS); break;
+      case 8: launch_kernel<T, 8, ROLE, TILES>(a, grid, per_shrink, ns, per_block, stream); break;
+      case 16: launch_kernel<T, 16, ROLE, TILES>(a, grid, per_shrink, ns, per_block, stream); break;
+      case 32: launch_kernel<T, 32, ROLE, TILES>(a, grid, per_shrink, ns, per_block, stream); break;
+      case 64: launch_kernel<T, 64, ROLE, TILES>(a, grid, per_shrink, ns, per_block, stream); break;
       default: return hipErrorInvalidValue;
     }
   }
-#undef WP_APPLY_ARGS
   return hipGetLastError();
 }
 
@@ -1230,20 +1280,27 @@ hipError_t launch_fused(int dtype_bf16, const ApplyArgs& a, hipStream_t stream) 
   // The kernels' shrink split is fixed per role; the grid and the readers
   // follow a.srows, so the two must agree.
   if (a.srows != (a.n_sub > 1 ? kShrinkRowsFused : kShrinkRows)) return hipErrorInvalidValue;
-  // The block's H rows live in LDS, sized for blocks of 16 tokens.
+  // The block's H rows live in LDS, sized for blocks of 16 tokens and at most
+  // kMaxSlices A slices; the probe gate takes at most 64 x kProbesPerLane
+  // shrink workgroups per block; one A per slice only with stacked weights.
   if (a.tiles != 1) return hipErrorInvalidValue;
+  if (a.w.n_a < 1 || a.w.n_a > kMaxSlices || (a.w.n_a > 1 && (a.w.n_a != a.w.n_slices || a.w.mode != kStacked)) ||
+      a.hs != a.w.n_a * a.hs1 || a.n_chunks * a.n_rgroups * a.w.n_a > 64 * kProbesPerLane)
+    return hipErrorInvalidValue;
   return a.n_sub > 1 ? launch_role<kFusedMulti>(dtype_bf16, a, stream) : launch_role<kFused>(dtype_bf16, a, stream);
 }
 hipError_t launch_shrink(int dtype_bf16, const ApplyArgs& a, hipStream_t stream) {
-  if (a.n_chunks < 1 || a.n_chunks > kMaxChunks) return hipErrorInvalidValue;
+  if (a.n_chunks < 1 || a.n_chunks > kMaxChunks || a.w.n_a != 1) return hipErrorInvalidValue;
   return dtype_bf16 ? launch_shrink_t<__bf16>(a, stream) : launch_shrink_t<_Float16>(a, stream);
 }
 hipError_t launch_shrink_small(int dtype_bf16, const ApplyArgs& a, hipStream_t stream) {
-  if (a.srows != kShrinkRowsFused || a.n_ochunks != 1 || a.n_sub != 1 || a.n_chunks < 1 || a.n_chunks > kMaxChunks)
+  if (a.srows != kShrinkRowsFused || a.n_ochunks != 1 || a.n_sub != 1 || a.n_chunks < 1 || a.n_chunks > kMaxChunks ||
+      a.w.n_a != 1)
     return hipErrorInvalidValue;
   return launch_role<kShrinkOnly>(dtype_bf16, a, stream);
 }
 hipError_t launch_expand(int dtype_bf16, const ApplyArgs& a, hipStream_t stream) {
+  if (a.w.n_a < 1 || a.w.n_a > kMaxSlices) return hipErrorInvalidValue;
   return launch_role<kExpandOnly>(dtype_bf16, a, stream);
 }
 

@@ -122,11 +122,11 @@ constexpr int kExpandWorkgroups = 16;
 // cfg1 9.2 -> 8.8 us.  Multi-slice calls skip the residency test: their grid
 // does not fit at either count, and the halved one only adds a load round
 // (qkv 20.6 -> 20.8 us).
-inline void shrink_split(int d, int rank, int rows, int64_t slots, int64_t expand_per_block, int64_t resident,
+inline void shrink_split(int d, int rank, int rows, int n_a, int64_t slots, int64_t expand_per_block, int64_t resident,
                          ApplyArgs* a) {
   const int g = shrink_rank_groups(rank, rows);
   int nc = static_cast<int>(std::min<int64_t>(std::max(8, shrink_workgroups(rows) / g), ceil_div(d, 128)));
-  while (nc > 4 && (d < nc * 512 || (resident > 0 && slots * (nc * g + expand_per_block) > resident))) nc /= 2;
+  while (nc > 4 && (d < nc * 512 || (resident > 0 && slots * (nc * g * n_a + expand_per_block) > resident))) nc /= 2;
   const int c = static_cast<int>(ceil_div(ceil_div(d, nc), 128) * 128);
   a->dc = c;
   a->n_chunks = static_cast<int>(ceil_div(d, c));
@@ -195,7 +195,7 @@ struct wp_engine {
   Entry* plan_entries = nullptr;
   float* part = nullptr;        // [kMaxChunks][ptok][kMaxRank] fp32 partial H of fused calls (kPartialEmpty between calls)
   float* spart = nullptr;       // [kMaxChunks][tok_cap][kMaxRank] d-range partials of shrink() launches (no invariant)
-  void* hbuf = nullptr;         // [tok_cap][kMaxRank] 2-byte H of large-plan add_lora calls
+  void* hbuf = nullptr;         // [tok_cap][kMaxSlices x kMaxRank] 2-byte H of large-plan add_lora calls
   SlotPub* pubs = nullptr;      // [num_staging_slots] staging publications
   Entry* dtable = nullptr;      // [table_cap] id-indexed adapter table of build_seg_bounds plans
   int table_cap = 0;
@@ -414,6 +414,8 @@ ApplyArgs base_args(const wp_engine* e, int rank) {
   a.n_sub = 1;
   a.tiles = (e->plan_bt + 15) / 16;
   a.hs = rank == 0 ? kMaxRank : rank;
+  a.hs1 = a.hs;
+  a.w.n_a = 1;
   a.ptok = e->ptok;
   a.part = e->part;
   a.consumed = e->consumed;
@@ -533,7 +535,7 @@ int wp_create(const wp_config* cfg_in, wp_engine** out) {
   const size_t o_pub = carve(sizeof(SlotPub) * std::max(cfg.num_staging_slots, 1));
   const size_t o_tab = carve(sizeof(Entry) * std::max(e->table_cap, 1));
   const size_t o_spart = carve(sizeof(float) * kMaxChunks * static_cast<size_t>(e->tok_cap) * kMaxRank);
-  const size_t hbuf_bytes = sizeof(uint16_t) * static_cast<size_t>(e->tok_cap) * kMaxRank;
+  const size_t hbuf_bytes = sizeof(uint16_t) * static_cast<size_t>(e->tok_cap) * kMaxSlices * kMaxRank;
   const size_t o_hbuf = carve(hbuf_bytes);
   const size_t o_part = carve(sizeof(float) * e->part_words);
   if (hipMalloc(reinterpret_cast<void**>(&e->ws), off) != hipSuccess)
@@ -949,21 +951,26 @@ int table_weights(wp_engine* e, hipStream_t stream, Weights* w) {
 // wb_t_all) and fills the launch fields that do not depend on the plan or on
 // where the scratch buffers live.  WP_NOT_HANDLED for a rank without kernels
 // (reference: add_lora_packed returns False, bindings:197-198).
-int stacked_call_args(const char* who, void* y, const void* x, const void* wa, int64_t wa_stride0, int32_t num_loras,
-                      int32_t n_slices, const void* const* wb, const int64_t* wb_stride0, const int32_t* out_features,
-                      const int32_t* y_col_offsets, float scale, int32_t rank, int32_t d_model, int64_t y_row_stride,
-                      int32_t dtype, ApplyArgs* a) {
+int stacked_call_args(const char* who, void* y, const void* x, int32_t n_a, const void* const* wa,
+                      const int64_t* wa_stride0, int32_t num_loras, int32_t n_slices, const void* const* wb,
+                      const int64_t* wb_stride0, const int32_t* out_features, const int32_t* y_col_offsets, float scale,
+                      int32_t rank, int32_t d_model, int64_t y_row_stride, int32_t dtype, ApplyArgs* a) {
   if (!rank_ok(rank)) return WP_NOT_HANDLED;
   int rc = check_io(who, dtype, x, "x");
   if (rc != WP_OK) return rc;
-  if ((rc = check_io(who, dtype, wa, "wa_t_all")) != WP_OK) return rc;
+  if (n_a != 1 && n_a != n_slices) return fail(WP_ERR_INVALID, "%s: one A for all slices, or one per slice", who);
+  if (!wa || !wa_stride0) return fail(WP_ERR_INVALID, "%s: null wa_t_all", who);
+  for (int s = 0; s < n_a; ++s) {
+    if ((rc = check_io(who, dtype, wa[s], "wa_t_all")) != WP_OK) return rc;
+    if (!wa[s]) return fail(WP_ERR_INVALID, "%s: null wa_t_all", who);
+    if (wa_stride0[s] % 8 != 0) return fail(WP_ERR_INVALID, "%s: wa_t_all stride must be a multiple of 8", who);
+  }
   if (!y || !aligned(y, 8)) return fail(WP_ERR_INVALID, "%s: y must be 8-byte aligned", who);
   if (d_model <= 0 || d_model % 8 != 0) return fail(WP_ERR_INVALID, "%s: d_model must be a positive multiple of 8", who);
   if (num_loras <= 0) return fail(WP_ERR_INVALID, "%s: num_loras must be positive", who);
   if (n_slices < 1 || n_slices > kMaxSlices || !wb || !wb_stride0 || !out_features || !y_col_offsets)
     return fail(WP_ERR_INVALID, "%s: 1..%d output slices with their weights, strides, widths and offsets", who,
                 kMaxSlices);
-  if (wa_stride0 % 8 != 0) return fail(WP_ERR_INVALID, "%s: wa_t_all stride must be a multiple of 8", who);
   if (y_row_stride % 4 != 0) return fail(WP_ERR_INVALID, "%s: y row stride must be a multiple of 4", who);
   for (int s = 0; s < n_slices; ++s) {
     if ((rc = check_io(who, dtype, wb[s], "wb_t_all")) != WP_OK) return rc;
@@ -975,7 +982,8 @@ int stacked_call_args(const char* who, void* y, const void* x, const void* wa, i
   }
   a->rank = rank;
   a->n_sub = 1;
-  a->hs = rank;
+  a->hs1 = rank;
+  a->hs = n_a * rank;
   a->x = x;
   a->ldx = d_model;
   a->y = y;
@@ -983,8 +991,11 @@ int stacked_call_args(const char* who, void* y, const void* x, const void* wa, i
   a->d_model = d_model;
   a->w.mode = kStacked;
   a->w.num_ids = num_loras;
-  a->w.a_base = wa;
-  a->w.a_stride = wa_stride0;
+  a->w.n_a = n_a;
+  for (int s = 0; s < n_a; ++s) {
+    a->w.a_base[s] = wa[s];
+    a->w.a_stride[s] = wa_stride0[s];
+  }
   a->w.scale = scale;
   a->w.n_slices = n_slices;
   const int cols = expand_cols_per_workgroup();
@@ -1012,8 +1023,9 @@ int stacked_call_args(const char* who, void* y, const void* x, const void* wa, i
 void fused_split(ApplyArgs* a, int rank, int d_model, int n_cu) {
   a->n_sub = static_cast<int>(ceil_div(a->n_ochunks, kExpandWorkgroups));
   const int multi = a->n_sub > 1 ? 1 : 0;
-  shrink_split(d_model, rank, multi ? kShrinkRowsFused : kShrinkRows, a->n_slots, ceil_div(a->n_ochunks, a->n_sub),
-               multi ? 0 : static_cast<int64_t>(n_cu) * fused_waves_per_simd(rank, multi), a);
+  shrink_split(d_model, rank, multi ? kShrinkRowsFused : kShrinkRows, a->w.n_a, a->n_slots,
+               ceil_div(a->n_ochunks, a->n_sub), multi ? 0 : static_cast<int64_t>(n_cu) * fused_waves_per_simd(rank, multi),
+               a);
 }
 
 }  // namespace
@@ -1116,17 +1128,25 @@ int wp_expand(wp_engine* e, const void* H, void* Y, int32_t out_features, int32_
   return WP_OK;
 }
 
-int wp_add_lora(wp_engine* e, void* y, const void* x, const void* wa, int64_t wa_stride0, int32_t num_loras,
-                int32_t n_slices, const void* const* wb, const int64_t* wb_stride0, const int32_t* out_features,
-                const int32_t* y_col_offsets, float scale, int32_t rank, int32_t d_model, int64_t T,
-                int64_t y_row_stride, int32_t dtype, void* stream_) {
-  if (!e) return fail(WP_ERR_INVALID, "add_lora: engine is NULL");
+}  // extern "C"
+
+namespace {
+
+// add_lora on stacked weights with one A shared by every slice (n_a = 1) or
+// one A per slice (n_a = n_slices).
+int add_lora_impl(wp_engine* e, const char* who, void* y, const void* x, int32_t n_a, const void* const* wa,
+                  const int64_t* wa_stride0, int32_t num_loras, int32_t n_slices, const void* const* wb,
+                  const int64_t* wb_stride0, const int32_t* out_features, const int32_t* y_col_offsets, float scale,
+                  int32_t rank, int32_t d_model, int64_t T, int64_t y_row_stride, int32_t dtype, void* stream_) {
+  if (!e) return fail(WP_ERR_INVALID, "%s: engine is NULL", who);
   ApplyArgs a{};
-  int rc = stacked_call_args("add_lora", y, x, wa, wa_stride0, num_loras, n_slices, wb, wb_stride0, out_features,
+  int rc = stacked_call_args(who, y, x, n_a, wa, wa_stride0, num_loras, n_slices, wb, wb_stride0, out_features,
                              y_col_offsets, scale, rank, d_model, y_row_stride, dtype, &a);
   if (rc != WP_OK) return rc;
-  if (e->plan_kind == 0) return fail(WP_ERR_STATE, "add_lora: no segment table (call build_seg_bounds first)");
-  if (e->plan_T > T) return fail(WP_ERR_INVALID, "add_lora: segments reach token %lld but x has %lld rows", (long long)e->plan_T, (long long)T);
+  if (e->plan_kind == 0) return fail(WP_ERR_STATE, "%s: no segment table (call build_seg_bounds first)", who);
+  if (e->plan_T > T)
+    return fail(WP_ERR_INVALID, "%s: segments reach token %lld but x has %lld rows", who, (long long)e->plan_T,
+                (long long)T);
   DeviceGuard g(e->device);
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   a.tiles = (e->plan_bt + 15) / 16;
@@ -1139,21 +1159,50 @@ int wp_add_lora(wp_engine* e, void* y, const void* x, const void* wa, int64_t wa
   fused_split(&a, rank, d_model, e->n_cu);
   if (e->plan_bt > 16) {
     // Large plans (prefill-sized, 64-token blocks): shrink into the engine's
-    // H, then expand from it.  Each launch keeps several token tiles in
-    // flight per workgroup; the kernel boundary replaces the in-kernel wait.
-    if (e->plan_T > e->tok_cap) return fail(WP_ERR_CAPACITY, "add_lora: table reaches past the engine's H rows");
+    // H (one launch per A slice, each into its columns of an H row), then
+    // expand from it.  Each launch keeps several token tiles in flight per
+    // workgroup; the kernel boundary replaces the in-kernel wait.
+    if (e->plan_T > e->tok_cap) return fail(WP_ERR_CAPACITY, "%s: table reaches past the engine's H rows", who);
     a.h = e->hbuf;
     a.ldh = a.hs;
     a.n_sub = 1;
     shrink_range_split(d_model, &a);
     a.part = e->spart;
     a.ptok = e->tok_cap;
-    WP_HIP(launch_shrink(dtype == WP_DTYPE_BF16, a, stream));
+    for (int sa = 0; sa < n_a; ++sa) {
+      ApplyArgs as = a;
+      as.w.n_a = 1;
+      as.hs = as.hs1 = rank;  // the d-range partials' row (a single A slice)
+      as.w.a_base[0] = a.w.a_base[sa];
+      as.w.a_stride[0] = a.w.a_stride[sa];
+      as.h = static_cast<char*>(e->hbuf) + sizeof(uint16_t) * static_cast<size_t>(sa) * rank;
+      WP_HIP(launch_shrink(dtype == WP_DTYPE_BF16, as, stream));
+    }
     WP_HIP(launch_expand(dtype == WP_DTYPE_BF16, a, stream));
     return WP_OK;
   }
   WP_HIP(launch_fused(dtype == WP_DTYPE_BF16, a, stream));
   return WP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int wp_add_lora(wp_engine* e, void* y, const void* x, const void* wa, int64_t wa_stride0, int32_t num_loras,
+                int32_t n_slices, const void* const* wb, const int64_t* wb_stride0, const int32_t* out_features,
+                const int32_t* y_col_offsets, float scale, int32_t rank, int32_t d_model, int64_t T,
+                int64_t y_row_stride, int32_t dtype, void* stream) {
+  return add_lora_impl(e, "add_lora", y, x, 1, &wa, &wa_stride0, num_loras, n_slices, wb, wb_stride0, out_features,
+                       y_col_offsets, scale, rank, d_model, T, y_row_stride, dtype, stream);
+}
+
+int wp_add_lora_nslice(wp_engine* e, void* y, const void* x, int32_t n_slices, const void* const* wa,
+                       const int64_t* wa_stride0, const void* const* wb, const int64_t* wb_stride0,
+                       const int32_t* out_features, const int32_t* y_col_offsets, int32_t num_loras, float scale,
+                       int32_t rank, int32_t d_model, int64_t T, int64_t y_row_stride, int32_t dtype, void* stream) {
+  return add_lora_impl(e, "add_lora_nslice", y, x, n_slices, wa, wa_stride0, num_loras, n_slices, wb, wb_stride0,
+                       out_features, y_col_offsets, scale, rank, d_model, T, y_row_stride, dtype, stream);
 }
 
 int wp_shrink_expand(wp_engine* e, const void* X, void* Y, int32_t d_model, int32_t out_features, int32_t rank,
@@ -1290,7 +1339,7 @@ int wp_add_lora_static(void* y, const void* x, const void* idx, int32_t idx_is_i
                        float scale, int32_t rank, int32_t d_model, int64_t y_row_stride, int32_t dtype,
                        void* stream_) {
   ApplyArgs a{};
-  int rc = stacked_call_args("add_lora_static", y, x, wa, wa_stride0, num_loras, n_slices, wb, wb_stride0,
+  int rc = stacked_call_args("add_lora_static", y, x, 1, &wa, &wa_stride0, num_loras, n_slices, wb, wb_stride0,
                              out_features, y_col_offsets, scale, rank, d_model, y_row_stride, dtype, &a);
   if (rc != WP_OK) return rc;
   if (T < 0) return fail(WP_ERR_INVALID, "add_lora_static: negative token count");

@@ -148,9 +148,12 @@ enum WeightsMode : int32_t {
 struct Weights {
   int32_t mode;
   int32_t num_ids;  // stacked: L; table: number of entries
-  const void* a_base;
-  int64_t a_stride;  // elements
+  // A matrices: 1 (shared by every slice: one H) or n_slices (slice s has
+  // its own A, stacked mode only: one H per slice, side by side in a row).
+  int32_t n_a;
   float scale;       // stacked: the call's scale
+  const void* a_base[kMaxSlices];
+  int64_t a_stride[kMaxSlices];  // elements
   const Entry* entries;
   int32_t n_slices;
   int32_t oc_start[kMaxSlices + 1];  // prefix of o-chunks per slice

@@ -18,8 +18,9 @@ Additions (each a superset of the reference behaviour):
   * shrink/expand also run on a build_seg_bounds table, through the adapter
     store (the reference reads stale pointers there);
   * rank=0 in shrink/expand selects mixed ranks (each adapter's own rank);
-  * add_lora_packed takes y_offset / y_slice_size, and add_lora_slices
-    expands one shared H into several output slices (packed q/k/v);
+  * add_lora_packed takes y_offset / y_slice_size; add_lora_slices expands
+    into several output slices in one launch, from one shared A or one A per
+    slice (add_lora_packed_nslice, vLLM's packed q/k/v and gate/up layers);
   * register_adapter with CPU tensors puts the adapter in the pinned host
     store; prefetch_adapter then stages it in HBM.
 """
@@ -328,8 +329,13 @@ class WarpPipeEngine:
 
     def add_lora_slices(self, y, x, wa_t_all, wb_t_alls: Sequence[torch.Tensor], scale,
                         y_offsets: Sequence[int], y_slice_sizes: Optional[Sequence[int]] = None) -> bool:
-        """One shrink, several expands: each wb_t_alls[i] ([L, 1, o_i, r]) writes
-        columns [y_offsets[i], y_offsets[i] + o_i) of y (packed q/k/v)."""
+        """Several output slices in one launch: each wb_t_alls[i] ([L, 1, o_i, r])
+        writes columns [y_offsets[i], y_offsets[i] + o_i) of y.  wa_t_all is one
+        [L, 1, r, d] tensor shared by every slice (one shrink: packed q/k/v over
+        one A) or a sequence with one per slice (vLLM's packed layers, each slice
+        with its own lora_a); x is read once either way."""
+        per_slice_a = isinstance(wa_t_all, (list, tuple))
+        was = list(wa_t_all) if per_slice_a else [wa_t_all]
         rank = int(wb_t_alls[0].size(-1))
         ok = self._ranks.get(rank)
         if ok is None:
@@ -339,7 +345,8 @@ class WarpPipeEngine:
         self._on_device(x, "x")
         self._on_device(y, "y")
         dt = _dtype_code(x, "x")
-        if y.dtype != x.dtype or wa_t_all.dtype != x.dtype or any(w.dtype != x.dtype for w in wb_t_alls):
+        if (y.dtype != x.dtype or any(w.dtype != x.dtype for w in was)
+                or any(w.dtype != x.dtype for w in wb_t_alls)):
             raise RuntimeError("add_lora_packed: x, y and the LoRA weights must share one dtype")
         x2 = x.reshape(-1, x.size(-1))
         y2 = y.reshape(-1, y.size(-1))
@@ -347,15 +354,18 @@ class WarpPipeEngine:
             raise RuntimeError("add_lora_packed: x/y must be contiguous")
         if y2.data_ptr() != y.data_ptr():
             raise RuntimeError("add_lora_packed: y must be viewable as 2-D in place")
-        if not wa_t_all.is_contiguous() or not all(w.is_contiguous() for w in wb_t_alls):
+        if not all(w.is_contiguous() for w in was) or not all(w.is_contiguous() for w in wb_t_alls):
             raise RuntimeError("add_lora_packed: wa_t_all/wb_t_all must be contiguous")
-        self._on_device(wa_t_all, "wa_t_all")
         T = int(x2.size(0))
         d_model = int(x2.size(1))
-        L = int(wa_t_all.size(0))
-        if int(wa_t_all.size(-1)) != d_model or int(wa_t_all.size(-2)) != rank:
-            raise RuntimeError(f"add_lora_packed: wa_t_all {tuple(wa_t_all.shape)} does not match x and rank {rank}")
+        L = int(was[0].size(0))
         n = len(wb_t_alls)
+        if per_slice_a and len(was) != n:
+            raise RuntimeError(f"add_lora_packed: {len(was)} lora_a tensors for {n} slices")
+        for w in was:
+            self._on_device(w, "wa_t_all")
+            if int(w.size(0)) != L or int(w.size(-1)) != d_model or int(w.size(-2)) != rank:
+                raise RuntimeError(f"add_lora_packed: wa_t_all {tuple(w.shape)} does not match x and rank {rank}")
         outs = []
         for i, w in enumerate(wb_t_alls):
             self._on_device(w, "wb_t_all")
@@ -371,11 +381,33 @@ class WarpPipeEngine:
         wb_strides = (ctypes.c_int64 * n)(*[int(w.stride(0)) for w in wb_t_alls])
         o_arr = (ctypes.c_int32 * n)(*outs)
         off_arr = (ctypes.c_int32 * n)(*[int(v) for v in y_offsets])
-        rc = _lib.check(self._lib.wp_add_lora(self._handle, _ptr(y2), _ptr(x2), _ptr(wa_t_all),
-                                              int(wa_t_all.stride(0)), L, n, wb_ptrs, wb_strides, o_arr, off_arr,
-                                              float(scale), rank, d_model, T, int(y2.size(1)), dt, self._stream()),
-                        "add_lora_packed")
+        if per_slice_a:
+            wa_ptrs = (ctypes.c_void_p * n)(*[w.data_ptr() for w in was])
+            wa_strides = (ctypes.c_int64 * n)(*[int(w.stride(0)) for w in was])
+            rc = _lib.check(self._lib.wp_add_lora_nslice(self._handle, _ptr(y2), _ptr(x2), n, wa_ptrs, wa_strides,
+                                                         wb_ptrs, wb_strides, o_arr, off_arr, L, float(scale), rank,
+                                                         d_model, T, int(y2.size(1)), dt, self._stream()),
+                            "add_lora_packed_nslice")
+        else:
+            wa = was[0]
+            rc = _lib.check(self._lib.wp_add_lora(self._handle, _ptr(y2), _ptr(x2), _ptr(wa), int(wa.stride(0)), L, n,
+                                                  wb_ptrs, wb_strides, o_arr, off_arr, float(scale), rank, d_model, T,
+                                                  int(y2.size(1)), dt, self._stream()),
+                            "add_lora_packed")
         return rc == _lib.WP_OK
+
+    def add_lora_packed_nslice(self, y, x, lora_a_stacked, lora_b_stacked, scale, output_slices) -> bool:
+        """vLLM's PunicaWrapper.add_lora_packed_nslice shape: slice i has its own
+        lora_a_stacked[i] [L, 1, r, d] and lora_b_stacked[i] [L, 1, o_i, r] and
+        writes columns [sum(output_slices[:i]), + output_slices[i]) of y; every
+        slice in one launch.  False (caller falls back) for a rank without
+        kernels."""
+        offs, acc = [], 0
+        for o in output_slices:
+            offs.append(acc)
+            acc += int(o)
+        return self.add_lora_slices(y, x, list(lora_a_stacked), list(lora_b_stacked), scale, offs,
+                                    [int(o) for o in output_slices])
 
     # ------------------------------------------------------------- staging --
     def prefetch_adapter(self, adapter_id, layer=None) -> int:

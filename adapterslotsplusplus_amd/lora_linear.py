@@ -19,13 +19,16 @@ is the engine-backed counterpart:
     call (shrink + expand in one launch, fp32 accumulation, one rounding of
     base + delta).  mode "none" returns the base only (the reference's
     shared-draft mode).
+  * `WarpPipeLoRAPackedLinear` groups linears that read the same input
+    (q/k/v): one base GEMM over their stacked weights and one launch for all
+    their deltas, each projection with its own adapters.
 
 There is no fallback: a call the engine cannot take (a rank without kernels,
 more tokens than the engine was sized for) raises.
 """
 from __future__ import annotations
 
-from typing import Dict, Iterable, Optional, Tuple
+from typing import Dict, Iterable, Optional, Sequence, Tuple
 
 import torch
 import torch.nn as nn
@@ -102,6 +105,64 @@ class WarpPipeLoRALinear(nn.Module):
                                                self.ctx.scale):
             raise RuntimeError(f"WarpPipeLoRALinear: rank {self.rank} has no kernels")
         return y
+
+
+class WarpPipeLoRAPackedLinear(nn.Module):
+    """Several linears that read the same input (q/k/v, gate/up) as one module:
+    one base GEMM over their stacked weights, then every projection's
+    per-token LoRA delta in ONE engine launch with one adapter pair per
+    projection (add_lora_slices with per-slice A: x is read once).
+    forward(x) returns one output per projection (views into one packed y).
+
+    bases: the nn.Linear modules (same in_features, dtype, device); As[i]
+    [K, rank, in] and Bs[i] [K, out_i, rank] are projection i's adapters."""
+
+    def __init__(self, bases: Sequence[nn.Linear], As: Sequence[torch.Tensor], Bs: Sequence[torch.Tensor],
+                 ctx: DraftLoRAContext):
+        super().__init__()
+        if not 1 <= len(bases) <= 4 or len(As) != len(bases) or len(Bs) != len(bases):
+            raise RuntimeError("WarpPipeLoRAPackedLinear: 1..4 linears, one (A, B) pair each")
+        self.in_features = bases[0].in_features
+        self.out_sizes = [b.out_features for b in bases]
+        if any(b.in_features != self.in_features for b in bases):
+            raise RuntimeError("WarpPipeLoRAPackedLinear: the linears must share in_features")
+        ranks = {int(A.size(1)) for A in As}
+        if len(ranks) != 1:
+            raise RuntimeError("WarpPipeLoRAPackedLinear: one rank for every projection")
+        self.rank = ranks.pop()
+        for base, A, B in zip(bases, As, Bs):
+            if (A.dim() != 3 or B.dim() != 3 or A.size(0) != B.size(0) or A.size(1) != B.size(2)
+                    or A.size(2) != self.in_features or B.size(1) != base.out_features):
+                raise RuntimeError("WarpPipeLoRAPackedLinear: A must be [K, rank, in] and B [K, out, rank]")
+        with torch.no_grad():
+            self.weight = nn.Parameter(torch.cat([b.weight.detach() for b in bases], 0), requires_grad=False)
+            if any(b.bias is not None for b in bases):
+                bias = [b.bias.detach() if b.bias is not None else torch.zeros(b.out_features, dtype=b.weight.dtype,
+                                                                               device=b.weight.device) for b in bases]
+                self.bias = nn.Parameter(torch.cat(bias), requires_grad=False)
+            else:
+                self.bias = None
+        self.ctx = ctx
+        self._offsets = [sum(self.out_sizes[:i]) for i in range(len(bases))]
+        self._was = [A.detach().unsqueeze(1).contiguous() for A in As]
+        self._wbs = [B.detach().unsqueeze(1).contiguous() for B in Bs]
+        for i, (wa, wb) in enumerate(zip(self._was, self._wbs)):
+            self.register_buffer(f"wa_t_all_{i}", wa, persistent=False)
+            self.register_buffer(f"wb_t_all_{i}", wb, persistent=False)
+
+    def forward(self, x: torch.Tensor):
+        y = F.linear(x, self.weight, self.bias)
+        if self.ctx.mode != "none":
+            x2d = x.reshape(-1, self.in_features)
+            if not x2d.is_contiguous():
+                x2d = x2d.contiguous()
+            if x2d.size(0) != self.ctx.tokens:
+                raise RuntimeError(f"WarpPipeLoRAPackedLinear: {x2d.size(0)} rows, but the step's routing covers "
+                                   f"{self.ctx.tokens} tokens")
+            if not self.ctx.engine.add_lora_slices(y.view(-1, y.size(-1)), x2d, self._was, self._wbs, self.ctx.scale,
+                                                   self._offsets):
+                raise RuntimeError(f"WarpPipeLoRAPackedLinear: rank {self.rank} has no kernels")
+        return tuple(y.split(self.out_sizes, dim=-1))
 
 
 def wrap_linears(model: nn.Module, weights: Dict[str, Tuple[torch.Tensor, torch.Tensor]],

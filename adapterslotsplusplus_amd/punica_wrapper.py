@@ -13,6 +13,10 @@ and :219-238 (install_warp_pipe_add_lora).  Same contract:
   * install_warp_pipe_add_lora(lora_manager) switches the live wrapper's class
     with __class__ reassignment and returns False when there is nothing to do.
 
+Added: add_lora_packed_nslice (vLLM's packed q/k/v and gate/up layers, one
+lora_a / lora_b per slice) runs every slice in one launch; the reference
+leaves it to its parent class (punica_wrapper.py:8-16).
+
 Differences: the reference can only subclass AdapterSlots' FusedPunicaWrapper
 (an absent dependency here), so the overrides live in a mixin that is combined
 with whatever class the live wrapper has; sliced outputs (y_offset /
@@ -79,6 +83,28 @@ class WarpPipeAddLoraMixin:
         if not handled:
             return super().add_lora(y, x, wa_t_all, wb_t_all, scale, y_offset, y_slice_size,  # type: ignore[misc]
                                     buffer=buffer)
+        return None
+
+    def add_lora_packed_nslice(self, y: torch.Tensor, x: torch.Tensor, lora_a_stacked, lora_b_stacked, scale: float,
+                               output_slices) -> None:
+        """vLLM's packed layers (q/k/v, gate/up): 2-3 slices that share x, each
+        with its own lora_a / lora_b.  All slices run in one launch on the
+        kernels; the same fallbacks as add_lora, plus slices of different
+        ranks.  The reference leaves this method to its parent
+        (punica_wrapper.py:8-16)."""
+        ranks = {int(b.size(-1)) for b in lora_b_stacked}
+        if (self.is_prefill  # type: ignore[attr-defined]
+                or not self._wp_step_ok
+                or not warp_pipe_available()
+                or not x.is_cuda
+                or len(ranks) != 1
+                or len(output_slices) > 4
+                or not _get_engine()._ext.rank_supported(ranks.pop())):
+            return super().add_lora_packed_nslice(y, x, lora_a_stacked, lora_b_stacked, scale,  # type: ignore[misc]
+                                                  output_slices)
+        if not _get_engine().add_lora_packed_nslice(y, x, lora_a_stacked, lora_b_stacked, float(scale), output_slices):
+            return super().add_lora_packed_nslice(y, x, lora_a_stacked, lora_b_stacked, scale,  # type: ignore[misc]
+                                                  output_slices)
         return None
 
 

@@ -58,6 +58,15 @@ def algorithmic_bytes(T: int, d_in: int, d_out: int, touched_ranks, elem_bytes: 
     return s * T * d_in + 2 * s * T * d_out + sum(s * int(r) * (d_in + d_out) for r in touched_ranks)
 
 
+def algorithmic_bytes_nslice(T: int, d_in: int, d_outs, touched_ranks, elem_bytes: int = 2) -> int:
+    """algorithmic_bytes of one call with one A per output slice: X read once,
+    every slice's Y window read and written once, each touched adapter's A_i
+    [r, d_in] and B_i [o_i, r] read once per slice."""
+    s = elem_bytes
+    return (s * T * d_in + 2 * s * T * sum(d_outs)
+            + sum(s * int(r) * (d_in + int(o)) for r in touched_ranks for o in d_outs))
+
+
 def algorithmic_flops(T: int, d_in: int, d_out: int, token_ranks) -> int:
     """2*T*r*(d_in + d_out) summed over tokens (token_ranks: rank per routed token)."""
     return sum(2 * int(r) * (d_in + d_out) for r in token_ranks)

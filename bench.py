@@ -25,13 +25,19 @@ once (COPY_BYTES read + written); null when that summary is absent.
 
 Prints one JSON line.  `--gpus N` with N > 1 exits: this build runs on one GPU.
 
-`--workload` selects another measurement (each prints its own JSON line; none
-is the metric line): `flatness` (cfg2 with 1..128 resident adapters), `cfg1`
-(with its CPU baseline), `cfg3` (13B mixed-rank decode
-through registered adapters: shrink + expand), `cfg4` (prefill chunk, MFMA),
-`cfg5` (88-call draft step in one graph, plus pinned-host prefetch overlap),
-`draft` (the cfg5 step as a model forward through WarpPipeLoRALinear, with
-and without the adapters).
+The same line also carries the north star's secondary targets, measured in
+the same run (skip with --no-secondary): `flatness_max_over_min` (cfg2 latency
+over 1..128 resident adapters, target <= 1.15), `cfg5_us_per_step` (the draft
+step, q/k/v of a layer in one call with one A per slice) and
+`cfg1_us_per_call`, with their details under `secondary`.
+
+`--workload` selects one measurement alone (each prints its own JSON line;
+none is the metric line): `flatness`, `cfg1` (with its CPU baseline), `cfg3`
+(13B mixed-rank decode through registered adapters: shrink + expand), `cfg4`
+(prefill chunk, MFMA), `cfg5` (the draft step as 88 calls, as 44 launches,
+and through the adapter store with 4 cold adapters staged per step), `draft`
+(the cfg5 step as a model forward through WarpPipeLoRALinear, with and
+without the adapters).
 """
 import argparse
 import json
@@ -56,6 +62,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--layers", type=int, default=40)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip the flatness, cfg5 and cfg1 keys of the default line")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample length")
     ap.add_argument("--workload", default="cfg2", choices=["cfg2", "flatness", "cfg1", "cfg3", "cfg4", "cfg5", "draft"])
     return ap.parse_args()
@@ -171,9 +179,10 @@ def emit(out):
     print(json.dumps(out), flush=True)
 
 
-def run_flatness(args):
+def measure_flatness(reps):
     """cfg2 shapes with N resident adapters, N = 1..128 (Zipf(1.1), seed 1):
-    8 layers x {qkv, o_proj} with distinct weights per layer, one graph per N."""
+    8 layers x {qkv, o_proj} with distinct weights per layer, one graph per N.
+    Returns the rows and max/min of the latency."""
     import torch
 
     from adapterslotsplusplus_amd import WarpPipeEngine
@@ -203,28 +212,32 @@ def run_flatness(args):
                 engine.add_lora_slices(ly["y_q"], ly["x"], ly["wa_q"], ly["wb_q"], 0.5, offs)
                 engine.add_lora_packed(ly["y_o"], ly["x"], ly["wa_o"], ly["wb_o"], 0.5)
 
-        us, _ = graph_us(step, max(5, args.steps))
+        us, _ = graph_us(step, reps)
         nbytes = n_layers * (wl.algorithmic_bytes(T, h, 3 * h, [r] * touched) + wl.algorithmic_bytes(T, h, h, [r] * touched))
         rows.append({"resident": N, "touched": touched, "us_per_16_calls": round(us, 2),
                      "us_per_80_call_step": round(us * 5, 1), "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1)})
         log(f"flatness N={N}: {rows[-1]}")
         del layers
         torch.cuda.empty_cache()
+    assert engine.device_errors() == 0
     lat = [x["us_per_16_calls"] for x in rows]
+    return {"rows": rows, "max_over_min_latency": round(max(lat) / min(lat), 3), "target_max_over_min": 1.15}
+
+
+def run_flatness(args):
+    res = measure_flatness(max(5, args.steps))
     emit({"workload": "cfg2 flatness: resident adapters 1..128, 8 layers x (qkv, o_proj) + build_seg_bounds per graph",
-          "rows": rows, "max_over_min_latency": round(max(lat) / min(lat), 3), "target_max_over_min": 1.15})
+          **res})
 
 
-def run_cfg1(args):
-    """h=4096, r=16, 4 adapters, 64 uniformly routed tokens,
-    fp16, scale 1: one call on the GPU (graph of 40 calls over distinct copies)
-    and the oracle on the host."""
+def measure_cfg1_gpu(reps):
+    """BASELINE configs[0] on the GPU: h=4096, r=16, 4 adapters, 64 uniformly
+    routed tokens, fp16, scale 1; us per add_lora call (a graph of 40 calls
+    over distinct copies of the inputs)."""
     import torch
 
     from adapterslotsplusplus_amd import WarpPipeEngine
     from adapterslotsplusplus_amd import workloads as wl
-    from oracle import bgmv
-    from oracle import segments as so
 
     dt = torch.float16
     idx = wl.uniform_indices(64, 4, seed=0)
@@ -240,8 +253,26 @@ def run_cfg1(args):
         for xc, ac, bc, yc in copies:
             engine.add_lora_packed(yc, xc, ac, bc, 1.0)
 
-    us, _ = graph_us(calls, max(5, args.steps))
+    us, _ = graph_us(calls, reps)
     us /= len(copies)
+    return {"us_per_call": round(us, 3), "bytes_per_call": nbytes, "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1)}
+
+
+def run_cfg1(args):
+    """one call on the GPU and the oracle on the host."""
+    import torch
+
+    from adapterslotsplusplus_amd import workloads as wl
+    from oracle import bgmv
+    from oracle import segments as so
+
+    gpu = measure_cfg1_gpu(max(5, args.steps))
+    dt = torch.float16
+    idx = wl.uniform_indices(64, 4, seed=0)
+    x = wl.normal((64, 4096), 1.0, dt, 10)
+    wa = wl.normal((4, 1, 16, 4096), 0.02, dt, 11)
+    wb = wl.normal((4, 1, 4096, 16), 0.02, dt, 12)
+    nbytes = gpu["bytes_per_call"]
     segs = so.seg_bounds(idx.numpy()).tolist()
     y = torch.zeros(64, 4096, dtype=dt)
     cores = os.cpu_count() or 1
@@ -257,7 +288,7 @@ def run_cfg1(args):
     times.sort()
     cpu_us = times[len(times) // 2] * 1e6
     emit({"workload": "cfg1: T=64, h=4096, r=16, 4 adapters uniform (seed 0), fp16, one add_lora call",
-          "bytes_per_call": nbytes, "gpu_us_per_call": round(us, 3), "gpu_GB_s": round(nbytes / (us * 1e-6) / 1e9, 1),
+          "bytes_per_call": nbytes, "gpu_us_per_call": gpu["us_per_call"], "gpu_GB_s": gpu["GB_s"],
           "cpu_baseline": {"us_per_call": round(cpu_us, 1), "GB_s": round(nbytes / (cpu_us * 1e-6) / 1e9, 3),
                            "cores": cores, "kind": "port", "runs": len(times)}})
 
@@ -379,68 +410,137 @@ def run_cfg4(args):
           "mfma_frac_fp16_dense": round((f_q + f_o) / (per_layer * 1e-6) / 2.5e15, 5)})
 
 
-def run_cfg5(args):
-    """draft step, h=2048, 22 layers x {q,k,v,o} = 88
-    calls, 32 tenants x 4 draft tokens (tenant-contiguous), r=32, bf16;
-    build_seg_bounds + 88 calls in one graph.  Then the same step replayed
-    while 4 cold adapters (one layer-target's A and B each, 256 KiB) are
-    prefetched from the pinned host store on the engine's prefetch stream."""
+CFG5_HOT = list(range(28))                         # device-resident tenants
+CFG5_COLD = [list(range(28, 32)), list(range(32, 36))]  # staged from the pinned host store, alternate steps
+
+
+def cfg5_routing(step):
+    """32 tenants x 4 draft tokens, tenant-contiguous: the 28 hot tenants and
+    this step's 4 cold ones, in a seeded order."""
     import torch
 
-    from adapterslotsplusplus_amd import WarpPipeEngine
+    tenants = CFG5_HOT + CFG5_COLD[step % 2]
+    order = torch.randperm(32, generator=torch.Generator().manual_seed(500 + step))
+    return torch.repeat_interleave(torch.tensor(tenants)[order], 4)
+
+
+def measure_cfg5(reps, warmup):
+    """draft step, h=2048, 22 layers x {q,k,v,o}, 32
+    tenants x 4 draft tokens (T=128, tenant-contiguous), r=32, bf16, one HIP
+    graph per step including build_seg_bounds.
+
+    * 88 calls: every target its own add_lora (vLLM stacked weights);
+    * 44 launches: per layer one q/k/v call with one A per slice
+      (add_lora_packed_nslice) and one o call;
+    * staged: the 88 targets through the multi-layer adapter store
+      (shrink_expand per target); each step routes 4 cold tenants whose
+      target-0 adapters live in the pinned host store: they are prefetched one
+      step ahead on the prefetch stream, the step's stream waits for them on
+      the device, the replay consumes them, and they are released after it
+      (device errors 0 = every routed adapter was applied).  Compared with the
+      same graph routed to resident tenants only."""
+    import torch
+
+    from adapterslotsplusplus_amd import WarpPipeConfig, WarpPipeEngine
     from adapterslotsplusplus_amd import workloads as wl
 
     dev = torch.device("cuda", 0)
-    dt, T, L, h, r, n_calls = torch.bfloat16, 128, 32, 2048, 32, 88
+    dt, T, L, h, r, n_layers = torch.bfloat16, 128, 32, 2048, 32, 22
     gen = torch.Generator(device=dev)
     gen.manual_seed(13)
 
     def rn(shape, std):
         return (torch.randn(*shape, generator=gen, device=dev, dtype=torch.float32) * std).to(dt)
 
+    out = {}
     engine = WarpPipeEngine()
-    was = [rn((L, 1, r, h), .02) for _ in range(n_calls)]
-    wbs = [rn((L, 1, h, r), .02) for _ in range(n_calls)]
-    xs = [rn((T, h), 1.) for _ in range(n_calls)]
-    ys = [rn((T, h), 1.) for _ in range(n_calls)]
     idx = torch.repeat_interleave(torch.arange(L), 4).to(dev)
+    layers = [dict(wa=[rn((L, 1, r, h), .02) for _ in range(4)], wb=[rn((L, 1, h, r), .02) for _ in range(4)],
+                   x=rn((T, h), 1.), y_qkv=rn((T, 3 * h), 1.), y=[rn((T, h), 1.) for _ in range(4)])
+              for _ in range(n_layers)]
 
-    def step():
+    def step88():
         engine.build_seg_bounds(idx)
-        for i in range(n_calls):
-            engine.add_lora_packed(ys[i], xs[i], was[i], wbs[i], 0.5)
+        for ly in layers:
+            for j in range(4):
+                engine.add_lora_packed(ly["y"][j], ly["x"], ly["wa"][j], ly["wb"][j], 0.5)
 
-    us, g = graph_us(step, max(5, args.steps))
-    nbytes = n_calls * wl.algorithmic_bytes(T, h, h, [r] * L)
-    # Cold adapters: pinned host store, prefetched while the step replays.
-    for k in range(4):
-        engine.register_adapter(1000 + k, wl.normal((r, h), .02, dt, 70 + k), wl.normal((h, r), .02, dt, 80 + k), 1.0,
-                                rank=r)
-    reps = max(5, args.steps)
-    for _ in range(max(1, args.warmup)):
-        for k in range(4):
-            engine.release_prefetch(1000 + k)
-            engine.prefetch_adapter(1000 + k)
-        g.replay()
+    def step44():
+        engine.build_seg_bounds(idx)
+        for ly in layers:
+            engine.add_lora_slices(ly["y_qkv"], ly["x"], ly["wa"][:3], ly["wb"][:3], 0.5, [0, h, 2 * h])
+            engine.add_lora_packed(ly["y"][3], ly["x"], ly["wa"][3], ly["wb"][3], 0.5)
+
+    us88, _ = graph_us(step88, reps)
+    us44, _ = graph_us(step44, reps)
+    assert engine.device_errors() == 0
+    b88 = n_layers * 4 * wl.algorithmic_bytes(T, h, h, [r] * L)
+    b44 = n_layers * (wl.algorithmic_bytes_nslice(T, h, [h] * 3, [r] * L) + wl.algorithmic_bytes(T, h, h, [r] * L))
+    out["88_calls"] = {"us_per_step": round(us88, 1), "us_per_call": round(us88 / 88, 2), "bytes_per_step": b88,
+                       "GB_s": round(b88 / (us88 * 1e-6) / 1e9, 1)}
+    out["44_launches_nslice"] = {"us_per_step": round(us44, 1), "bytes_per_step": b44,
+                                 "GB_s": round(b44 / (us44 * 1e-6) / 1e9, 1)}
+    del layers, engine
+    torch.cuda.empty_cache()
+
+    # Adapter store: target t's adapter of tenant i under id t * 64 + i.
+    n_t, stride = 4 * n_layers, 64
+    store = WarpPipeEngine(WarpPipeConfig(layer_stride=stride, max_adapter_ids=n_t * stride))
+    for t in range(n_t):
+        for i in CFG5_HOT + CFG5_COLD[0] + CFG5_COLD[1]:
+            A, B = rn((r, h), .02), rn((h, r), .02)
+            if t == 0 and i >= 28:
+                A, B = A.cpu(), B.cpu()
+            store.register_adapter(i, A, B, 0.5, rank=r, layer=t)
+    xs = [rn((T, h), 1.) for _ in range(n_t)]
+    ys = [rn((T, h), 1.) for _ in range(n_t)]
+    routes = [cfg5_routing(s).to(dev) for s in range(2)]
+    hot_route = torch.repeat_interleave(torch.tensor(CFG5_HOT + CFG5_HOT[:4]), 4).to(dev)
+    idx_buf = hot_route.clone()
+
+    def step_store():
+        store.build_seg_bounds(idx_buf)
+        for t in range(n_t):
+            store.shrink_expand(xs[t], ys[t], h, r, layer=t)
+
+    us_hot, g = graph_us(step_store, reps)
+    for a in CFG5_COLD[0]:
+        assert store.prefetch_adapter(a, layer=0) >= 0
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record()
-    for _ in range(reps):
-        for k in range(4):
-            engine.release_prefetch(1000 + k)
-            engine.prefetch_adapter(1000 + k)
+    n = warmup + reps
+    for s in range(n):
+        if s == warmup:
+            e0.record()
+        if s + 1 < n:
+            for a in CFG5_COLD[(s + 1) % 2]:
+                assert store.prefetch_adapter(a, layer=0) >= 0
+        for a in CFG5_COLD[s % 2]:
+            assert store.wait_prefetch(a, layer=0)
+        idx_buf.copy_(routes[s % 2])
         g.replay()
+        for a in CFG5_COLD[s % 2]:
+            store.release_prefetch(a, layer=0)
     e1.record()
     torch.cuda.synchronize()
-    ready = all(engine.is_prefetch_ready(1000 + k) for k in range(4))
-    us_pf = e0.elapsed_time(e1) * 1e3 / reps
-    emit({"workload": "cfg5: draft step, h=2048, 22 layers x 4 targets = 88 add_lora calls, T=128 (32 tenants x 4), "
-                      "r=32, bf16, build_seg_bounds + 88 calls in one graph",
-          "us_per_step": round(us, 1), "us_per_call": round(us / n_calls, 2), "bytes_per_step": nbytes,
-          "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1),
-          "with_4_cold_prefetches": {"us_per_step": round(us_pf, 1), "prefetches_ready": ready,
-                                     "bytes_per_prefetch": 2 * r * h * 2}})
+    us_cold = e0.elapsed_time(e1) * 1e3 / reps
+    errors = store.device_errors()
+    b_store = n_t * wl.algorithmic_bytes(T, h, h, [r] * 32)
+    out["adapter_store_88_calls"] = {
+        "us_per_step_resident_only": round(us_hot, 1),
+        "us_per_step_with_4_cold_staged": round(us_cold, 1),
+        "GB_s_with_4_cold_staged": round(b_store / (us_cold * 1e-6) / 1e9, 1),
+        "bytes_per_prefetch": 2 * r * h * 2, "device_errors": errors,
+        "cold_adapters_consumed": errors == 0}
+    del store, xs, ys
+    torch.cuda.empty_cache()
+    return out
+
+
+def run_cfg5(args):
+    res = measure_cfg5(max(5, args.steps), max(1, args.warmup))
+    emit({"workload": "cfg5: draft step, h=2048, 22 layers x (q, k, v, o), T=128 (32 tenants x 4), r=32, bf16, "
+                      "build_seg_bounds + the layers' calls in one graph per step", **res})
 
 
 def run_draft(args):
@@ -603,6 +703,9 @@ def main():
     o_us = launch_duration_us([o_call(ly) for ly in layers], reps)
     achieved = bytes_qkv / (qkv_us * 1e-6) / 1e9
 
+    del layers
+    torch.cuda.empty_cache()
+
     # Calibration copy for the PMC runs: reads and writes COPY_BYTES once.
     src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
     dst = torch.empty_like(src)
@@ -650,6 +753,26 @@ def main():
             },
         },
     }
+    if not args.no_secondary:
+        # The north star's other targets, on the same run: latency flatness
+        # over 1..128 resident adapters, the cfg5 draft step, cfg1 per call.
+        reps = max(10, args.steps)
+        log("secondary: flatness")
+        flat = measure_flatness(reps)
+        log("secondary: cfg5 draft step")
+        c5 = measure_cfg5(reps, max(2, args.warmup))
+        log("secondary: cfg1")
+        c1 = measure_cfg1_gpu(reps)
+        out["flatness_max_over_min"] = flat["max_over_min_latency"]
+        out["cfg5_us_per_step"] = c5["44_launches_nslice"]["us_per_step"]
+        out["cfg1_us_per_call"] = c1["us_per_call"]
+        out["secondary"] = {
+            "flatness": {**flat, "workload": "cfg2 shapes, 8 layers x (qkv, o_proj) per graph, N resident adapters"},
+            "cfg5_draft_step": {**c5, "workload": "h=2048, 22 layers x (q, k, v, o), T=128 (32 tenants x 4), r=32, "
+                                                  "bf16, build_seg_bounds + the calls in one graph; cfg5_us_per_step "
+                                                  "is the 44-launch form (q/k/v in one call, one A per slice)"},
+            "cfg1": {**c1, "workload": "T=64, h=4096, r=16, 4 adapters uniform (seed 0), fp16, one add_lora call"},
+        }
     if not args.no_cpu_baseline:
         log("cpu baseline")
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)

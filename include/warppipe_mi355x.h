@@ -202,6 +202,19 @@ int wp_add_lora_static(void* y, const void* x, const void* idx, int32_t idx_is_i
                        const int64_t* wb_stride0, const int32_t* out_features, const int32_t* y_col_offsets,
                        float scale, int32_t rank, int32_t d_model, int64_t y_row_stride, int32_t dtype, void* stream);
 
+/* wp_add_lora with one A per output slice: vLLM's add_lora_packed_nslice
+ * (packed q/k/v or gate/up layers, each slice with its own lora_a and lora_b;
+ * the reference hook leaves this method to the stock path,
+ * lora_warp_pipe/punica_wrapper.py:8-16).  In one launch, for every token t
+ * of the last build_seg_bounds table and every slice s:
+ *   h_s = rn(scale * x[t] . wa[s][id]^T);  y[t, y_off[s] + o] = rn(y[...] + h_s . wb[s][id][o, :])
+ * x is read once per call; wa[s]: [L, rank, d] with element stride
+ * wa_stride0[s]; wb[s]: [L, o[s], rank].  1..4 slices, one rank for all. */
+int wp_add_lora_nslice(wp_engine* e, void* y, const void* x, int32_t n_slices, const void* const* wa,
+                       const int64_t* wa_stride0, const void* const* wb, const int64_t* wb_stride0,
+                       const int32_t* out_features, const int32_t* y_col_offsets, int32_t num_loras, float scale,
+                       int32_t rank, int32_t d_model, int64_t T, int64_t y_row_stride, int32_t dtype, void* stream);
+
 /* ---- staging / prefetch ---------------------------------------------------- */
 
 /* Replaces WarpPipeExtension::prefetch_adapter (bindings:46-57): copies the

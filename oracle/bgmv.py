@@ -94,3 +94,19 @@ def add_lora(y: torch.Tensor, x: torch.Tensor, wa_t_all: torch.Tensor, wb_t_all,
             yn[ts:ts + tc, off:off + o] = expand_rows(h, b, yn[ts:ts + tc, off:off + o])
     return yn.reshape(y.shape)
 
+
+def add_lora_nslice(y: torch.Tensor, x: torch.Tensor, wa_t_alls: Sequence[torch.Tensor],
+                    wb_t_alls: Sequence[torch.Tensor], scale: float, segments: Iterable[Sequence[int]],
+                    y_offsets: Sequence[int]) -> torch.Tensor:
+    """add_lora over the build_seg_bounds table with one A per slice: slice i
+    is an independent add_lora with (wa_t_alls[i], wb_t_alls[i]) into columns
+    [y_offsets[i], + o_i) of y -- vLLM's PunicaWrapper.add_lora_packed_nslice
+    is that loop over slices (one add_lora per slice, offsets accumulated from
+    output_slices), named by the reference at lora_warp_pipe/punica_wrapper.py:8-16.
+    Each slice's H is rounded after scale and y once per slice, as in add_lora
+    (warp_pipe_r32.cu:129, :194).  Returns the updated copy of y."""
+    yn = y
+    for wa, wb, off in zip(wa_t_alls, wb_t_alls, y_offsets):
+        yn = add_lora(yn, x, wa, wb, scale, segments, off)
+    return yn
+

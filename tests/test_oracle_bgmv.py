@@ -145,3 +145,35 @@ def test_slices_write_their_windows():
     h = bgmv.shrink_rows(x, A, 1.0)
     for i, w in enumerate(wbs):
         assert torch.equal(yn[:, 8 * i:8 * i + 8], bgmv.expand_rows(h, w[0, 0], y3[:, 8 * i:8 * i + 8]))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_nslice_brute_force_and_slice_independence(dtype):
+    """add_lora_nslice: every slice equals the float64 brute force with its own
+    A and B in its own column window; columns outside every window are
+    untouched; swapping two slices' A tensors (a plausible mistake: one A
+    shared, or A indexed by the wrong slice) changes the result."""
+    g = torch.Generator().manual_seed(41)
+    T, d, r, L = 9, 12, 4, 3
+    widths = [5, 3, 6]
+    offs = [2, 9, 14]
+    was = [(torch.randn(L, 1, r, d, generator=g) * 0.3).to(dtype) for _ in widths]
+    wbs = [(torch.randn(L, 1, o, r, generator=g) * 0.3).to(dtype) for o in widths]
+    x = torch.randn(T, d, generator=g).to(dtype)
+    y = torch.randn(T, 21, generator=g).to(dtype)
+    idx = [0, 0, 2, -1, 1, 1, 1, 2, 0]
+    segs = so.seg_bounds(idx).tolist()
+    out = bgmv.add_lora_nslice(y, x, was, wbs, 0.7, segs, offs)
+    covered = torch.zeros(21, dtype=torch.bool)
+    for wa, wb, off, o in zip(was, wbs, offs, widths):
+        covered[off:off + o] = True
+        for t, i in enumerate(idx):
+            if i < 0:
+                continue
+            h = brute_shrink(x[t:t + 1], wa[i, 0], 0.7, dtype)
+            ref = brute_expand(h, wb[i, 0], y[t:t + 1, off:off + o])
+            assert torch.equal(out[t:t + 1, off:off + o], ref), f"token {t}, slice at {off}"
+    assert torch.equal(out[:, ~covered], y[:, ~covered])
+    assert torch.equal(out[3], y[3])  # id < 0
+    swapped = bgmv.add_lora_nslice(y, x, [was[1], was[0], was[2]], wbs, 0.7, segs, offs)
+    assert not torch.equal(swapped, out)
