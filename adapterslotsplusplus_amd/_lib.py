@@ -10,7 +10,9 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libwarppipe_mi355x.so")
+# WP_LIB_PATH selects another build of the library (the traced one, for
+# adapterslotsplusplus_amd.trace_phases).
+LIB_PATH = os.environ.get("WP_LIB_PATH") or os.path.join(HERE, "libwarppipe_mi355x.so")
 
 WP_OK = 0
 WP_NOT_HANDLED = 1
@@ -38,7 +40,7 @@ EXPORTED = (
     "wp_build_seg_bounds", "wp_read_segments", "wp_read_plan", "wp_read_device_errors",
     "wp_shrink", "wp_expand", "wp_shrink_expand", "wp_add_lora", "wp_prefetch_adapter", "wp_is_prefetch_ready",
     "wp_release_prefetch", "wp_add_lora_static", "wp_wait_prefetch", "wp_set_spin_limit",
-    "wp_add_lora_nslice",
+    "wp_add_lora_nslice", "wp_prefetch_adapters", "wp_release_prefetches", "wp_wait_prefetches", "wp_set_trace",
 )
 
 
@@ -94,6 +96,10 @@ def load():
         "wp_is_prefetch_ready": ([p, i32, P(i32)], ctypes.c_int),
         "wp_release_prefetch": ([p, i32, p], ctypes.c_int),
         "wp_wait_prefetch": ([p, i32, p], ctypes.c_int),
+        "wp_prefetch_adapters": ([p, p, i32, p], ctypes.c_int),
+        "wp_release_prefetches": ([p, p, i32, p], ctypes.c_int),
+        "wp_wait_prefetches": ([p, p, i32, p], ctypes.c_int),
+        "wp_set_trace": ([p, p, i64], ctypes.c_int),
         "wp_add_lora_nslice": ([p, p, p, i32, p, p, p, p, p, p, i32, f32, i32, i32, i64, i64, i32, p], ctypes.c_int),
         "wp_set_spin_limit": ([p, ctypes.c_uint32], ctypes.c_int),
         "wp_add_lora_static": ([p, p, p, i32, i64, p, i64, i32, i32, p, p, p, p, f32, i32, i32, i64, i32, p],

@@ -47,23 +47,32 @@ def _run(cmd):
     return out
 
 
-def build(verbose: bool = False) -> str:
-    """Compiles every source (always) and links the shared library."""
-    os.makedirs(OBJ_DIR, exist_ok=True)
-    objs = [os.path.join(OBJ_DIR, s.rsplit(".", 1)[0] + ".o") for s in SOURCES]
-    cmds = [[HIPCC, *COMMON, *EXTRA.get(s, []), "-c", os.path.join(CSRC, s), "-o", o] for s, o in zip(SOURCES, objs)]
+TRACE_LIB_PATH = os.path.join(HERE, "libwarppipe_mi355x_trace.so")
+
+
+def build(verbose: bool = False, trace: bool = False) -> str:
+    """Compiles every source (always) and links the shared library.  trace:
+    the diagnostic build (-DWP_TRACE, per-workgroup phase timestamps of the
+    fused kernels; see trace_phases.py) as libwarppipe_mi355x_trace.so."""
+    obj_dir = OBJ_DIR + ("_trace" if trace else "")
+    lib_path = TRACE_LIB_PATH if trace else LIB_PATH
+    flags = ["-DWP_TRACE=1"] if trace else []
+    os.makedirs(obj_dir, exist_ok=True)
+    objs = [os.path.join(obj_dir, s.rsplit(".", 1)[0] + ".o") for s in SOURCES]
+    cmds = [[HIPCC, *COMMON, *flags, *EXTRA.get(s, []), "-c", os.path.join(CSRC, s), "-o", o]
+            for s, o in zip(SOURCES, objs)]
     with ThreadPoolExecutor(max_workers=len(cmds)) as ex:
         outs = list(ex.map(_run, cmds))
-    tmp = LIB_PATH + ".tmp"
+    tmp = lib_path + ".tmp"
     outs.append(_run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-o", tmp, *objs]))
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, lib_path)
     if verbose:
         for o in outs:
             if o.strip():
                 print(o)
-    return LIB_PATH
+    return lib_path
 
 
 if __name__ == "__main__":
-    path = build(verbose="-v" in sys.argv)
+    path = build(verbose="-v" in sys.argv, trace="--trace" in sys.argv)
     print(path)

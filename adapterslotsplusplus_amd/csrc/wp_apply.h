@@ -32,9 +32,17 @@ struct ApplyArgs {
   uint32_t* consumed; // per block (stride kCounterStride): fused calls count expand workgroups done reading,
                       // shrink() counts d-range workgroups done; zero between calls
   uint32_t spin_limit; // polls before a wait on partials gives up (kDefaultSpinLimit)
+  uint64_t* trace;     // traced builds (WP_TRACE) only: kTraceWords timestamps per workgroup, or null
+  int64_t trace_words; // capacity of `trace` (a launch whose grid does not fit is not traced)
   PlanView plan;
   Weights w;
 };
+
+// Words per workgroup of a traced build's timestamp buffer: stamps 0..6 and
+// a tag (role and block) in word 7.
+constexpr int kTraceWords = 8;
+// 1 in a library built with WP_TRACE.
+int traced_build();
 
 // Bound of a wait on partials: polls of ~1 us each, so about 0.1 s.
 constexpr uint32_t kDefaultSpinLimit = 1u << 17;
@@ -53,7 +61,7 @@ hipError_t launch_maintain(uint32_t* header, const Maint& m, hipStream_t stream)
 // Tiny writes of adapter-table entries and of one slot publication, in stream
 // order (one wave): pub (if not null) gets (pub_id, pub_entry) under its
 // sequence lock, then dst[i] = val[i] for i < n.
-constexpr int kMaxEntryWrites = 4;
+constexpr int kMaxEntryWrites = 16;
 struct EntryWrites {
   int32_t n;
   int32_t pub_id;
@@ -61,8 +69,38 @@ struct EntryWrites {
   Entry pub_entry;
   Entry* dst[kMaxEntryWrites];
   Entry val[kMaxEntryWrites];
+  // Further publications to empty (id -1) under their sequence locks.
+  int32_t n_clear;
+  SlotPub* clear[kMaxEntryWrites];
 };
 hipError_t launch_entry_writes(const EntryWrites& w, hipStream_t stream);
+
+// Staging copies: job j copies a_bytes from src_a to dst_a and b_bytes from
+// src_b to dst_b (sources in device memory or in pinned host memory the
+// device reads directly), over kStageWorkgroups workgroups; the job's last
+// workgroup to finish then publishes (pub_id, pub_entry) into *pub under its
+// sequence lock.  pub->pad[0] counts the job's finished workgroups (zero
+// between jobs).
+constexpr int kMaxStageJobs = 8;
+constexpr int kStageWorkgroups = 8;
+struct StageJob {
+  const void* src_a;
+  void* dst_a;
+  uint64_t a_bytes;  // multiple of 16
+  const void* src_b;
+  void* dst_b;
+  uint64_t b_bytes;  // multiple of 16
+  SlotPub* pub;
+  int32_t pub_id;
+  int32_t pad;
+  Entry pub_entry;
+};
+struct StageJobs {
+  int32_t n;
+  int32_t pad;
+  StageJob job[kMaxStageJobs];
+};
+hipError_t launch_stage_copies(const StageJobs& jobs, hipStream_t stream);
 
 // shrink(): a workgroup streams its d-range (a.dc, a multiple of
 // kShrinkSlices * 128 columns) in groups of kShrinkSlices 128-column slices.

@@ -182,6 +182,29 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 
 __device__ __forceinline__ void flag_error(uint32_t* header, uint32_t bits) { atomicOr(&header[kHdrErrors], bits); }
 
+// Traced builds (-DWP_TRACE, python -m adapterslotsplusplus_amd.build --trace):
+// thread 0 of every workgroup records the 100 MHz real-time counter at the
+// phase boundaries of the fused kernels, after waiting for wave 0's memory
+// operations so that a stamp follows the data it names (which perturbs the
+// timing a little).  Stamps: 0 entry, 1 plan loaded; shrink workgroups 2 first
+// token tile's MFMAs done, 3 partials stored and acknowledged; expand
+// workgroups 2 B and Y loaded, 3 gate open, 4 partials collected, 5 Y
+// stored.  Word 7: role (1 shrink, 2 expand) | block << 8.
+#ifdef WP_TRACE
+__device__ __forceinline__ void trace_stamp(const ApplyArgs& a, int i) {
+  if (a.trace != nullptr && threadIdx.x == 0) {
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    a.trace[static_cast<size_t>(blockIdx.x) * kTraceWords + i] = wall_clock64();
+  }
+}
+__device__ __forceinline__ void trace_tag(const ApplyArgs& a, uint64_t tag) {
+  if (a.trace != nullptr && threadIdx.x == 0) a.trace[static_cast<size_t>(blockIdx.x) * kTraceWords + 7] = tag;
+}
+#else
+__device__ __forceinline__ void trace_stamp(const ApplyArgs&, int) {}
+__device__ __forceinline__ void trace_tag(const ApplyArgs&, uint64_t) {}
+#endif
+
 // A wait on partials that reached its bound: flagged (kErrSpin), and the
 // partial buffer marked poisoned (kHdrPoison).  A shrink workgroup that was
 // late may yet write its partial after the block's readers emptied the
@@ -357,6 +380,7 @@ __device__ __forceinline__ void shrink_body(const ApplyArgs& a, int b, int c, in
         for (int m = 0; m < MT; ++m)
           if (m < mt_used) acc[m] = mfma16(af[st][m], xf[st], acc[m]);
     }
+    if (tt == 0) trace_stamp(a, 2);
     // Reduce the four waves' d-slices through LDS (fixed order) and store
     // the tile's partial, coherently.
 #pragma unroll
@@ -375,6 +399,7 @@ __device__ __forceinline__ void shrink_body(const ApplyArgs& a, int b, int c, in
     }
     __syncthreads();
   }
+  trace_stamp(a, 3);
 }
 
 // ---------------------------------------------------------------- reduce ----
@@ -758,6 +783,7 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
   V8 bf[kOT][KS];
   YRows yq;
   load_chunk<T, RANK>(a, cur, tok0, bf, yq);
+  trace_stamp(a, 2);
 
   bool go = cur.res.ptr != nullptr;
   unsigned consumed_prev = 0;
@@ -769,6 +795,7 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
       // larger blocks and for the single-slice kernel (measured on MI355X).
       go = (ROLE == kFused || blk.count * wrote_all * a.n_chunks > 2048) ? wait_partials<PA>(a, blk, wrote, s_flag)
                                                                           : true;
+      trace_stamp(a, 3);
       if (go) {
         const auto to_lds = [&](int j, int r0, f32x2 v) {
           typename VecOf<T>::v2 o;
@@ -791,6 +818,7 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
       await_partials(a, blk, wrote_all);
     }
     __syncthreads();
+    trace_stamp(a, 4);
     // This workgroup has read everything it needs from the partials; the
     // count's latency hides behind the MFMAs.
     if (threadIdx.x == 0) consumed_prev = atomic_add_u(&a.consumed[b * kCounterStride], 1u);
@@ -844,6 +872,7 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
     }
   }
 
+  trace_stamp(a, 5);
   if constexpr (kFusedRole) {
     // The last expand workgroup of the block to finish reading (every other
     // one has counted) empties the block's partials and resets the counter.
@@ -923,6 +952,7 @@ void apply_kernel(const uint32_t* header, const Block* __restrict__ blocks,
   using SM = SharedMem<T, RANK>;
   __shared__ SM smem;
   __shared__ int s_flag;
+  trace_stamp(a, 0);
   f32x4* s_red = smem.buf;
   T* s_h = reinterpret_cast<T*>(smem.buf);
   const int S = ROLE == kExpandOnly ? 0 : n_shrink;
@@ -954,6 +984,8 @@ void apply_kernel(const uint32_t* header, const Block* __restrict__ blocks,
     flag_error(a.plan.header, kErrCapacity);
   if ((b >= n_blocks) | (blk.count <= 0) | (tok0 < -1) | (poison != 0u)) return;
   const int32_t t0 = row < blk.count ? tok0 : -1;
+  trace_stamp(a, 1);
+  trace_tag(a, (shrink_role ? 1u : 2u) | (static_cast<uint64_t>(b) << 8));
 
   if (shrink_role) {
     // part = (A slice, rank group, d-range), d-range fastest.
@@ -1227,18 +1259,24 @@ hipError_t launch_rank(const ApplyArgs& a, hipStream_t stream) {
   const int32_t per_shrink = a.n_chunks * a.n_rgroups * a.w.n_a;
   const int32_t per_block = (a.n_ochunks + a.n_sub - 1) / a.n_sub;
   const int32_t ns = static_cast<int32_t>(S);
+  ApplyArgs at;
+  if (a.trace != nullptr && n * kTraceWords > a.trace_words) {
+    at = a;
+    at.trace = nullptr;
+  }
+  const ApplyArgs& a2 = (a.trace != nullptr && n * kTraceWords > a.trace_words) ? at : a;
   if constexpr (ROLE == kShrinkOnly) {
     // Its shrink side takes the rank from each block's adapter.
-    launch_kernel<T, 0, ROLE, TILES>(a, grid, per_shrink, ns, per_block, stream);
+    launch_kernel<T, 0, ROLE, TILES>(a2, grid, per_shrink, ns, per_block, stream);
   } else {
     switch (a.rank) {
       case 0:  // mixed ranks (registered adapters): each block's adapter decides
-        launch_kernel<T, 0, ROLE, TILES>(a, grid, per_shrink, ns, per_block, stream);
+        launch_kernel<T, 0, ROLE, TILES>(a2, grid, per_shrink, ns, per_block, stream);
         break;
-      case 8: launch_kernel<T, 8, ROLE, TILES>(a, grid, per_shrink, ns, per_block, stream); break;
-      case 16: launch_kernel<T, 16, ROLE, TILES>(a, grid, per_shrink, ns, per_block, stream); break;
-      case 32: launch_kernel<T, 32, ROLE, TILES>(a, grid, per_shrink, ns, per_block, stream); break;
-      case 64: launch_kernel<T, 64, ROLE, TILES>(a, grid, per_shrink, ns, per_block, stream); break;
+      case 8: launch_kernel<T, 8, ROLE, TILES>(a2, grid, per_shrink, ns, per_block, stream); break;
+      case 16: launch_kernel<T, 16, ROLE, TILES>(a2, grid, per_shrink, ns, per_block, stream); break;
+      case 32: launch_kernel<T, 32, ROLE, TILES>(a2, grid, per_shrink, ns, per_block, stream); break;
+      case 64: launch_kernel<T, 64, ROLE, TILES>(a2, grid, per_shrink, ns, per_block, stream); break;
       default: return hipErrorInvalidValue;
     }
   }
@@ -1270,6 +1308,11 @@ hipError_t launch_fill_u32(uint32_t* p, uint32_t v, size_t n, hipStream_t stream
 }
 
 int expand_cols_per_workgroup() { return kOC; }
+#ifdef WP_TRACE
+int traced_build() { return 1; }
+#else
+int traced_build() { return 0; }
+#endif
 int fused_waves_per_simd(int rank, int multi) {
   const bool wide = rank == 0 || rank == 64;
   if (multi) return wide ? waves_per_simd<64, kFusedMulti, 1>() : waves_per_simd<32, kFusedMulti, 1>();

@@ -80,7 +80,7 @@ struct Adapter {
   void* dA = nullptr;    // device copies (pool)
   void* dB = nullptr;
   void* host = nullptr;  // host-resident adapters: one pinned allocation, A then B
-  void* hA = nullptr;
+  void* hA = nullptr;    // ... and its A and B as the device addresses them
   void* hB = nullptr;
   size_t a_bytes = 0, b_bytes = 0;
   hipEvent_t copied = nullptr;  // recorded after the registration copy
@@ -90,16 +90,19 @@ struct Adapter {
 // once the copy has landed, the prefetch stream publishes the slot's entry
 // (SlotPub); the next plan build -- or an eager call that finds the slot ready
 // -- writes it into the table; a release writes the adapter's registered
-// entry back on the caller's stream, and the slot's next copy waits for that.
+// entry back on the caller's stream and hands the buffers to the engine's
+// free list behind an event recorded there.  A prefetch takes a free buffer
+// whose event has completed (a host query) or a new one from the pool, so a
+// copy never waits for the caller's stream: that wait -- a side stream
+// waiting on an event of the stream that replays the step -- measured ~70 us
+// per step on MI355X, and a stream-ordered free ~170 us of host time.
 struct Slot {
   int32_t adapter = -1;
   void* A = nullptr;
   void* B = nullptr;
-  size_t cap_a = 0, cap_b = 0;
+  size_t a_bytes = 0, b_bytes = 0;  // sizes of A and B
   hipEvent_t ready = nullptr;     // prefetch stream: copy and publication done
-  hipEvent_t released = nullptr;  // caller's stream: the registered entry is back
   bool issued = false;
-  bool release_pending = false;   // `released` recorded and not yet waited for by a copy
   bool applied = false;           // an eager call has enqueued the table write of the publication
 };
 
@@ -183,6 +186,17 @@ struct wp_engine {
   // Pinned host copies of evicted adapters, freed once the prefetch stream
   // has passed the recorded event (a copy may still read them).
   std::vector<std::pair<void*, hipEvent_t>> host_graveyard;
+  // Released slot buffers: reusable once `after` (recorded on the releasing
+  // stream behind the release) has completed.  Events are shared by the
+  // buffers of one release batch (event_refs) and recycled.
+  struct FreeBuf {
+    void* ptr;
+    size_t bytes;
+    hipEvent_t after;
+  };
+  std::vector<FreeBuf> free_bufs;
+  std::vector<hipEvent_t> spare_events;
+  std::unordered_map<hipEvent_t, int> event_refs;
 
   // Workspace (one allocation).
   char* ws = nullptr;
@@ -206,6 +220,8 @@ struct wp_engine {
   int32_t entry_offset = 0;  // table-mode calls on device-built plans read dtable + entry_offset
   int32_t entry_count = 0;   // ... and at most this many entries (0: to the table's end)
   uint32_t spin_limit = kDefaultSpinLimit;
+  uint64_t* trace = nullptr;  // traced builds: per-workgroup timestamps of fused launches
+  int64_t trace_words = 0;
 
   char* pinned[kUploadRing] = {};
   hipEvent_t upload_done[kUploadRing] = {};
@@ -334,42 +350,91 @@ void invalidate_host_plan_for(wp_engine* e, int32_t id) {
     }
 }
 
-// Frees slot s, on `stream`: once its copy has landed, the publication is
-// emptied and the adapter's registered entry written back into the table and
-// into the current host-built plan, so kernels enqueued after this never read
-// the slot; `released` marks that point for the slot's next copy.  Kernels
-// enqueued before it on `stream` (graph replays included) finish first.
-int release_slot_on(wp_engine* e, int s, hipStream_t stream) {
-  if (s < 0) return WP_OK;
-  Slot& sl = e->slots[s];
-  if (sl.adapter < 0) return WP_OK;
-  if (sl.issued) WP_HIP(hipStreamWaitEvent(stream, sl.ready, 0));
-  EntryWrites w{};
-  w.pub = e->pubs + s;
-  w.pub_id = -1;
-  Entry reg{};
-  auto it = e->adapters.find(sl.adapter);
-  if (it != e->adapters.end()) reg = registered_entry(it->second);
-  if (sl.adapter < e->table_cap) {
-    w.dst[w.n] = e->dtable + sl.adapter;
-    w.val[w.n++] = reg;
-  }
-  if (e->plan_kind == 1)
-    for (size_t k = 0; k < e->plan_entry_slot.size(); ++k)
-      if (e->plan_entry_slot[k] == s) {
-        // A slot holds one adapter, which a host-built plan lists once.
-        if (w.n < kMaxEntryWrites) {
-          w.dst[w.n] = e->plan_entries + k;
-          w.val[w.n++] = reg;
-        }
-        e->plan_entry_slot[k] = -1;
+// Frees slots, on `stream`: once a slot's copy has landed, its publication
+// is emptied and the adapter's registered entry written back into the table
+// and into the current host-built plan, so kernels enqueued after this never
+// read the slot, and then its buffers are freed on `stream`.  Kernels
+// enqueued before it on `stream` (graph replays included) finish first.  One
+// entry-write launch for up to kMaxEntryWrites / 2 slots.
+int release_slots_on(wp_engine* e, const int* slot_ids, int n, hipStream_t stream) {
+  int done = 0;
+  while (done < n) {
+    EntryWrites w{};
+    std::vector<int> batch;
+    for (; done < n && w.n + 2 <= kMaxEntryWrites; ++done) {
+      const int s = slot_ids[done];
+      if (s < 0 || e->slots[s].adapter < 0) continue;
+      Slot& sl = e->slots[s];
+      if (sl.issued && hipEventQuery(sl.ready) != hipSuccess) WP_HIP(hipStreamWaitEvent(stream, sl.ready, 0));
+      w.clear[w.n_clear++] = e->pubs + s;
+      Entry reg{};
+      auto it = e->adapters.find(sl.adapter);
+      if (it != e->adapters.end()) reg = registered_entry(it->second);
+      if (sl.adapter < e->table_cap) {
+        w.dst[w.n] = e->dtable + sl.adapter;
+        w.val[w.n++] = reg;
       }
-  WP_HIP(launch_entry_writes(w, stream));
-  WP_HIP(hipEventRecord(sl.released, stream));
-  sl.release_pending = true;
-  sl.adapter = -1;
-  sl.issued = false;
-  sl.applied = false;
+      if (e->plan_kind == 1)
+        for (size_t k = 0; k < e->plan_entry_slot.size(); ++k)
+          if (e->plan_entry_slot[k] == s) {
+            // A slot holds one adapter, which a host-built plan lists once.
+            w.dst[w.n] = e->plan_entries + k;
+            w.val[w.n++] = reg;
+            e->plan_entry_slot[k] = -1;
+          }
+      sl.adapter = -1;
+      sl.issued = false;
+      sl.applied = false;
+      batch.push_back(s);
+    }
+    if (batch.empty()) continue;
+    WP_HIP(launch_entry_writes(w, stream));
+    // The batch's buffers go to the free list behind one event.
+    hipEvent_t ev = nullptr;
+    if (!e->spare_events.empty()) {
+      ev = e->spare_events.back();
+      e->spare_events.pop_back();
+    } else {
+      WP_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+    }
+    WP_HIP(hipEventRecord(ev, stream));
+    int refs = 0;
+    for (int s : batch) {
+      Slot& sl = e->slots[s];
+      if (sl.A) e->free_bufs.push_back({sl.A, sl.a_bytes, ev}), ++refs;
+      if (sl.B) e->free_bufs.push_back({sl.B, sl.b_bytes, ev}), ++refs;
+      sl.A = sl.B = nullptr;
+    }
+    if (refs > 0) e->event_refs[ev] = refs;
+    else e->spare_events.push_back(ev);
+  }
+  return WP_OK;
+}
+
+int release_slot_on(wp_engine* e, int s, hipStream_t stream) { return release_slots_on(e, &s, 1, stream); }
+
+// A slot buffer of at least `bytes`: the smallest free one whose release has
+// completed, else a new pool allocation on the prefetch stream.
+int take_slot_buffer(wp_engine* e, size_t bytes, void** out) {
+  int best = -1;
+  for (size_t i = 0; i < e->free_bufs.size(); ++i) {
+    const auto& f = e->free_bufs[i];
+    if (f.bytes < bytes || (best >= 0 && f.bytes >= e->free_bufs[best].bytes)) continue;
+    if (hipEventQuery(f.after) != hipSuccess) continue;
+    best = static_cast<int>(i);
+  }
+  if (best < 0) {
+    WP_HIP(hipMallocFromPoolAsync(out, bytes, e->pool, e->pstream));
+    return WP_OK;
+  }
+  *out = e->free_bufs[best].ptr;
+  hipEvent_t ev = e->free_bufs[best].after;
+  e->free_bufs[best] = e->free_bufs.back();
+  e->free_bufs.pop_back();
+  if (--e->event_refs[ev] == 0) {
+    e->event_refs.erase(ev);
+    e->spare_events.push_back(ev);
+  }
   return WP_OK;
 }
 
@@ -420,6 +485,8 @@ ApplyArgs base_args(const wp_engine* e, int rank) {
   a.part = e->part;
   a.consumed = e->consumed;
   a.spin_limit = e->spin_limit;
+  a.trace = e->trace;
+  a.trace_words = e->trace_words;
   a.plan = plan_view(e);
   return a;
 }
@@ -510,6 +577,12 @@ int wp_create(const wp_config* cfg_in, wp_engine** out) {
     return bail(fail(WP_ERR_HIP, "wp_create: hipMemPoolCreate failed"));
   uint64_t keep = ~0ull;
   (void)hipMemPoolSetAttribute(e->pool, hipMemPoolAttrReleaseThreshold, &keep);
+  // A block freed on one stream is reused by another only once the free has
+  // completed; the pool never makes a stream wait for another's frees.
+  int no = 0, yes = 1;
+  (void)hipMemPoolSetAttribute(e->pool, hipMemPoolReuseAllowInternalDependencies, &no);
+  (void)hipMemPoolSetAttribute(e->pool, hipMemPoolReuseFollowEventDependencies, &no);
+  (void)hipMemPoolSetAttribute(e->pool, hipMemPoolReuseAllowOpportunistic, &yes);
 
   e->tok_cap = cfg.max_tokens;
   e->seg_cap = std::max(cfg.max_tokens, kRefMaxSegments);
@@ -587,8 +660,7 @@ int wp_create(const wp_config* cfg_in, wp_engine** out) {
     return bail(fail(WP_ERR_HIP, "wp_create: prefetch stream warm-up copy failed"));
   e->slots.resize(cfg.num_staging_slots);
   for (auto& s : e->slots) {
-    if (hipEventCreateWithFlags(&s.ready, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&s.released, hipEventDisableTiming) != hipSuccess)
+    if (hipEventCreateWithFlags(&s.ready, hipEventDisableTiming) != hipSuccess)
       return bail(fail(WP_ERR_HIP, "wp_create: slot event creation failed"));
   }
   *out = e;
@@ -607,11 +679,13 @@ int wp_destroy(wp_engine* e) {
     if (ad.copied) (void)hipEventDestroy(ad.copied);
   }
   sweep_graveyard(e, true);
+  for (auto& f : e->free_bufs) (void)hipFree(f.ptr);
+  for (auto& kv : e->event_refs) (void)hipEventDestroy(kv.first);
+  for (hipEvent_t ev : e->spare_events) (void)hipEventDestroy(ev);
   for (auto& s : e->slots) {
     if (s.A) (void)hipFree(s.A);
     if (s.B) (void)hipFree(s.B);
     if (s.ready) (void)hipEventDestroy(s.ready);
-    if (s.released) (void)hipEventDestroy(s.released);
   }
   if (e->ws) (void)hipFree(e->ws);
   for (int i = 0; i < kUploadRing; ++i) {
@@ -651,12 +725,15 @@ int wp_register_adapter(wp_engine* e, int32_t adapter_id, const void* A, const v
   ad.a_bytes = sizeof(uint16_t) * static_cast<size_t>(rank) * d_model;
   ad.b_bytes = sizeof(uint16_t) * static_cast<size_t>(out_features) * rank;
   if (host_resident) {
+    // Pinned and mapped: the staging copy kernel reads it directly.
     const size_t a_span = (ad.a_bytes + 255) & ~size_t(255);
-    WP_HIP(hipHostMalloc(&ad.host, a_span + ad.b_bytes, hipHostMallocDefault));
-    ad.hA = ad.host;
-    ad.hB = static_cast<char*>(ad.host) + a_span;
-    std::memcpy(ad.hA, A, ad.a_bytes);
-    std::memcpy(ad.hB, B, ad.b_bytes);
+    WP_HIP(hipHostMalloc(&ad.host, a_span + ad.b_bytes, hipHostMallocMapped));
+    std::memcpy(ad.host, A, ad.a_bytes);
+    std::memcpy(static_cast<char*>(ad.host) + a_span, B, ad.b_bytes);
+    void* dev = nullptr;
+    WP_HIP(hipHostGetDevicePointer(&dev, ad.host, 0));
+    ad.hA = dev;
+    ad.hB = static_cast<char*>(dev) + a_span;
   } else {
     WP_HIP(hipMallocFromPoolAsync(&ad.dA, ad.a_bytes, e->pool, stream));
     WP_HIP(hipMallocFromPoolAsync(&ad.dB, ad.b_bytes, e->pool, stream));
@@ -1154,6 +1231,8 @@ int add_lora_impl(wp_engine* e, const char* who, void* y, const void* x, int32_t
   a.part = e->part;
   a.consumed = e->consumed;
   a.spin_limit = e->spin_limit;
+  a.trace = e->trace;
+  a.trace_words = e->trace_words;
   a.plan = plan_view(e);
   a.n_slots = block_bound(e, num_loras);
   fused_split(&a, rank, d_model, e->n_cu);
@@ -1383,67 +1462,79 @@ int wp_add_lora_static(void* y, const void* x, const void* idx, int32_t idx_is_i
   return WP_OK;
 }
 
-int wp_prefetch_adapter(wp_engine* e, int32_t adapter_id, int32_t* slot_out) {
-  if (!e || !slot_out) return fail(WP_ERR_INVALID, "prefetch_adapter: null argument");
-  *slot_out = -1;
-  auto it = e->adapters.find(adapter_id);
-  if (it == e->adapters.end()) return WP_OK;
-  // Existing slot for the id, else the first free one, else none
-  // (reference: StagingBufferPool::acquire_slot, staging_buffer.h:62-73).  A
-  // slot that already holds the id holds its current weights (registering
-  // the id again releases the slot), so nothing is copied again.
-  int s = find_slot(e, adapter_id);
-  if (s >= 0) {
-    *slot_out = s;
-    return WP_OK;
-  }
-  for (size_t i = 0; i < e->slots.size(); ++i)
-    if (e->slots[i].adapter < 0) {
-      s = static_cast<int>(i);
-      break;
-    }
-  if (s < 0) return WP_OK;
+int wp_prefetch_adapters(wp_engine* e, const int32_t* adapter_ids, int32_t n, int32_t* slots_out) {
+  if (!e || (n > 0 && (!adapter_ids || !slots_out))) return fail(WP_ERR_INVALID, "prefetch_adapters: null argument");
   DeviceGuard g(e->device);
-  Slot& sl = e->slots[s];
-  const Adapter& ad = it->second;
-  // The slot's last release (and with it every kernel enqueued before it on
-  // the releasing stream) comes first; so does the registration copy.
-  if (sl.release_pending) {
-    WP_HIP(hipStreamWaitEvent(e->pstream, sl.released, 0));
-    sl.release_pending = false;
+  StageJobs jobs{};
+  std::vector<int> job_slot;
+  auto flush = [&]() -> int {
+    if (jobs.n == 0) return WP_OK;
+    WP_HIP(launch_stage_copies(jobs, e->pstream));
+    for (int s : job_slot) WP_HIP(hipEventRecord(e->slots[s].ready, e->pstream));
+    jobs.n = 0;
+    job_slot.clear();
+    return WP_OK;
+  };
+  for (int k = 0; k < n; ++k) {
+    slots_out[k] = -1;
+    auto it = e->adapters.find(adapter_ids[k]);
+    if (it == e->adapters.end()) continue;
+    // Existing slot for the id, else the first free one, else none
+    // (reference: StagingBufferPool::acquire_slot, staging_buffer.h:62-73).
+    // A slot that already holds the id holds its current weights
+    // (registering the id again releases the slot): nothing is copied again.
+    int s = find_slot(e, adapter_ids[k]);
+    if (s >= 0) {
+      slots_out[k] = s;
+      continue;
+    }
+    for (size_t i = 0; i < e->slots.size(); ++i)
+      if (e->slots[i].adapter < 0) {
+        s = static_cast<int>(i);
+        break;
+      }
+    if (s < 0) continue;
+    Slot& sl = e->slots[s];
+    const Adapter& ad = it->second;
+    // The registration copy comes first (a device-side wait only if it has
+    // not completed yet); buffers nobody reads any more.
+    if (ad.copied && hipEventQuery(ad.copied) != hipSuccess) WP_HIP(hipStreamWaitEvent(e->pstream, ad.copied, 0));
+    int rcb = take_slot_buffer(e, ad.a_bytes, &sl.A);
+    if (rcb == WP_OK) rcb = take_slot_buffer(e, ad.b_bytes, &sl.B);
+    if (rcb != WP_OK) return rcb;
+    sl.a_bytes = ad.a_bytes;
+    sl.b_bytes = ad.b_bytes;
+    // One copy kernel for the batch (from the pinned host store, or D2D);
+    // its last workgroup per slot publishes the slot for the next plan build.
+    StageJob& job = jobs.job[jobs.n++];
+    job.src_a = ad.hA ? ad.hA : ad.dA;
+    job.dst_a = sl.A;
+    job.a_bytes = ad.a_bytes;
+    job.src_b = ad.hB ? ad.hB : ad.dB;
+    job.dst_b = sl.B;
+    job.b_bytes = ad.b_bytes;
+    job.pub = e->pubs + s;
+    job.pub_id = adapter_ids[k];
+    job.pub_entry = staged_entry(ad, sl);
+    job_slot.push_back(s);
+    sl.adapter = adapter_ids[k];
+    sl.issued = true;
+    sl.applied = false;
+    slots_out[k] = s;
+    if (jobs.n == kMaxStageJobs) {
+      const int rc = flush();
+      if (rc != WP_OK) return rc;
+    }
   }
-  if (ad.copied) WP_HIP(hipStreamWaitEvent(e->pstream, ad.copied, 0));
-  if (sl.cap_a < ad.a_bytes) {
-    if (sl.A) WP_HIP(hipFreeAsync(sl.A, e->pstream));
-    sl.A = nullptr;
-    WP_HIP(hipMallocFromPoolAsync(&sl.A, ad.a_bytes, e->pool, e->pstream));
-    sl.cap_a = ad.a_bytes;
-  }
-  if (sl.cap_b < ad.b_bytes) {
-    if (sl.B) WP_HIP(hipFreeAsync(sl.B, e->pstream));
-    sl.B = nullptr;
-    WP_HIP(hipMallocFromPoolAsync(&sl.B, ad.b_bytes, e->pool, e->pstream));
-    sl.cap_b = ad.b_bytes;
-  }
-  const void* srcA = ad.hA ? ad.hA : ad.dA;
-  const void* srcB = ad.hB ? ad.hB : ad.dB;
-  const hipMemcpyKind kind = ad.hA ? hipMemcpyHostToDevice : hipMemcpyDeviceToDevice;
-  WP_HIP(hipMemcpyAsync(sl.A, srcA, ad.a_bytes, kind, e->pstream));
-  WP_HIP(hipMemcpyAsync(sl.B, srcB, ad.b_bytes, kind, e->pstream));
-  // Published behind the copy, in stream order: the next plan build writes it
-  // into the table.
-  EntryWrites w{};
-  w.pub = e->pubs + s;
-  w.pub_id = adapter_id;
-  w.pub_entry = staged_entry(ad, sl);
-  WP_HIP(launch_entry_writes(w, e->pstream));
-  WP_HIP(hipEventRecord(sl.ready, e->pstream));
-  sl.adapter = adapter_id;
-  sl.issued = true;
-  sl.applied = false;
-  *slot_out = s;
+  const int rc = flush();
+  if (rc != WP_OK) return rc;
   sweep_graveyard(e, false);
   return WP_OK;
+}
+
+int wp_prefetch_adapter(wp_engine* e, int32_t adapter_id, int32_t* slot_out) {
+  if (!e || !slot_out) return fail(WP_ERR_INVALID, "prefetch_adapter: null argument");
+  return wp_prefetch_adapters(e, &adapter_id, 1, slot_out);
 }
 
 int wp_is_prefetch_ready(wp_engine* e, int32_t adapter_id, int32_t* ready) {
@@ -1453,24 +1544,54 @@ int wp_is_prefetch_ready(wp_engine* e, int32_t adapter_id, int32_t* ready) {
   return WP_OK;
 }
 
-int wp_release_prefetch(wp_engine* e, int32_t adapter_id, void* stream_) {
-  if (!e) return fail(WP_ERR_INVALID, "release_prefetch: engine is NULL");
-  const int s = find_slot(e, adapter_id);
-  if (s < 0) return WP_OK;
+int wp_release_prefetches(wp_engine* e, const int32_t* adapter_ids, int32_t n, void* stream_) {
+  if (!e || (n > 0 && !adapter_ids)) return fail(WP_ERR_INVALID, "release_prefetches: null argument");
+  std::vector<int> slot_ids;
+  for (int k = 0; k < n; ++k) {
+    const int s = find_slot(e, adapter_ids[k]);
+    if (s >= 0) slot_ids.push_back(s);
+  }
+  if (slot_ids.empty()) return WP_OK;
   DeviceGuard g(e->device);
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   if (stream_capturing(stream)) return fail(WP_ERR_STATE, "release_prefetch cannot run during graph capture");
-  return release_slot_on(e, s, stream);
+  return release_slots_on(e, slot_ids.data(), static_cast<int>(slot_ids.size()), stream);
 }
 
-int wp_wait_prefetch(wp_engine* e, int32_t adapter_id, void* stream_) {
-  if (!e) return fail(WP_ERR_INVALID, "wait_prefetch: engine is NULL");
-  const int s = find_slot(e, adapter_id);
-  if (s < 0 || !e->slots[s].issued) return WP_NOT_HANDLED;
+int wp_release_prefetch(wp_engine* e, int32_t adapter_id, void* stream) {
+  if (!e) return fail(WP_ERR_INVALID, "release_prefetch: engine is NULL");
+  return wp_release_prefetches(e, &adapter_id, 1, stream);
+}
+
+int wp_wait_prefetches(wp_engine* e, const int32_t* adapter_ids, int32_t n, void* stream_) {
+  if (!e || (n > 0 && !adapter_ids)) return fail(WP_ERR_INVALID, "wait_prefetches: null argument");
   DeviceGuard g(e->device);
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   if (stream_capturing(stream)) return fail(WP_ERR_STATE, "wait_prefetch cannot run during graph capture");
-  WP_HIP(hipStreamWaitEvent(stream, e->slots[s].ready, 0));
+  int rc = WP_OK;
+  for (int k = 0; k < n; ++k) {
+    const int s = find_slot(e, adapter_ids[k]);
+    if (s < 0 || !e->slots[s].issued) {
+      rc = WP_NOT_HANDLED;
+      continue;
+    }
+    if (hipEventQuery(e->slots[s].ready) != hipSuccess) WP_HIP(hipStreamWaitEvent(stream, e->slots[s].ready, 0));
+  }
+  return rc;
+}
+
+int wp_wait_prefetch(wp_engine* e, int32_t adapter_id, void* stream) {
+  if (!e) return fail(WP_ERR_INVALID, "wait_prefetch: engine is NULL");
+  return wp_wait_prefetches(e, &adapter_id, 1, stream);
+}
+
+int wp_set_trace(wp_engine* e, void* buffer, int64_t n_words) {
+  if (!e) return fail(WP_ERR_INVALID, "set_trace: engine is NULL");
+  if (!traced_build()) return fail(WP_ERR_STATE, "set_trace: this library was built without WP_TRACE");
+  if (buffer != nullptr && (n_words <= 0 || !aligned(buffer, 8)))
+    return fail(WP_ERR_INVALID, "set_trace: a device buffer of n_words 8-byte words");
+  e->trace = static_cast<uint64_t*>(buffer);
+  e->trace_words = buffer != nullptr ? n_words : 0;
   return WP_OK;
 }
 

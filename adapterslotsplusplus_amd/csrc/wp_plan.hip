@@ -136,24 +136,68 @@ __global__ __launch_bounds__(256) void maintain_kernel(uint32_t* header, Maint m
   maintain(header, m, &s_flag);
 }
 
-// One wave; thread 0 writes.  The publication follows the sequence-lock
-// protocol: odd sequence, payload, even sequence, with agent-scope release
-// fences between, so a reader that saw the same even value before and after
-// its payload loads has a whole payload.
+// A publication under its sequence lock: odd sequence, payload, even
+// sequence, with agent-scope release fences between, so a reader that saw
+// the same even value before and after its payload loads has a whole payload.
+// One thread.
+__device__ void publish(SlotPub* pub, int32_t id, const Entry& en) {
+  const uint32_t base = __hip_atomic_load(&pub->seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & ~1u;
+  __hip_atomic_store(&pub->seq, base + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __hip_atomic_store(&pub->id, id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    agent_store64(reinterpret_cast<uint64_t*>(&pub->entry) + i, reinterpret_cast<const uint64_t*>(&en)[i]);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __hip_atomic_store(&pub->seq, base + 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One wave; thread 0 writes.
 __global__ __launch_bounds__(64) void entry_writes_kernel(EntryWrites w) {
   if (threadIdx.x != 0) return;
-  if (w.pub != nullptr) {
-    const uint32_t base = __hip_atomic_load(&w.pub->seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & ~1u;
-    __hip_atomic_store(&w.pub->seq, base + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    __hip_atomic_store(&w.pub->id, w.pub_id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      agent_store64(reinterpret_cast<uint64_t*>(&w.pub->entry) + i, reinterpret_cast<const uint64_t*>(&w.pub_entry)[i]);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    __hip_atomic_store(&w.pub->seq, base + 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  if (w.pub != nullptr) publish(w.pub, w.pub_id, w.pub_entry);
+  for (int i = 0; i < w.n_clear; ++i) publish(w.clear[i], -1, Entry{});
   for (int i = 0; i < w.n; ++i) *w.dst[i] = w.val[i];
+}
+
+// Workgroup (job, part) copies its share of the job's A and B in 16-byte
+// units; every workgroup's stores complete before it counts itself done, and
+// the job's last workgroup publishes the slot.
+__global__ __launch_bounds__(256) void stage_copy_kernel(StageJobs jobs) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const int j = blockIdx.x / kStageWorkgroups;
+  const int part = blockIdx.x - j * kStageWorkgroups;
+  const StageJob& job = jobs.job[j];
+  const uint64_t stride = static_cast<uint64_t>(kStageWorkgroups) * blockDim.x;
+  const uint64_t first = static_cast<uint64_t>(part) * blockDim.x + threadIdx.x;
+  for (int m = 0; m < 2; ++m) {
+    const u32x4* src = static_cast<const u32x4*>(m == 0 ? job.src_a : job.src_b);
+    u32x4* dst = static_cast<u32x4*>(m == 0 ? job.dst_a : job.dst_b);
+    const uint64_t n = (m == 0 ? job.a_bytes : job.b_bytes) / 16;
+    // Four loads in flight per thread.
+    uint64_t i = first;
+    for (; i + 3 * stride < n; i += 4 * stride) {
+      const u32x4 v0 = src[i], v1 = src[i + stride], v2 = src[i + 2 * stride], v3 = src[i + 3 * stride];
+      dst[i] = v0;
+      dst[i + stride] = v1;
+      dst[i + 2 * stride] = v2;
+      dst[i + 3 * stride] = v3;
+    }
+    for (; i < n; i += stride) dst[i] = src[i];
+  }
+  __shared__ int s_last;
+  // Release: this workgroup's stores are visible device-wide before its count.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t done = __hip_atomic_fetch_add(&job.pub->pad[0], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = done == kStageWorkgroups - 1 ? 1 : 0;
+  }
+  __syncthreads();
+  if (s_last != 0 && threadIdx.x == 0) {
+    __hip_atomic_store(&job.pub->pad[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    publish(job.pub, job.pub_id, job.pub_entry);
+  }
 }
 
 // Runs sorted by counting (below) when there are at most kRankMax of them and
@@ -474,8 +518,18 @@ hipError_t launch_maintain(uint32_t* header, const Maint& m, hipStream_t stream)
 }
 
 hipError_t launch_entry_writes(const EntryWrites& w, hipStream_t stream) {
-  if (w.n < 0 || w.n > kMaxEntryWrites) return hipErrorInvalidValue;
+  if (w.n < 0 || w.n > kMaxEntryWrites || w.n_clear < 0 || w.n_clear > kMaxEntryWrites) return hipErrorInvalidValue;
   entry_writes_kernel<<<1, 64, 0, stream>>>(w);
+  return hipGetLastError();
+}
+
+hipError_t launch_stage_copies(const StageJobs& jobs, hipStream_t stream) {
+  if (jobs.n < 0 || jobs.n > kMaxStageJobs) return hipErrorInvalidValue;
+  for (int j = 0; j < jobs.n; ++j)
+    if (jobs.job[j].pub == nullptr || jobs.job[j].a_bytes % 16 != 0 || jobs.job[j].b_bytes % 16 != 0)
+      return hipErrorInvalidValue;
+  if (jobs.n == 0) return hipSuccess;
+  stage_copy_kernel<<<jobs.n * kStageWorkgroups, 256, 0, stream>>>(jobs);
   return hipGetLastError();
 }
 

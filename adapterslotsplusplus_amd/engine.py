@@ -418,6 +418,29 @@ class WarpPipeEngine:
                    "prefetch_adapter")
         return int(slot.value)
 
+    def prefetch_adapters(self, adapter_ids, layer=None) -> List[int]:
+        """prefetch_adapter for several ids in one call (one copy kernel);
+        returns their slots (-1 where none)."""
+        ids = [self._store_id(a, layer) for a in adapter_ids]
+        n = len(ids)
+        arr = (ctypes.c_int32 * max(n, 1))(*ids)
+        out = (ctypes.c_int32 * max(n, 1))()
+        _lib.check(self._lib.wp_prefetch_adapters(self._handle, arr, n, out), "prefetch_adapters")
+        return [int(out[k]) for k in range(n)]
+
+    def release_prefetches(self, adapter_ids, layer=None) -> None:
+        """release_prefetch for several ids in one call (one launch)."""
+        ids = [self._store_id(a, layer) for a in adapter_ids]
+        arr = (ctypes.c_int32 * max(len(ids), 1))(*ids)
+        _lib.check(self._lib.wp_release_prefetches(self._handle, arr, len(ids), self._stream()), "release_prefetch")
+
+    def wait_prefetches(self, adapter_ids, layer=None) -> bool:
+        """wait_prefetch for several ids in one call; False if any holds no slot."""
+        ids = [self._store_id(a, layer) for a in adapter_ids]
+        arr = (ctypes.c_int32 * max(len(ids), 1))(*ids)
+        rc = _lib.check(self._lib.wp_wait_prefetches(self._handle, arr, len(ids), self._stream()), "wait_prefetch")
+        return rc == _lib.WP_OK
+
     def is_prefetch_ready(self, adapter_id, layer=None) -> bool:
         r = ctypes.c_int32(0)
         _lib.check(self._lib.wp_is_prefetch_ready(self._handle, self._store_id(adapter_id, layer), ctypes.byref(r)),

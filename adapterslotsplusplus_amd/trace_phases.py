@@ -1,0 +1,145 @@
+"""Phase breakdown of the fused decode kernels, from a traced build.
+
+    python -m adapterslotsplusplus_amd.build --trace
+    python -m adapterslotsplusplus_amd.trace_phases [--call o_proj|qkv|cfg5_o] [--out FILE]
+
+The traced library (-DWP_TRACE) records, per workgroup, the 100 MHz
+real-time counter at the phase boundaries of one fused launch (thread 0,
+after waiting for wave 0's memory operations, which perturbs the timing a
+little): entry, plan loaded; shrink workgroups: first token tile's MFMAs done,
+partials stored and acknowledged; expand workgroups: B and Y loaded, gate
+open, partials collected, Y stored.  This script runs the cfg2 decode step's
+calls over 40 layers of distinct weights (so the traced call's weights are
+not in the caches), traces one call of the last layer, and prints a markdown
+table of each phase's duration (median, p10, p90 over workgroups) and of the
+times, from the first workgroup's entry, at which each role reaches each
+stamp; the same call's duration from HIP events on the normal library is
+measured separately by bench.py.
+"""
+from __future__ import annotations
+
+import argparse
+import os
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def _pct(v, q):
+    v = sorted(v)
+    if not v:
+        return float("nan")
+    i = min(len(v) - 1, max(0, int(round(q * (len(v) - 1)))))
+    return v[i]
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--call", default="o_proj", choices=["o_proj", "qkv", "cfg5_o"])
+    ap.add_argument("--out", default=None)
+    args = ap.parse_args(argv)
+    from . import build as wp_build
+
+    if not os.path.exists(wp_build.TRACE_LIB_PATH):
+        raise SystemExit("build the traced library first: python -m adapterslotsplusplus_amd.build --trace")
+    import torch
+
+    from . import _lib, workloads as wl
+    from .engine import WarpPipeEngine
+
+    # The library is loaded when the first engine is created: point it at the
+    # traced build before that.
+    if _lib._lib is not None and _lib.LIB_PATH != wp_build.TRACE_LIB_PATH:
+        raise SystemExit("the normal library is already loaded in this process")
+    _lib.LIB_PATH = wp_build.TRACE_LIB_PATH
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    if args.call == "cfg5_o":
+        T, L, r, h, n_layers = 128, 32, 32, 2048, 40
+        idx = torch.repeat_interleave(torch.arange(L), 4).to(dev)
+    else:
+        c = wl.CFG2
+        T, L, r, h, n_layers = c["T"], c["n_adapters"], c["rank"], c["hidden"], 40
+        idx = wl.zipf_indices(T, L, c["zipf_s"], c["routing_seed"]).to(dev)
+    dt = torch.bfloat16
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(77)
+
+    def rn(shape, std):
+        return (torch.randn(*shape, generator=gen, device=dev, dtype=torch.float32) * std).to(dt)
+
+    n_slices = 3 if args.call == "qkv" else 1
+    layers = [dict(wa=rn((L, 1, r, h), .02), wb=[rn((L, 1, h, r), .02) for _ in range(n_slices)],
+                   x=rn((T, h), 1.), y=rn((T, n_slices * h), 1.)) for _ in range(n_layers)]
+    engine = WarpPipeEngine()
+    lib = _lib.load()
+    words = 1 << 20
+    buf = torch.zeros(words, dtype=torch.int64, device=dev)
+    assert engine.build_seg_bounds(idx)
+    offs = [k * h for k in range(n_slices)]
+
+    def call(ly):
+        engine.add_lora_slices(ly["y"], ly["x"], ly["wa"], ly["wb"], 0.5, offs)
+
+    for ly in layers:
+        call(ly)
+    torch.cuda.synchronize()
+    for ly in layers[:-1]:
+        call(ly)
+    torch.cuda.synchronize()
+    _lib.check(lib.wp_set_trace(engine._handle, buf.data_ptr(), words), "set_trace")
+    call(layers[-1])
+    torch.cuda.synchronize()
+    _lib.check(lib.wp_set_trace(engine._handle, None, 0), "set_trace")
+    assert engine.device_errors() == 0
+    tr = buf.view(-1, 8).cpu()
+    tags = tr[:, 7]
+    live = tags != 0
+    tr = tr[live]
+    tags = tags[live]
+    role = (tags & 0xFF).tolist()
+    t0 = int(tr[:, 0].min())
+    ticks_us = 0.01  # 100 MHz
+    rows = tr.tolist()
+    shrink = [x for x, ro in zip(rows, role) if ro == 1]
+    expand = [x for x, ro in zip(rows, role) if ro == 2]
+
+    def rel(lst, i):
+        return [(x[i] - t0) * ticks_us for x in lst if x[i] > 0]
+
+    def dur(lst, i, j):
+        return [(x[j] - x[i]) * ticks_us for x in lst if x[i] > 0 and x[j] > 0]
+
+    end = max(max(x[3] for x in shrink) if shrink else 0, max(x[5] for x in expand) if expand else 0)
+    lines = [f"### Phases of one `{args.call}` call (T={T}, {L} resident adapters, r={r}, h={h}, bf16, "
+             f"{n_layers} layers of distinct weights; traced build)", "",
+             f"Workgroups with work: {len(shrink)} shrink, {len(expand)} expand; first entry to last stamp "
+             f"{(end - t0) * ticks_us:.2f} us.", "",
+             "| role | phase | median us | p10 | p90 |", "|---|---|---|---|---|"]
+
+    def row(name, phase, v):
+        lines.append(f"| {name} | {phase} | {_pct(v, .5):.2f} | {_pct(v, .1):.2f} | {_pct(v, .9):.2f} |")
+
+    row("shrink", "entry, from the first entry (dispatch)", rel(shrink, 0))
+    row("shrink", "plan loads (entry -> plan loaded)", dur(shrink, 0, 1))
+    row("shrink", "A and X stream + MFMA (-> first tile done)", dur(shrink, 1, 2))
+    row("shrink", "reduce + partial store acknowledged", dur(shrink, 2, 3))
+    row("shrink", "partials stored, from the first entry", rel(shrink, 3))
+    row("expand", "entry, from the first entry (dispatch)", rel(expand, 0))
+    row("expand", "plan loads (entry -> plan loaded)", dur(expand, 0, 1))
+    row("expand", "B and Y loads (-> landed)", dur(expand, 1, 2))
+    row("expand", "gate (-> every shrink workgroup's probe word written)", dur(expand, 2, 3))
+    row("expand", "partials collected (-> H in LDS)", dur(expand, 3, 4))
+    row("expand", "MFMA + Y store acknowledged", dur(expand, 4, 5))
+    row("expand", "gate open, from the first entry", rel(expand, 3))
+    row("expand", "Y stored, from the first entry", rel(expand, 5))
+    text = "\n".join(lines)
+    print(text)
+    if args.out:
+        with open(args.out, "w") as f:
+            f.write(text + "\n")
+
+
+if __name__ == "__main__":
+    sys.exit(main())

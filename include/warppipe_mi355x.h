@@ -219,12 +219,17 @@ int wp_add_lora_nslice(wp_engine* e, void* y, const void* x, int32_t n_slices, c
 
 /* Replaces WarpPipeExtension::prefetch_adapter (bindings:46-57): copies the
  * adapter's A and B into a staging slot on the engine's prefetch stream (H2D
- * from the pinned host store, or D2D).  Writes the slot index, or -1 when the
- * id is unknown or every slot is taken (*slot_out).  Once the copy has landed
+ * from the pinned host store, which the copy kernel reads directly, or D2D).
+ * Writes the slot index, or -1 when the id is unknown or every slot is taken
+ * (*slot_out); an id that already holds a slot keeps it (nothing is copied).  Once the copy has landed
  * the slot is published on the device; the next build_seg_bounds (captured or
  * not) puts it into the adapter table, and an eager call on a table built
  * before that picks it up when it finds the copy complete. */
 int wp_prefetch_adapter(wp_engine* e, int32_t adapter_id, int32_t* slot_out);
+
+/* prefetch_adapter for n ids in one call (no reference counterpart): one copy
+ * kernel for the batch.  slots_out[k] as wp_prefetch_adapter's *slot_out. */
+int wp_prefetch_adapters(wp_engine* e, const int32_t* adapter_ids, int32_t n, int32_t* slots_out);
 
 /* Replaces is_prefetch_ready (bindings:59-62): *ready = 1 once the copy completed. */
 int wp_is_prefetch_ready(wp_engine* e, int32_t adapter_id, int32_t* ready);
@@ -237,10 +242,17 @@ int wp_is_prefetch_ready(wp_engine* e, int32_t adapter_id, int32_t* ready);
  * once (staging_buffer.h:75-79). */
 int wp_release_prefetch(wp_engine* e, int32_t adapter_id, void* stream);
 
+/* wp_release_prefetch for n ids in one call (no reference counterpart). */
+int wp_release_prefetches(wp_engine* e, const int32_t* adapter_ids, int32_t n, void* stream);
+
 /* No reference counterpart: makes `stream` wait (on the device, no host
  * wait) until the id's prefetch copy has landed, so that a plan built next on
  * it uses the staged copy.  WP_NOT_HANDLED when the id holds no slot. */
 int wp_wait_prefetch(wp_engine* e, int32_t adapter_id, void* stream);
+
+/* wp_wait_prefetch for n ids in one call; WP_NOT_HANDLED when any holds no slot
+ * (the others are still waited for). */
+int wp_wait_prefetches(wp_engine* e, const int32_t* adapter_ids, int32_t n, void* stream);
 
 /* Test and debug: polls a wait on partials makes before it gives up (device
  * error 8, kErrSpin); 0xFFFFFFFF restores the default (131072, about 0.1 s).
@@ -248,6 +260,12 @@ int wp_wait_prefetch(wp_engine* e, int32_t adapter_id, void* stream);
  * the next build_seg_bounds / build_segments (or wp_read_device_errors) has
  * repaired the buffer. */
 int wp_set_spin_limit(wp_engine* e, uint32_t polls);
+
+/* Diagnostics: in a library built with WP_TRACE (adapterslotsplusplus_amd.build
+ * --trace), fused launches whose grid fits record 8 timestamps per workgroup
+ * into the device buffer (n_words 64-bit words; NULL stops tracing).  In a
+ * normal build: WP_ERR_STATE. */
+int wp_set_trace(wp_engine* e, void* buffer, int64_t n_words);
 
 #ifdef __cplusplus
 }

@@ -85,17 +85,25 @@ def test_captured_step_consumes_staged_adapters_between_replays():
     routes_d = [r.cuda() for r in routes]
     announce("captured step with cold adapters staged between replays")
     for s in range(n_steps):
+        # Odd steps use the per-id calls, even steps the batched ones.
         if s + 1 < n_steps:
-            slots = [engine.prefetch_adapter(a) for a in COLD[(s + 1) % 2]]
+            nxt = COLD[(s + 1) % 2]
+            slots = engine.prefetch_adapters(nxt) if s % 2 == 0 else [engine.prefetch_adapter(a) for a in nxt]
             assert all(sl >= 0 for sl in slots), f"step {s}: no free slot for the next step ({slots})"
-        for a in COLD[s % 2]:
-            assert engine.wait_prefetch(a), f"step {s}: adapter {a} holds no slot"
+        if s % 2 == 0:
+            assert engine.wait_prefetches(COLD[s % 2]), f"step {s}: a cold adapter holds no slot"
+        else:
+            for a in COLD[s % 2]:
+                assert engine.wait_prefetch(a), f"step {s}: adapter {a} holds no slot"
         idx_buf.copy_(routes_d[s])
         Y.copy_(Y0d)
         graph.replay()
         outs[s].copy_(Y)
-        for a in COLD[s % 2]:
-            engine.release_prefetch(a)
+        if s % 2 == 0:
+            engine.release_prefetches(COLD[s % 2])
+        else:
+            for a in COLD[s % 2]:
+                engine.release_prefetch(a)
     torch.cuda.synchronize()
     for s in range(n_steps):
         assert_close(outs[s], reference(adapters, X, Y0, routes[s]), f"replay {s}")
