@@ -27,6 +27,8 @@ struct ApplyArgs {
   int32_t n_slots;    // block slots of the grid (>= the plan's block count)
   int32_t hs;         // elements per H / partial row: n_a x hs1
   int32_t hs1;        // elements of one A slice's H in a row: rank, or 64 for mixed ranks
+  int32_t pad_rank;   // 1: the shrink side writes all hs1 rows of a slice, zeros past the adapter's rank
+                      // (table mode with one A per slice and mixed ranks: every slice's partial has one width)
   int32_t ptok;       // rows per chunk of `part` (plan positions)
   float* part;        // fp32 partial H by plan position: [n_chunks][ptok][hs], kPartialEmpty between calls
   uint32_t* consumed; // per block (stride kCounterStride): fused calls count expand workgroups done reading,

@@ -249,8 +249,10 @@ struct Resolved {
   uint32_t err = 0;
 };
 
-// A of A-slice sa (0 when every output slice shares one A).
-template <typename T>
+// A of A-slice sa (0 when every output slice shares one A).  TS: table mode
+// with one adapter per slice (each slice's entries at its own offset; other
+// table calls fold their one offset into a.w.entries).
+template <typename T, bool TS = false>
 __device__ __forceinline__ Resolved<T> resolve_a(const ApplyArgs& a, const Block& blk, int sa = 0) {
   Resolved<T> r;
   if (a.w.mode == kStacked) {
@@ -267,7 +269,7 @@ __device__ __forceinline__ Resolved<T> resolve_a(const ApplyArgs& a, const Block
     r.err = kErrUnregistered;
     return r;
   }
-  const Entry en = load_entry(a.w.entries + blk.entry);
+  const Entry en = load_entry(a.w.entries + (TS ? a.w.entry_off[sa] : 0) + blk.entry);
   const int32_t rank = entry_rank(en.rank_dtype);
   // One test over both halves, so that both loads go out before the wait.
   if ((en.a_ptr == 0) | (en.b_ptr == 0) | (rank <= 0)) {
@@ -284,7 +286,7 @@ __device__ __forceinline__ Resolved<T> resolve_a(const ApplyArgs& a, const Block
   return r;
 }
 
-template <typename T>
+template <typename T, bool TS = false>
 __device__ __forceinline__ Resolved<T> resolve_b(const ApplyArgs& a, const Block& blk, int slice) {
   Resolved<T> r;
   if (a.w.mode == kStacked) {
@@ -301,14 +303,14 @@ __device__ __forceinline__ Resolved<T> resolve_b(const ApplyArgs& a, const Block
     r.err = kErrUnregistered;
     return r;
   }
-  const Entry en = load_entry(a.w.entries + blk.entry);
+  const Entry en = load_entry(a.w.entries + (TS ? a.w.entry_off[slice] : 0) + blk.entry);
   const int32_t rank = entry_rank(en.rank_dtype);
   // One test over both halves, so that both loads go out before the wait.
   if ((en.a_ptr == 0) | (en.b_ptr == 0) | (rank <= 0)) {
     r.err = kErrUnregistered;
     return r;
   }
-  if (en.out_features != a.w.o_size[0] || (a.rank != 0 && rank != a.rank) ||
+  if (en.out_features != a.w.o_size[TS ? slice : 0] || (a.rank != 0 && rank != a.rank) ||
       (a.d_model != 0 && en.d_model != a.d_model) || entry_dtype(en.rank_dtype) != dtype_code<T>()) {
     r.err = kErrShape;
     return r;
@@ -344,8 +346,11 @@ __device__ __forceinline__ void shrink_body(const ApplyArgs& a, int b, int c, in
   const int row = lane & 15;
   const int kq = (lane >> 4) * 8;
   const int n_rows = min(16 * MT, res.rank - r_begin);
-  if (res.ptr == nullptr || n_rows <= 0) return;
-  const int mt_used = (n_rows + 15) >> 4;
+  // Zero-padded slices (a.pad_rank) store every row of the group, zeros past
+  // the adapter's rank, so that all slices' partials have one width.
+  const int store_rows = a.pad_rank ? 16 * MT : n_rows;
+  if (res.ptr == nullptr || store_rows <= 0) return;
+  const int mt_used = n_rows > 0 ? (n_rows + 15) >> 4 : 0;
   const int d = a.d_model;
   const int kw_len = a.dc / kWaves;
   const int k_begin = c * a.dc + wave * kw_len;
@@ -363,7 +368,7 @@ __device__ __forceinline__ void shrink_body(const ApplyArgs& a, int b, int c, in
     f32x4 acc[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int k = k_begin; k < k_end; k += 32 * KB) {
+    for (int k = k_begin; mt_used > 0 && k < k_end; k += 32 * KB) {
       V8 af[KB][MT];
       V8 xf[KB];
 #pragma unroll
@@ -386,11 +391,11 @@ __device__ __forceinline__ void shrink_body(const ApplyArgs& a, int b, int c, in
 #pragma unroll
     for (int m = 0; m < MT; ++m) s_red[(m * kWaves + wave) * 64 + lane] = acc[m];
     __syncthreads();
-    if (static_cast<int>(threadIdx.x) < 64 * mt_used) {
+    if (static_cast<int>(threadIdx.x) < 64 * (a.pad_rank ? MT : mt_used)) {
       const int m = threadIdx.x >> 6;
       const int tl = tt * 16 + (lane & 15);
       const int r0 = m * 16 + (lane >> 4) * 4;
-      if (tl < blk.count && r0 < n_rows) {
+      if (tl < blk.count && r0 < store_rows) {
         f32x4 sum = s_red[m * kWaves * 64 + lane];
 #pragma unroll
         for (int w = 1; w < kWaves; ++w) sum += s_red[(m * kWaves + w) * 64 + lane];
@@ -415,7 +420,8 @@ __device__ __forceinline__ bool any_empty(f32x4 v) { return is_empty(v[0]) || is
 // PA: one A per slice (more shrink workgroups than one probe per lane).
 constexpr int kProbesPerLane = 4;
 template <bool PA>
-__device__ __forceinline__ bool wait_partials(const ApplyArgs& a, const Block& blk, int rank, int* s_flag) {
+__device__ __forceinline__ bool wait_partials(const ApplyArgs& a, const Block& blk, int rank, int* s_flag,
+                                              uint32_t wmask = 1u) {
   constexpr int kProbes = PA ? kProbesPerLane : 1;
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
@@ -434,7 +440,9 @@ __device__ __forceinline__ bool wait_partials(const ApplyArgs& a, const Block& b
         const int k = i - sa * per_a;
         const int rg = k / a.n_chunks;
         const int kc = k - rg * a.n_chunks;
-        probe[q] = static_cast<uint32_t>((kc * a.ptok + blk.first) * a.hs + sa * a.hs1 + rg * a.srows);
+        // Only slices whose shrink side writes (one A per slice, table mode).
+        if (!PA || ((wmask >> sa) & 1u))
+          probe[q] = static_cast<uint32_t>((kc * a.ptok + blk.first) * a.hs + sa * a.hs1 + rg * a.srows);
       }
     }
     int ok = 1;
@@ -551,6 +559,104 @@ __device__ __forceinline__ void clear_partials(const ApplyArgs& a, const Block& 
   }
 }
 
+// One A per slice: the partial row holds n_a slices of hs1 columns; slice sa
+// (if bit sa of wmask is set: its shrink side wrote) has W columns at
+// sa * hs1 (W = the rank, or hs1 for zero-padded slices).  The same as
+// collect_partials / await_partials / clear_partials otherwise; emit gets the
+// column in the row, and each slice's alpha (alphas[sa]) is applied.
+__device__ __forceinline__ float slice_alpha(const float (&al)[kMaxSlices], int sa) {
+  return sa == 0 ? al[0] : sa == 1 ? al[1] : sa == 2 ? al[2] : al[3];
+}
+
+template <int CB, typename Emit>
+__device__ __forceinline__ void collect_partials_pa(const ApplyArgs& a, const Block& blk, int W, uint32_t wmask,
+                                                     const float (&alphas)[kMaxSlices], Emit emit) {
+  const int W2 = W / 2;
+  const int per_tok = a.w.n_a * W2;
+  const int n_units = blk.count * per_tok;
+  const int nch = a.n_chunks;
+  const uint32_t cstride = static_cast<uint32_t>(a.ptok) * static_cast<uint32_t>(a.hs) * 4u;
+  const char* pbase = reinterpret_cast<const char*>(a.part + static_cast<int64_t>(blk.first) * a.hs);
+  for (int u = threadIdx.x; u < n_units; u += kThreads) {
+    const int j = u / per_tok;
+    const int rem = u - j * per_tok;
+    const int sa = rem / W2;
+    const int col = sa * a.hs1 + (rem - sa * W2) * 2;
+    if (!((wmask >> sa) & 1u)) {
+      emit(j, col, f32x2{0.f, 0.f});
+      continue;
+    }
+    const uint32_t o0 = static_cast<uint32_t>(j * a.hs + col) * 4u;
+    f32x2 sum = f32x2{0.f, 0.f};
+    for (int c0 = 0; c0 < nch; c0 += CB) {
+      f32x2 v[CB];
+      for (unsigned spins = 0;; ++spins) {
+        if (spins >= a.spin_limit || (spins > 0 && poisoned(a.plan.header))) {
+          if (spins >= a.spin_limit) give_up(a.plan.header);
+#pragma unroll
+          for (int i = 0; i < CB; ++i) v[i] = f32x2{0.f, 0.f};
+          break;
+        }
+        bool missing = false;
+#pragma unroll
+        for (int i = 0; i < CB; ++i) {
+          const int cc = min(c0 + i, nch - 1);
+          v[i] = __builtin_bit_cast(f32x2, coherent_load8(pbase + (o0 + static_cast<uint32_t>(cc) * cstride)));
+        }
+#pragma unroll
+        for (int i = 0; i < CB; ++i) missing = missing || is_empty(v[i][0]) || is_empty(v[i][1]);
+        if (!missing) break;
+        __builtin_amdgcn_s_sleep(2);
+      }
+#pragma unroll
+      for (int i = 0; i < CB; ++i)
+        if (c0 + i < nch) sum += v[i];
+    }
+    emit(j, col, sum * slice_alpha(alphas, sa));
+  }
+}
+
+// The words of the written slices, each (d-range, token, slice, 4 columns):
+// visit(c, j, col) for every unit `tid` owns.
+template <typename Visit>
+__device__ __forceinline__ void for_pa_units(const ApplyArgs& a, const Block& blk, int W, uint32_t wmask, int tid,
+                                             int nthreads, Visit visit) {
+  const int W4 = W / 4;
+  const int per_chunk = blk.count * a.w.n_a * W4;
+  const int total = per_chunk * a.n_chunks;
+  for (int u = tid; u < total; u += nthreads) {
+    const int c = u / per_chunk;
+    const int q = u - c * per_chunk;
+    const int j = q / (a.w.n_a * W4);
+    const int rem = q - j * (a.w.n_a * W4);
+    const int sa = rem / W4;
+    if (!((wmask >> sa) & 1u)) continue;
+    visit(c, j, sa * a.hs1 + (rem - sa * W4) * 4);
+  }
+}
+
+__device__ __forceinline__ void await_partials_pa(const ApplyArgs& a, const Block& blk, int W, uint32_t wmask) {
+  for_pa_units(a, blk, W, wmask, threadIdx.x, kThreads, [&](int c, int j, int col) {
+    const float* p = a.part + (static_cast<int64_t>(c) * a.ptok + blk.first + j) * a.hs + col;
+    for (unsigned spins = 0;; ++spins) {
+      if (spins >= a.spin_limit || (spins > 0 && poisoned(a.plan.header))) {
+        if (spins >= a.spin_limit) give_up(a.plan.header);
+        break;
+      }
+      if (!any_empty(coherent_load_f4(p))) break;
+      __builtin_amdgcn_s_sleep(4);
+    }
+  });
+}
+
+__device__ __forceinline__ void clear_partials_pa(const ApplyArgs& a, const Block& blk, int W, uint32_t wmask, int tid,
+                                                  int nthreads) {
+  const f32x4 e = __builtin_bit_cast(f32x4, u32x4{kPartialEmpty, kPartialEmpty, kPartialEmpty, kPartialEmpty});
+  for_pa_units(a, blk, W, wmask, tid, nthreads, [&](int c, int j, int col) {
+    coherent_store_f4(a.part + (static_cast<int64_t>(c) * a.ptok + blk.first + j) * a.hs + col, e);
+  });
+}
+
 // ---------------------------------------------------------------- expand ----
 
 // Row stride (elements) of the block's H in LDS: RANK plus 8 to spread banks.
@@ -569,13 +675,13 @@ struct OutChunk {
 };
 
 // kSliceH: a slice may have its own H (one A per slice, or expand() of such
-// a call's H); otherwise every slice reads H from column 0.
-template <typename T, bool kSliceH>
+// a call's H); otherwise every slice reads H from column 0.  TS: as resolve_b.
+template <typename T, bool kSliceH, bool TS = false>
 __device__ __forceinline__ OutChunk<T> out_chunk(const ApplyArgs& a, const Block& blk, int oc) {
   int s = 0;
   while (s + 1 < a.w.n_slices && oc >= a.w.oc_start[s + 1]) ++s;
   OutChunk<T> c;
-  c.res = resolve_b<T>(a, blk, s);
+  c.res = resolve_b<T, TS>(a, blk, s);
   c.o_first = (oc - a.w.oc_start[s]) * kOC;
   c.o_size = a.w.o_size[s];
   c.y_off = a.w.y_off[s];
@@ -660,10 +766,13 @@ __device__ __forceinline__ void yrows_store(const ApplyArgs& a, int y_off, int o
 }
 
 // This wave's 64 rows of the chunk's B and token tile 0 of its Y columns.
-template <typename T, int RANK>
+// DYN: B's row stride is the chunk's adapter rank (zero-padded slices of
+// mixed ranks, expanded at RANK = 64); otherwise RANK.
+template <typename T, int RANK, bool DYN = false>
 __device__ __forceinline__ void load_chunk(const ApplyArgs& a, const OutChunk<T>& c, int32_t tok0,
                                            typename VecOf<T>::v8 (&bf)[kOT][(RANK + 31) / 32], YRows& y0) {
   constexpr int KS = (RANK + 31) / 32;
+  const int rb = DYN ? c.res.rank : RANK;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int row = lane & 15;
@@ -676,8 +785,8 @@ __device__ __forceinline__ void load_chunk(const ApplyArgs& a, const OutChunk<T>
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int k = ks * 32 + kq;
-      bf[ot][ks] = (ok && o < c.o_size && k < RANK) ? load8(c.res.ptr + static_cast<int64_t>(o) * RANK + k)
-                                                      : zero8<T>();
+      bf[ot][ks] = (ok && o < c.o_size && k < rb) ? load8(c.res.ptr + static_cast<int64_t>(o) * rb + k)
+                                                    : zero8<T>();
     }
   }
   int32_t tok[2];
@@ -760,41 +869,76 @@ __device__ __forceinline__ void compute_chunk(const ApplyArgs& a, int b, const B
 
 // Expand workgroup `p` of block b: output chunks p, p + n_owg, ... (at most
 // n_sub of them; with several slices of equal width, one chunk per slice).
-// Chunk 0's B and Y are loaded before the wait.
-template <typename T, int RANK, int ROLE, int TILES, bool PA>
+// Chunk 0's B and Y are loaded before the wait.  MIX: mixed ranks in a
+// fused role, expanded at RANK = kMaxRank whatever the block's adapter rank:
+// B rows at the adapter's own stride (zeros past its rank), H columns past
+// it zero in LDS.  One body instead of one per rank keeps the multi-chunk
+// kernel within its registers.
+template <typename T, int RANK, int ROLE, int TILES, bool PA, bool MIX = false>
 __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, const Block& blk, int32_t tok0,
                                             T* s_h, T* s_stage, int* s_flag) {
   using V8 = typename VecOf<T>::v8;
   constexpr int KS = (RANK + 31) / 32;
   constexpr bool kFusedRole = ROLE == kFused || ROLE == kFusedMulti;
-  // LDS row of the block's H: every A slice's H side by side, plus 8
-  // elements to spread banks.
-  const int hsl = PA ? a.w.n_a * RANK + 8 : RANK + 8;
+  constexpr bool kDyn = PA || MIX;  // B row stride: the adapter's rank
+  // LDS row of the block's H: every A slice's H side by side (hs1 columns
+  // each), plus 8 elements to spread banks.
+  const int hsl = PA ? a.w.n_a * a.hs1 + 8 : RANK + 8;
   constexpr bool kSliceH = PA || ROLE == kExpandOnly;
   const int n_owg = (a.n_ochunks + a.n_sub - 1) / a.n_sub;
   T* stage = s_stage + (threadIdx.x >> 6) * 16 * kStageStride;
-  OutChunk<T> cur = out_chunk<T, kSliceH>(a, blk, p);
-  if (cur.res.err != 0 && p == 0 && threadIdx.x == 0) flag_error(a.plan.header, cur.res.err);
+  OutChunk<T> cur = out_chunk<T, kSliceH, PA>(a, blk, p);
+  if (cur.res.err != 0 && cur.o_first == 0 && threadIdx.x == 0) flag_error(a.plan.header, cur.res.err);
   // Rank rows the block's shrink side writes (0: it could not resolve the
   // adapter and writes nothing).
-  const int wrote = kFusedRole ? resolve_a<T>(a, blk).rank : 0;
-  // Partial words per token: every A slice's rank rows.
-  const int wrote_all = PA ? wrote * a.w.n_a : wrote;
+  int wrote = kFusedRole ? resolve_a<T, PA>(a, blk).rank : 0;
+  // One A per slice: the slices whose shrink side writes (the same
+  // resolution as theirs), the columns each writes (W: the rank, or all hs1
+  // of a zero-padded slice) and each one's alpha.
+  uint32_t wmask = 1u;
+  int W = RANK;
+  float alphas[kMaxSlices] = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (PA && kFusedRole) {
+    W = a.pad_rank ? a.hs1 : RANK;
+    if (a.w.mode == kStacked) {
+      wmask = wrote > 0 ? (1u << a.w.n_a) - 1u : 0u;
+#pragma unroll
+      for (int s = 0; s < kMaxSlices; ++s) alphas[s] = a.w.scale;
+    } else {
+      wmask = 0u;
+#pragma unroll
+      for (int s = 0; s < kMaxSlices; ++s) {
+        if (s >= a.w.n_a) break;
+        const Resolved<T> rs = resolve_a<T, true>(a, blk, s);
+        if (rs.ptr != nullptr) {
+          wmask |= 1u << s;
+          alphas[s] = rs.alpha;
+        }
+      }
+    }
+    wrote = wmask != 0u ? W : 0;
+  }
+  // Partial words per token the block's shrink side writes.
+  const int wrote_all = PA ? W * __builtin_popcount(wmask) : wrote;
   V8 bf[kOT][KS];
   YRows yq;
-  load_chunk<T, RANK>(a, cur, tok0, bf, yq);
+  load_chunk<T, RANK, kDyn>(a, cur, tok0, bf, yq);
   trace_stamp(a, 2);
 
   bool go = cur.res.ptr != nullptr;
   unsigned consumed_prev = 0;
   if constexpr (kFusedRole) {
-    go = go && wrote > 0;
+    // One A per slice over several chunks: a later chunk's slice may have
+    // resolved where the first one's did not (table mode), so the workgroup
+    // collects H if any slice wrote, and each chunk is tested on its own.
+    go = (PA && ROLE == kFusedMulti ? true : go) && wrote > 0;
     if (go) {
       // Multi-slice workgroups of small blocks (at most 2048 partial words)
       // poll the data straight away; the probe gate in front pays off for
       // larger blocks and for the single-slice kernel (measured on MI355X).
-      go = (ROLE == kFused || blk.count * wrote_all * a.n_chunks > 2048) ? wait_partials<PA>(a, blk, wrote, s_flag)
-                                                                          : true;
+      go = (ROLE == kFused || blk.count * wrote_all * a.n_chunks > 2048)
+               ? wait_partials<PA>(a, blk, wrote, s_flag, wmask)
+               : true;
       trace_stamp(a, 3);
       if (go) {
         const auto to_lds = [&](int j, int r0, f32x2 v) {
@@ -806,16 +950,38 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
         // Batches of d-ranges: all eight of a multi-slice call's at once;
         // four in the single-slice kernel (eight cost it a spill and
         // measured slower).
-        if constexpr (ROLE == kFusedMulti) {
-          collect_partials<8>(a, blk, (PA ? a.w.n_a : 1) * RANK / 2, cur.res.alpha, to_lds);
+        if constexpr (PA) {
+          if constexpr (ROLE == kFusedMulti) {
+            collect_partials_pa<8>(a, blk, W, wmask, alphas, to_lds);
+          } else {
+            collect_partials_pa<4>(a, blk, W, wmask, alphas, to_lds);
+          }
+        } else if constexpr (MIX) {
+          // The adapter's rank columns from the partials, zeros past it.
+          const int zp = (RANK - wrote) / 2;
+          for (int u = threadIdx.x; u < blk.count * zp; u += kThreads) {
+            const int j = u / zp;
+            to_lds(j, wrote + (u - j * zp) * 2, f32x2{0.f, 0.f});
+          }
+          if constexpr (ROLE == kFusedMulti) {
+            collect_partials<8>(a, blk, wrote / 2, cur.res.alpha, to_lds);
+          } else {
+            collect_partials<4>(a, blk, wrote / 2, cur.res.alpha, to_lds);
+          }
+        } else if constexpr (ROLE == kFusedMulti) {
+          collect_partials<8>(a, blk, RANK / 2, cur.res.alpha, to_lds);
         } else {
-          collect_partials<4>(a, blk, (PA ? a.w.n_a : 1) * RANK / 2, cur.res.alpha, to_lds);
+          collect_partials<4>(a, blk, RANK / 2, cur.res.alpha, to_lds);
         }
       }
     } else if (wrote > 0) {
       // Nothing to compute, but this may be the workgroup that empties the
       // partials: every store must have landed first.
-      await_partials(a, blk, wrote_all);
+      if constexpr (PA) {
+        await_partials_pa(a, blk, W, wmask);
+      } else {
+        await_partials(a, blk, wrote_all);
+      }
     }
     __syncthreads();
     trace_stamp(a, 4);
@@ -837,9 +1003,9 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
         const int oc = p + (j + 1) * n_owg;
         cn[j].res.ptr = nullptr;
         if (j + 1 < a.n_sub && oc < a.n_ochunks) {
-          cn[j] = out_chunk<T, kSliceH>(a, blk, oc);
-          if (cn[j].res.err != 0 && p == 0 && threadIdx.x == 0) flag_error(a.plan.header, cn[j].res.err);
-          if (cn[j].res.ptr != nullptr) load_chunk<T, RANK>(a, cn[j], tok0, bfn[j], yqn[j]);
+          cn[j] = out_chunk<T, kSliceH, PA>(a, blk, oc);
+          if (cn[j].res.err != 0 && cn[j].o_first == 0 && threadIdx.x == 0) flag_error(a.plan.header, cn[j].res.err);
+          if (cn[j].res.ptr != nullptr) load_chunk<T, RANK, kDyn>(a, cn[j], tok0, bfn[j], yqn[j]);
         }
       }
       if (cur.res.ptr != nullptr) compute_chunk<T, RANK, true, 1>(a, b, blk, tok0, cur, bf, yq, s_h, hsl, stage);
@@ -849,9 +1015,9 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
       for (int i = 3; i < a.n_sub; ++i) {
         const int oc = p + i * n_owg;
         if (oc >= a.n_ochunks) break;
-        cur = out_chunk<T, kSliceH>(a, blk, oc);
-        if (cur.res.err != 0 && p == 0 && threadIdx.x == 0) flag_error(a.plan.header, cur.res.err);
-        load_chunk<T, RANK>(a, cur, tok0, bf, yq);
+        cur = out_chunk<T, kSliceH, PA>(a, blk, oc);
+        if (cur.res.err != 0 && cur.o_first == 0 && threadIdx.x == 0) flag_error(a.plan.header, cur.res.err);
+        load_chunk<T, RANK, kDyn>(a, cur, tok0, bf, yq);
         if (cur.res.ptr != nullptr) compute_chunk<T, RANK, true, 1>(a, b, blk, tok0, cur, bf, yq, s_h, hsl, stage);
       }
     } else if constexpr (ROLE == kFusedMulti) {
@@ -861,9 +1027,9 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
         const int oc = p + i * n_owg;
         if (oc >= a.n_ochunks) break;
         if (i > 0) {
-          cur = out_chunk<T, kSliceH>(a, blk, oc);
-          if (cur.res.err != 0 && p == 0 && threadIdx.x == 0) flag_error(a.plan.header, cur.res.err);
-          load_chunk<T, RANK>(a, cur, tok0, bf, yq);
+          cur = out_chunk<T, kSliceH, PA>(a, blk, oc);
+          if (cur.res.err != 0 && cur.o_first == 0 && threadIdx.x == 0) flag_error(a.plan.header, cur.res.err);
+          load_chunk<T, RANK, kDyn>(a, cur, tok0, bf, yq);
         }
         if (cur.res.ptr != nullptr) compute_chunk<T, RANK, true, 1>(a, b, blk, tok0, cur, bf, yq, s_h, hsl, stage);
       }
@@ -880,7 +1046,11 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
     __syncthreads();
     if (*s_flag != 0) {
       if (threadIdx.x == 0) atomic_store_u(&a.consumed[b * kCounterStride], 0u);
-      if (wrote > 0) clear_partials(a, blk, wrote_all, threadIdx.x, kThreads);
+      if constexpr (PA) {
+        if (wmask != 0u) clear_partials_pa(a, blk, W, wmask, threadIdx.x, kThreads);
+      } else {
+        if (wrote > 0) clear_partials(a, blk, wrote_all, threadIdx.x, kThreads);
+      }
     }
   }
 }
@@ -994,8 +1164,9 @@ void apply_kernel(const uint32_t* header, const Block* __restrict__ blocks,
     const int k = part - sa * per_a;
     const int rg = k / a.n_chunks;
     const int c = k - rg * a.n_chunks;
-    const Resolved<T> res = resolve_a<T>(a, blk, sa);
-    if (res.err != 0 && part == 0 && threadIdx.x == 0) flag_error(a.plan.header, res.err);
+    const Resolved<T> res = resolve_a<T, PA>(a, blk, sa);
+    // Each slice's first workgroup reports its resolution error.
+    if (res.err != 0 && k == 0 && threadIdx.x == 0) flag_error(a.plan.header, res.err);
     if constexpr (ROLE == kFusedMulti || ROLE == kShrinkOnly) {
       shrink_body<T, kShrinkRowsFused / 16>(a, b, c, sa, rg * kShrinkRowsFused, blk, t0, res, s_red);
     } else {
@@ -1007,6 +1178,14 @@ void apply_kernel(const uint32_t* header, const Block* __restrict__ blocks,
     reduce_to_h<T>(a, b, blk, &s_flag);
   } else if constexpr (RANK != 0) {
     expand_body<T, RANK, ROLE, TILES, PA>(a, b, part, blk, t0, s_h, smem.stage, &s_flag);
+  } else if constexpr (PA) {
+    // Mixed ranks with one A per slice (zero-padded slices): every block at
+    // the largest rank, B read at each adapter's own row stride.
+    expand_body<T, kMaxRank, ROLE, TILES, PA>(a, b, part, blk, t0, s_h, smem.stage, &s_flag);
+  } else if constexpr (ROLE == kFusedMulti) {
+    // Mixed ranks over several chunks per workgroup: one body at the largest
+    // rank (four per-rank bodies here spill).
+    expand_body<T, kMaxRank, ROLE, TILES, false, true>(a, b, part, blk, t0, s_h, smem.stage, &s_flag);
   } else {
     // Mixed ranks: the block's adapter decides (resolved again inside).
     const Resolved<T> r0 = resolve_b<T>(a, blk, 0);
@@ -1325,10 +1504,13 @@ hipError_t launch_fused(int dtype_bf16, const ApplyArgs& a, hipStream_t stream) 
   if (a.srows != (a.n_sub > 1 ? kShrinkRowsFused : kShrinkRows)) return hipErrorInvalidValue;
   // The block's H rows live in LDS, sized for blocks of 16 tokens and at most
   // kMaxSlices A slices; the probe gate takes at most 64 x kProbesPerLane
-  // shrink workgroups per block; one A per slice only with stacked weights.
+  // shrink workgroups per block; the partial buffer holds kMaxChunks x
+  // kMaxRank fp32 per plan position.
   if (a.tiles != 1) return hipErrorInvalidValue;
-  if (a.w.n_a < 1 || a.w.n_a > kMaxSlices || (a.w.n_a > 1 && (a.w.n_a != a.w.n_slices || a.w.mode != kStacked)) ||
-      a.hs != a.w.n_a * a.hs1 || a.n_chunks * a.n_rgroups * a.w.n_a > 64 * kProbesPerLane)
+  if (a.w.n_a < 1 || a.w.n_a > kMaxSlices || (a.w.n_a > 1 && a.w.n_a != a.w.n_slices) ||
+      a.hs != a.w.n_a * a.hs1 || a.n_chunks * a.n_rgroups * a.w.n_a > 64 * kProbesPerLane ||
+      a.n_chunks * a.hs > kMaxChunks * kMaxRank ||
+      (a.pad_rank && (a.w.n_a < 2 || a.rank != 0 || a.hs1 != kMaxRank)) || (a.rank == 0 && a.w.n_a > 1 && !a.pad_rank))
     return hipErrorInvalidValue;
   return a.n_sub > 1 ? launch_role<kFusedMulti>(dtype_bf16, a, stream) : launch_role<kFused>(dtype_bf16, a, stream);
 }

@@ -124,12 +124,17 @@ constexpr int kExpandWorkgroups = 16;
 // Measured on MI355X: cfg2 o_proj 14.3 -> 14.1 us, cfg5 step 836 -> 797 us,
 // cfg1 9.2 -> 8.8 us.  Multi-slice calls skip the residency test: their grid
 // does not fit at either count, and the halved one only adds a load round
-// (qkv 20.6 -> 20.8 us).
-inline void shrink_split(int d, int rank, int rows, int n_a, int64_t slots, int64_t expand_per_block, int64_t resident,
-                         ApplyArgs* a) {
+// (qkv 20.6 -> 20.8 us).  It is also halved while the d-ranges' partial rows
+// (nc x hs fp32 per plan position, hs = the A slices' H columns side by side)
+// exceed the partial buffer's kMaxChunks x kMaxRank; four d-ranges of four
+// 64-column slices fill it exactly.
+inline void shrink_split(int d, int rank, int rows, int n_a, int hs, int64_t slots, int64_t expand_per_block,
+                         int64_t resident, ApplyArgs* a) {
   const int g = shrink_rank_groups(rank, rows);
   int nc = static_cast<int>(std::min<int64_t>(std::max(8, shrink_workgroups(rows) / g), ceil_div(d, 128)));
-  while (nc > 4 && (d < nc * 512 || (resident > 0 && slots * (nc * g * n_a + expand_per_block) > resident))) nc /= 2;
+  while (nc > 4 && (d < nc * 512 || nc * hs > kMaxChunks * kMaxRank ||
+                    (resident > 0 && slots * (nc * g * n_a + expand_per_block) > resident)))
+    nc /= 2;
   const int c = static_cast<int>(ceil_div(ceil_div(d, nc), 128) * 128);
   a->dc = c;
   a->n_chunks = static_cast<int>(ceil_div(d, c));
@@ -1100,7 +1105,7 @@ int stacked_call_args(const char* who, void* y, const void* x, int32_t n_a, cons
 void fused_split(ApplyArgs* a, int rank, int d_model, int n_cu) {
   a->n_sub = static_cast<int>(ceil_div(a->n_ochunks, kExpandWorkgroups));
   const int multi = a->n_sub > 1 ? 1 : 0;
-  shrink_split(d_model, rank, multi ? kShrinkRowsFused : kShrinkRows, a->w.n_a, a->n_slots,
+  shrink_split(d_model, rank, multi ? kShrinkRowsFused : kShrinkRows, a->w.n_a, a->hs, a->n_slots,
                ceil_div(a->n_ochunks, a->n_sub), multi ? 0 : static_cast<int64_t>(n_cu) * fused_waves_per_simd(rank, multi),
                a);
 }
@@ -1333,6 +1338,92 @@ int wp_shrink_expand(wp_engine* e, const void* X, void* Y, int32_t d_model, int3
   a.w.oc_start[1] = static_cast<int32_t>(ceil_div(out_features, cols));
   a.n_ochunks = a.w.oc_start[1];
   a.n_slots = block_bound(e, resolvable_ids(e));
+  fused_split(&a, rank, d_model, e->n_cu);
+  WP_HIP(launch_fused(dtype == WP_DTYPE_BF16, a, stream));
+  return WP_OK;
+}
+
+int wp_shrink_expand_slices(wp_engine* e, const void* X, void* Y, int32_t d_model, int32_t n_slices,
+                            const int32_t* id_offsets, int32_t ids_per_layer, const int32_t* out_features,
+                            const int32_t* y_col_offsets, int32_t rank, int64_t T, int64_t y_row_stride, int32_t dtype,
+                            void* stream_) {
+  if (!e) return fail(WP_ERR_INVALID, "shrink_expand_slices: engine is NULL");
+  if (n_slices < 1 || n_slices > kMaxSlices || !id_offsets || !out_features || !y_col_offsets)
+    return fail(WP_ERR_INVALID, "shrink_expand_slices: 1..%d slices with their ids, widths and offsets", kMaxSlices);
+  if (e->plan_kind != 2)
+    return fail(WP_ERR_STATE, "shrink_expand_slices: needs a build_seg_bounds table (a build_segments table resolves "
+                              "its adapters when it is built)");
+  if (ids_per_layer < 0) return fail(WP_ERR_INVALID, "shrink_expand_slices: negative ids_per_layer");
+  for (int s = 0; s < n_slices; ++s) {
+    if (id_offsets[s] < 0 || id_offsets[s] > e->table_cap)
+      return fail(WP_ERR_INVALID, "shrink_expand_slices: slice %d id offset %d outside the adapter table", s,
+                  id_offsets[s]);
+    if (out_features[s] <= 0 || out_features[s] % 4 != 0 || y_col_offsets[s] < 0 || y_col_offsets[s] % 4 != 0 ||
+        y_col_offsets[s] + out_features[s] > y_row_stride)
+      return fail(WP_ERR_INVALID, "shrink_expand_slices: slice %d window [%d, %d) does not fit Y (row stride %lld, "
+                                  "4-aligned)", s, y_col_offsets[s], y_col_offsets[s] + out_features[s],
+                  (long long)y_row_stride);
+  }
+  if (e->plan_T > kSmallPlanTokens || n_slices == 1) {
+    // Large plans (and a single slice): one shrink_expand per slice, each
+    // on its layer's adapters.
+    const int32_t off0 = e->entry_offset, cnt0 = e->entry_count;
+    int rc = WP_OK;
+    for (int s = 0; s < n_slices && rc == WP_OK; ++s) {
+      e->entry_offset = id_offsets[s];
+      e->entry_count = ids_per_layer;
+      rc = wp_shrink_expand(e, X, Y, d_model, out_features[s], rank, T, y_row_stride, y_col_offsets[s], dtype, stream_);
+    }
+    e->entry_offset = off0;
+    e->entry_count = cnt0;
+    return rc;
+  }
+  if (rank != 0 && !rank_ok(rank)) return fail(WP_ERR_INVALID, "shrink_expand_slices: unsupported rank (only 8/16/32/64)");
+  int rc = check_io("shrink_expand_slices", dtype, X, "X");
+  if (rc != WP_OK) return rc;
+  if (!aligned(Y, 8)) return fail(WP_ERR_INVALID, "shrink_expand_slices: Y must be 8-byte aligned");
+  if (d_model <= 0 || d_model % 8 != 0)
+    return fail(WP_ERR_INVALID, "shrink_expand_slices: d_model must be a positive multiple of 8");
+  if (y_row_stride % 4 != 0) return fail(WP_ERR_INVALID, "shrink_expand_slices: Y row stride must be a multiple of 4");
+  if (e->plan_T > T)
+    return fail(WP_ERR_INVALID, "shrink_expand_slices: segments reach token %lld but X has %lld rows",
+                (long long)e->plan_T, (long long)T);
+  DeviceGuard g(e->device);
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  ApplyArgs a = base_args(e, rank);
+  a.x = X;
+  a.ldx = d_model;
+  a.y = Y;
+  a.ldy = y_row_stride;
+  a.d_model = d_model;
+  if (!stream_capturing(stream) && (rc = apply_ready_slots(e, stream)) != WP_OK) return rc;
+  a.w.mode = kTable;
+  a.w.entries = e->dtable;
+  int32_t max_off = 0;
+  for (int s = 0; s < n_slices; ++s) max_off = std::max(max_off, id_offsets[s]);
+  a.w.num_ids = std::max(0, e->table_cap - max_off);
+  if (ids_per_layer > 0) a.w.num_ids = std::min(a.w.num_ids, ids_per_layer);
+  a.w.n_a = n_slices;
+  a.w.n_slices = n_slices;
+  a.hs1 = rank == 0 ? kMaxRank : rank;
+  a.hs = n_slices * a.hs1;
+  a.pad_rank = rank == 0 ? 1 : 0;
+  const int cols = expand_cols_per_workgroup();
+  int oc = 0;
+  for (int s = 0; s < n_slices; ++s) {
+    a.w.entry_off[s] = id_offsets[s];
+    a.w.o_size[s] = out_features[s];
+    a.w.y_off[s] = y_col_offsets[s];
+    a.w.oc_start[s] = oc;
+    oc += static_cast<int>(ceil_div(out_features[s], cols));
+  }
+  a.w.oc_start[n_slices] = oc;
+  a.n_ochunks = oc;
+  // Blocks: bounded as for one layer's window (an id registered in any
+  // slice's layer forms a block).
+  int64_t ids = static_cast<int64_t>(e->adapters.size());
+  if (ids_per_layer > 0) ids = std::min<int64_t>(ids, ids_per_layer);
+  a.n_slots = block_bound(e, ids);
   fused_split(&a, rank, d_model, e->n_cu);
   WP_HIP(launch_fused(dtype == WP_DTYPE_BF16, a, stream));
   return WP_OK;

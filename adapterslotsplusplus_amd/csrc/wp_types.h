@@ -155,6 +155,9 @@ struct Weights {
   const void* a_base[kMaxSlices];
   int64_t a_stride[kMaxSlices];  // elements
   const Entry* entries;
+  // Table mode, one A per slice: slice s reads entries[entry_off[s] + block's
+  // id] (a layer of a multi-layer store per slice); 0 otherwise.
+  int32_t entry_off[kMaxSlices];
   int32_t n_slices;
   int32_t oc_start[kMaxSlices + 1];  // prefix of o-chunks per slice
   const void* b_base[kMaxSlices];

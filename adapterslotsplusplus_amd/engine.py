@@ -319,6 +319,35 @@ class WarpPipeEngine:
                                               int(Y.size(0)), int(Y.size(-1)), int(y_offset), dt, self._stream()),
                    "shrink_expand")
 
+    def shrink_expand_slices(self, X, Y, layers, out_features, y_offsets, rank=0):
+        """shrink_expand over several layers of the multi-layer store in one
+        launch (not in the reference): slice i applies layer layers[i]'s
+        adapter of each token's id into columns [y_offsets[i], + out_features[i])
+        of Y, in place; X is read once (packed gate/up, for instance).  rank=0:
+        each adapter at its registered rank."""
+        rank = int(rank or 0)
+        self._on_device(X, "X")
+        self._on_device(Y, "Y")
+        if X.dim() != 2 or Y.dim() != 2:
+            raise RuntimeError("shrink_expand_slices: X and Y must be 2-D ([T, d] and [T, width])")
+        if X.dtype != Y.dtype:
+            raise RuntimeError("X/Y must have the same dtype")
+        dt = _dtype_code(Y, "Y")
+        if not (X.is_contiguous() and Y.is_contiguous()):
+            raise RuntimeError("X/Y must be contiguous")
+        if X.size(0) != Y.size(0):
+            raise RuntimeError("X and Y have different token counts")
+        n = len(layers)
+        if len(out_features) != n or len(y_offsets) != n:
+            raise RuntimeError("shrink_expand_slices: one width and one offset per layer")
+        stride = int(self.config.layer_stride or 0)
+        offs = (ctypes.c_int32 * max(n, 1))(*[self._store_id(0, int(l)) for l in layers])
+        o_arr = (ctypes.c_int32 * max(n, 1))(*[int(o) for o in out_features])
+        y_arr = (ctypes.c_int32 * max(n, 1))(*[int(v) for v in y_offsets])
+        _lib.check(self._lib.wp_shrink_expand_slices(self._handle, _ptr(X), _ptr(Y), int(X.size(-1)), n, offs, stride,
+                                                     o_arr, y_arr, rank, int(Y.size(0)), int(Y.size(-1)), dt,
+                                                     self._stream()), "shrink_expand_slices")
+
     def add_lora_packed(self, y, x, wa_t_all, wb_t_all, scale, y_offset=None, y_slice_size=None) -> bool:
         """y += (scale * x . A[idx]^T) . B[idx]^T for the tokens of the last
         build_seg_bounds table (reference engine.py:56-62, bindings:195-234).

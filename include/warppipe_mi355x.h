@@ -171,6 +171,19 @@ int wp_expand(wp_engine* e, const void* H, void* Y, int32_t out_features, int32_
 int wp_shrink_expand(wp_engine* e, const void* X, void* Y, int32_t d_model, int32_t out_features, int32_t rank,
                      int64_t T, int64_t y_row_stride, int32_t y_col_offset, int32_t dtype, void* stream);
 
+/* shrink_expand over several layers of a multi-layer store in one launch (no
+ * reference counterpart): slice s applies, to every token of the last
+ * build_seg_bounds table, the adapter registered under id_offsets[s] + the
+ * token's id (ids >= ids_per_layer skipped and flagged; 0: no limit), into
+ * columns [y_col_offsets[s], + out_features[s]) of Y.  X is read once; each
+ * slice's adapter has its own A, B, alpha and (rank = 0) rank.  The packed
+ * gate/up projections of a layer, for instance, as one call.  Plans over 512
+ * tokens run one shrink_expand per slice. */
+int wp_shrink_expand_slices(wp_engine* e, const void* X, void* Y, int32_t d_model, int32_t n_slices,
+                            const int32_t* id_offsets, int32_t ids_per_layer, const int32_t* out_features,
+                            const int32_t* y_col_offsets, int32_t rank, int64_t T, int64_t y_row_stride, int32_t dtype,
+                            void* stream);
+
 /* Replaces WarpPipeExtension::add_lora_packed (bindings:195-234) and the DSAK
  * kernels (warp_pipe_r32.cu:280-423), generalised to ranks 8/16/32/64, bf16,
  * and n_slices (1..4) output slices sharing one H:

@@ -73,6 +73,21 @@ def test_nslice_ranks_ragged_windows(rank):
     assert engine.device_errors() == 0
 
 
+def test_nslice_four_rank64_slices_wide_d():
+    """Four 64-column A slices over d = 4096: the d-range count is capped so
+    that the partial rows (d-ranges x 256 columns) fit the partial buffer."""
+    T, L, d, widths = 256, 16, 4096, [1024, 1024, 512, 512]
+    announce("nslice four rank-64 slices d=4096")
+    idx = wl.zipf_indices(T, L, 1.1, 2)
+    idx, x, was, wbs, y0 = inputs(T, L, 64, d, widths, torch.bfloat16, 60, idx)
+    offs = [sum(widths[:i]) for i in range(len(widths))]
+    engine = WarpPipeEngine()
+    y = run(engine, idx, x, was, wbs, y0, 0.5, offs)
+    segs = so.seg_bounds(idx.tolist()).tolist()
+    assert_close(y, bgmv.add_lora_nslice(y0, x, was, wbs, 0.5, segs, offs), "4 x r64")
+    assert engine.device_errors() == 0
+
+
 def test_nslice_large_plan():
     """More than 512 tokens (64-token blocks): one shrink launch per A slice
     into its columns of the engine's H, then one expand."""
