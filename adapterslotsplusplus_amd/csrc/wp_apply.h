@@ -61,28 +61,31 @@ hipError_t launch_plan(const void* idx, int idx_is_int64, int T, uint32_t* heade
 hipError_t launch_maintain(uint32_t* header, const Maint& m, hipStream_t stream);
 
 // Tiny writes of adapter-table entries and of one slot publication, in stream
-// order (one wave): pub (if not null) gets (pub_id, pub_entry) under its
-// sequence lock, then dst[i] = val[i] for i < n.
+// order (one wave): pub (if not null) gets (pub_id, pub_gen, pub_entry) under
+// its sequence lock, the retired generations are raised, then dst[i] =
+// val[i] for i < n.
 constexpr int kMaxEntryWrites = 16;
 struct EntryWrites {
   int32_t n;
   int32_t pub_id;
+  uint32_t pub_gen;
   SlotPub* pub;
   Entry pub_entry;
   Entry* dst[kMaxEntryWrites];
   Entry val[kMaxEntryWrites];
-  // Further publications to empty (id -1) under their sequence locks.
-  int32_t n_clear;
-  SlotPub* clear[kMaxEntryWrites];
+  // Slot generations released: *retire[i] = max(*retire[i], retire_gen[i]).
+  int32_t n_retire;
+  uint32_t* retire[kMaxEntryWrites];
+  uint32_t retire_gen[kMaxEntryWrites];
 };
 hipError_t launch_entry_writes(const EntryWrites& w, hipStream_t stream);
 
 // Staging copies: job j copies a_bytes from src_a to dst_a and b_bytes from
 // src_b to dst_b (sources in device memory or in pinned host memory the
 // device reads directly), over kStageWorkgroups workgroups; the job's last
-// workgroup to finish then publishes (pub_id, pub_entry) into *pub under its
-// sequence lock.  pub->pad[0] counts the job's finished workgroups (zero
-// between jobs).
+// workgroup to finish then publishes (pub_id, pub_gen, pub_entry) into *pub
+// under its sequence lock.  pub->copies counts the job's finished workgroups
+// (zero between jobs).
 constexpr int kMaxStageJobs = 8;
 constexpr int kStageWorkgroups = 8;
 struct StageJob {
@@ -94,6 +97,7 @@ struct StageJob {
   uint64_t b_bytes;  // multiple of 16
   SlotPub* pub;
   int32_t pub_id;
+  uint32_t pub_gen;
   int32_t pad;
   Entry pub_entry;
 };

@@ -102,6 +102,7 @@ struct Slot {
   void* B = nullptr;
   size_t a_bytes = 0, b_bytes = 0;  // sizes of A and B
   hipEvent_t ready = nullptr;     // prefetch stream: copy and publication done
+  uint32_t gen = 0;               // generation of the slot's current (or last) fill
   bool issued = false;
   bool applied = false;           // an eager call has enqueued the table write of the publication
 };
@@ -216,6 +217,7 @@ struct wp_engine {
   float* spart = nullptr;       // [kMaxChunks][tok_cap][kMaxRank] d-range partials of shrink() launches (no invariant)
   void* hbuf = nullptr;         // [tok_cap][kMaxSlices x kMaxRank] 2-byte H of large-plan add_lora calls
   SlotPub* pubs = nullptr;      // [num_staging_slots] staging publications
+  uint32_t* retired = nullptr;  // [num_staging_slots] highest released generation per slot
   Entry* dtable = nullptr;      // [table_cap] id-indexed adapter table of build_seg_bounds plans
   int table_cap = 0;
   int seg_cap = 0, block_cap = 0, tok_cap = 0, entry_cap = 0;
@@ -299,6 +301,7 @@ Maint maint_view(const wp_engine* e) {
   m.consumed = e->consumed;
   m.consumed_words = e->consumed_words;
   m.pubs = e->pubs;
+  m.retired = e->retired;
   m.n_pubs = static_cast<int32_t>(e->slots.size());
   m.table_cap = e->table_cap;
   m.table = e->dtable;
@@ -355,12 +358,15 @@ void invalidate_host_plan_for(wp_engine* e, int32_t id) {
     }
 }
 
-// Frees slots, on `stream`: once a slot's copy has landed, its publication
-// is emptied and the adapter's registered entry written back into the table
-// and into the current host-built plan, so kernels enqueued after this never
-// read the slot, and then its buffers are freed on `stream`.  Kernels
-// enqueued before it on `stream` (graph replays included) finish first.  One
-// entry-write launch for up to kMaxEntryWrites / 2 slots.
+// Frees slots, on `stream`: the fill's generation is retired (no plan build
+// after this installs its publication, whether the copy lands before or
+// after) and the adapter's registered entry written back into the table and
+// into the current host-built plan, so kernels enqueued after this never
+// read the slot; its buffers go to the free list behind an event recorded
+// after these writes.  Kernels enqueued before it on `stream` (graph replays
+// included) finish first.  The slot index is free again at once: its next
+// fill publishes a higher generation.  One entry-write launch for up to
+// kMaxEntryWrites / 2 slots.
 int release_slots_on(wp_engine* e, const int* slot_ids, int n, hipStream_t stream) {
   int done = 0;
   while (done < n) {
@@ -370,8 +376,11 @@ int release_slots_on(wp_engine* e, const int* slot_ids, int n, hipStream_t strea
       const int s = slot_ids[done];
       if (s < 0 || e->slots[s].adapter < 0) continue;
       Slot& sl = e->slots[s];
-      if (sl.issued && hipEventQuery(sl.ready) != hipSuccess) WP_HIP(hipStreamWaitEvent(stream, sl.ready, 0));
-      w.clear[w.n_clear++] = e->pubs + s;
+      // The fill's generation is retired in this stream's order; its
+      // publication may land before or after (the copy is not waited for),
+      // and a later fill of the slot publishes a higher generation.
+      w.retire[w.n_retire] = e->retired + s;
+      w.retire_gen[w.n_retire++] = sl.gen;
       Entry reg{};
       auto it = e->adapters.find(sl.adapter);
       if (it != e->adapters.end()) reg = registered_entry(it->second);
@@ -611,6 +620,7 @@ int wp_create(const wp_config* cfg_in, wp_engine** out) {
   const size_t o_cons = carve(sizeof(uint32_t) * e->consumed_words);
   const size_t o_ent = carve(sizeof(Entry) * e->entry_cap);
   const size_t o_pub = carve(sizeof(SlotPub) * std::max(cfg.num_staging_slots, 1));
+  const size_t o_ret = carve(sizeof(uint32_t) * std::max(cfg.num_staging_slots, 1));
   const size_t o_tab = carve(sizeof(Entry) * std::max(e->table_cap, 1));
   const size_t o_spart = carve(sizeof(float) * kMaxChunks * static_cast<size_t>(e->tok_cap) * kMaxRank);
   const size_t hbuf_bytes = sizeof(uint16_t) * static_cast<size_t>(e->tok_cap) * kMaxSlices * kMaxRank;
@@ -626,6 +636,7 @@ int wp_create(const wp_config* cfg_in, wp_engine** out) {
   e->consumed = reinterpret_cast<uint32_t*>(e->ws + o_cons);
   e->plan_entries = reinterpret_cast<Entry*>(e->ws + o_ent);
   e->pubs = reinterpret_cast<SlotPub*>(e->ws + o_pub);
+  e->retired = reinterpret_cast<uint32_t*>(e->ws + o_ret);
   e->dtable = reinterpret_cast<Entry*>(e->ws + o_tab);
   e->spart = reinterpret_cast<float*>(e->ws + o_spart);
   e->hbuf = e->ws + o_hbuf;
@@ -1606,6 +1617,7 @@ int wp_prefetch_adapters(wp_engine* e, const int32_t* adapter_ids, int32_t n, in
     job.b_bytes = ad.b_bytes;
     job.pub = e->pubs + s;
     job.pub_id = adapter_ids[k];
+    job.pub_gen = ++sl.gen;
     job.pub_entry = staged_entry(ad, sl);
     job_slot.push_back(s);
     sl.adapter = adapter_ids[k];

@@ -104,13 +104,17 @@ __device__ void maintain(uint32_t* header, const Maint& m, int* s_flag) {
     const uint32_t s1 = __hip_atomic_load(&p->seq, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
     if ((s1 & 1u) == 0u) {
       const int32_t id = __hip_atomic_load(&p->id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t gen = __hip_atomic_load(&p->gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t retired = __hip_atomic_load(m.retired + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       uint64_t w[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) w[i] = agent_load64(reinterpret_cast<const uint64_t*>(&p->entry) + i);
       // The payload loads complete before the sequence is read again.
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
       const uint32_t s2 = __hip_atomic_load(&p->seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (s1 == s2 && id >= 0 && id < m.table_cap) {
+      // A fill whose release has been enqueued before this build is not
+      // installed again, whichever landed first.
+      if (s1 == s2 && id >= 0 && id < m.table_cap && gen > retired) {
         uint64_t* dst = reinterpret_cast<uint64_t*>(m.table + id);
 #pragma unroll
         for (int i = 0; i < 4; ++i) dst[i] = w[i];
@@ -140,11 +144,12 @@ __global__ __launch_bounds__(256) void maintain_kernel(uint32_t* header, Maint m
 // sequence, with agent-scope release fences between, so a reader that saw
 // the same even value before and after its payload loads has a whole payload.
 // One thread.
-__device__ void publish(SlotPub* pub, int32_t id, const Entry& en) {
+__device__ void publish(SlotPub* pub, int32_t id, uint32_t gen, const Entry& en) {
   const uint32_t base = __hip_atomic_load(&pub->seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & ~1u;
   __hip_atomic_store(&pub->seq, base + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
   __hip_atomic_store(&pub->id, id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(&pub->gen, gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     agent_store64(reinterpret_cast<uint64_t*>(&pub->entry) + i, reinterpret_cast<const uint64_t*>(&en)[i]);
@@ -155,8 +160,9 @@ __device__ void publish(SlotPub* pub, int32_t id, const Entry& en) {
 // One wave; thread 0 writes.
 __global__ __launch_bounds__(64) void entry_writes_kernel(EntryWrites w) {
   if (threadIdx.x != 0) return;
-  if (w.pub != nullptr) publish(w.pub, w.pub_id, w.pub_entry);
-  for (int i = 0; i < w.n_clear; ++i) publish(w.clear[i], -1, Entry{});
+  if (w.pub != nullptr) publish(w.pub, w.pub_id, w.pub_gen, w.pub_entry);
+  for (int i = 0; i < w.n_retire; ++i)
+    __hip_atomic_fetch_max(w.retire[i], w.retire_gen[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   for (int i = 0; i < w.n; ++i) *w.dst[i] = w.val[i];
 }
 
@@ -190,13 +196,13 @@ __global__ __launch_bounds__(256) void stage_copy_kernel(StageJobs jobs) {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
   __syncthreads();
   if (threadIdx.x == 0) {
-    const uint32_t done = __hip_atomic_fetch_add(&job.pub->pad[0], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t done = __hip_atomic_fetch_add(&job.pub->copies, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     s_last = done == kStageWorkgroups - 1 ? 1 : 0;
   }
   __syncthreads();
   if (s_last != 0 && threadIdx.x == 0) {
-    __hip_atomic_store(&job.pub->pad[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    publish(job.pub, job.pub_id, job.pub_entry);
+    __hip_atomic_store(&job.pub->copies, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    publish(job.pub, job.pub_id, job.pub_gen, job.pub_entry);
   }
 }
 
@@ -518,7 +524,7 @@ hipError_t launch_maintain(uint32_t* header, const Maint& m, hipStream_t stream)
 }
 
 hipError_t launch_entry_writes(const EntryWrites& w, hipStream_t stream) {
-  if (w.n < 0 || w.n > kMaxEntryWrites || w.n_clear < 0 || w.n_clear > kMaxEntryWrites) return hipErrorInvalidValue;
+  if (w.n < 0 || w.n > kMaxEntryWrites || w.n_retire < 0 || w.n_retire > kMaxEntryWrites) return hipErrorInvalidValue;
   entry_writes_kernel<<<1, 64, 0, stream>>>(w);
   return hipGetLastError();
 }

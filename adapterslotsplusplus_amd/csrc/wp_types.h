@@ -125,13 +125,19 @@ __host__ __device__ inline constexpr int32_t entry_dtype(int32_t rank_dtype) { r
 // slot's copy has landed, and read by the plan kernel at the start of every
 // step (which then writes `entry` into the adapter table at `id`, so that
 // every kernel of the step sees one table).  A sequence lock guards it: the
-// writer makes `seq` odd, writes id and entry, then makes it even again; a
-// reader uses what it read only if it saw the same even `seq` before and
-// after.  id < 0: the slot publishes nothing.
+// writer makes `seq` odd, writes id, gen and entry, then makes it even
+// again; a reader uses what it read only if it saw the same even `seq`
+// before and after.  id < 0: the slot publishes nothing.  Every fill of a
+// slot has a new generation `gen` (from 1 up); releasing the fill raises the
+// slot's retired generation (a separate word, in the releasing stream's
+// order) to it, and a publication counts only while its generation is above
+// the retired one -- so a release and the slot's next publication, issued on
+// different streams, may land in either order.
 struct SlotPub {  // 48 B
   uint32_t seq;
   int32_t id;
-  uint32_t pad[2];
+  uint32_t copies;  // the copy job's finished workgroups (zero between jobs)
+  uint32_t gen;
   Entry entry;
 };
 
@@ -176,6 +182,7 @@ struct Maint {
   uint32_t* consumed;    // per-block counters
   uint64_t consumed_words;
   const SlotPub* pubs;   // staging slot publications (n_pubs of them)
+  const uint32_t* retired;  // per slot: the highest generation released
   int32_t n_pubs;
   int32_t table_cap;     // entries in `table`
   Entry* table;          // id-indexed adapter table

@@ -110,6 +110,52 @@ def test_captured_step_consumes_staged_adapters_between_replays():
     assert engine.device_errors() == 0
 
 
+def test_release_landing_after_the_next_fill_of_its_slot():
+    """A release held behind a bounded spin on the compute stream while the
+    slot's next fill (the same adapters, the same slot indices) is copied and
+    published on the prefetch stream: the release retires only its own fill,
+    so the next step still uses the new one.  (Emptying the publication at
+    release, as a plain clear would, loses the newer fill here.)"""
+    if not hasattr(torch.cuda, "_sleep"):
+        pytest.skip("torch.cuda._sleep is not available")
+    import time
+
+    engine = WarpPipeEngine()
+    adapters = register_all(engine, seed=40)
+    X = randn((T, D), 41, DT)
+    Y0 = randn((T, O), 42, DT)
+    Xd = X.cuda()
+    idx = routing(0)
+    ref = reference(adapters, X, Y0, idx)
+    slots0 = engine.prefetch_adapters(COLD[0])
+    assert engine.wait_prefetches(COLD[0])
+    assert engine.build_seg_bounds(idx.cuda())
+    Y = Y0.cuda()
+    engine.shrink_expand(Xd, Y, O, R)
+    torch.cuda.synchronize()
+    assert_close(Y, ref, "first fill")
+    announce("release held behind a spin while the slots are filled again")
+    torch.cuda._sleep(100_000_000)
+    engine.release_prefetches(COLD[0])
+    released = torch.cuda.Event()
+    released.record()
+    slots1 = engine.prefetch_adapters(COLD[0])
+    assert sorted(slots1) == sorted(slots0), (slots0, slots1)
+    t0 = time.time()
+    while not all(engine.is_prefetch_ready(a) for a in COLD[0]):
+        assert time.time() - t0 < 10, "the second fill did not land"
+        time.sleep(1e-4)
+    # The order this test is about: the new fills landed first.
+    assert not released.query(), "the spin ended before the second fill landed"
+    assert engine.wait_prefetches(COLD[0])
+    assert engine.build_seg_bounds(idx.cuda())
+    Y = Y0.cuda()
+    engine.shrink_expand(Xd, Y, O, R)
+    torch.cuda.synchronize()
+    assert_close(Y, ref, "second fill")
+    assert engine.device_errors() == 0
+
+
 def test_unstaged_cold_adapter_is_skipped_and_flagged():
     """Negative control of the test above: a replay that routes to cold
     adapters nobody staged skips their tokens and flags them (device error 2);
