@@ -92,7 +92,9 @@ constexpr int kShrinkKSteps = 4;        // 32-wide K-steps per wave per load bat
 // large plans); the fused kernel, which decode-sized plans use, works one
 // tile at a time to keep its registers for occupancy.
 constexpr int kTilesInFlight = kBlockTokens / 16;
-constexpr int kShrinkWavesPerSimd = 4;
+// shrink(): its LDS (two A slices and one X tile per wave: 52 KB at rank 64)
+// holds three workgroups per compute unit.
+constexpr int kShrinkWavesPerSimd = 3;
 
 // kFusedMulti: fused, with several output chunks per expand workgroup.
 // kShrinkOnly: shrink() of decode-sized plans: the fused shrink side, and
@@ -189,7 +191,10 @@ __device__ __forceinline__ void flag_error(uint32_t* header, uint32_t bits) { at
 // timing a little).  Stamps: 0 entry, 1 plan loaded; shrink workgroups 2 first
 // token tile's MFMAs done, 3 partials stored and acknowledged; expand
 // workgroups 2 B and Y loaded, 3 gate open, 4 partials collected, 5 Y
-// stored.  Word 7: role (1 shrink, 2 expand) | block << 8.
+// stored.  Word 7: role (1 shrink, 2 expand) | block << 8.  shrink_kernel
+// (role 3 | block << 8 | d-range << 32): 0 entry, 1 block resolved, 2 slice
+// loop done, 3 partial stored and counted, 4 the last arriver's H stored;
+// word 6: the wave's hardware ids (HW_ID low word, XCC id << 32).
 #ifdef WP_TRACE
 __device__ __forceinline__ void trace_stamp(const ApplyArgs& a, int i) {
   if (a.trace != nullptr && threadIdx.x == 0) {
@@ -200,9 +205,19 @@ __device__ __forceinline__ void trace_stamp(const ApplyArgs& a, int i) {
 __device__ __forceinline__ void trace_tag(const ApplyArgs& a, uint64_t tag) {
   if (a.trace != nullptr && threadIdx.x == 0) a.trace[static_cast<size_t>(blockIdx.x) * kTraceWords + 7] = tag;
 }
+// HW_ID (register 4: wave, SIMD, CU, shader array, engine) and XCC_ID
+// (register 20), read whole.
+__device__ __forceinline__ void trace_hw(const ApplyArgs& a) {
+  if (a.trace != nullptr && threadIdx.x == 0) {
+    const uint32_t hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);
+    const uint32_t xcc = __builtin_amdgcn_s_getreg((31 << 11) | 20);
+    a.trace[static_cast<size_t>(blockIdx.x) * kTraceWords + 6] = hw | (static_cast<uint64_t>(xcc) << 32);
+  }
+}
 #else
 __device__ __forceinline__ void trace_stamp(const ApplyArgs&, int) {}
 __device__ __forceinline__ void trace_tag(const ApplyArgs&, uint64_t) {}
+__device__ __forceinline__ void trace_hw(const ApplyArgs&) {}
 #endif
 
 // A wait on partials that reached its bound: flagged (kErrSpin), and the
@@ -1217,14 +1232,20 @@ template <typename T, int MAXR, bool kMixed>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kShrinkWavesPerSimd)))
 void shrink_kernel(ApplyArgs a) {
   using V8 = typename VecOf<T>::v8;
-  constexpr int MT = (MAXR + 15) / 16;  // 16-row MFMA tiles of the largest rank
-  constexpr int KS = kSliceK / 32;      // K-steps per slice
+  constexpr int MT = (MAXR + 15) / 16;          // 16-row MFMA tiles of the largest rank
+  constexpr int KS = kSliceK / 32;              // K-steps per slice
+  constexpr int XL = 16 * kSliceK / (64 * 8);   // a wave's whole-row X loads per slice (4)
   __shared__ T s_a[2][MT * 16 * kSliceStride];
+  // Each wave's X tile of the current slice: only that wave reads it, after
+  // writing it, so one buffer suffices.
+  __shared__ T s_x[kWaves][16 * kSliceStride];
   __shared__ int s_last;
   const int tid = static_cast<int>(threadIdx.x);
   const int n_kc = a.n_chunks;
   const int b = static_cast<int>(blockIdx.x) / n_kc;
   const int c = static_cast<int>(blockIdx.x) - b * n_kc;
+  trace_stamp(a, 0);
+  trace_hw(a);
   const int n_blocks = static_cast<int>(a.plan.header[kHdrNumBlocks]);
   if (b == a.n_slots - 1 && c == 0 && tid == 0 && n_blocks > a.n_slots) flag_error(a.plan.header, kErrCapacity);
   if (b >= n_blocks) return;
@@ -1234,6 +1255,8 @@ void shrink_kernel(ApplyArgs a) {
     if (res.err != 0 && c == 0 && tid == 0) flag_error(a.plan.header, res.err);
     return;
   }
+  trace_tag(a, 3u | (static_cast<uint64_t>(b) << 8) | (static_cast<uint64_t>(c) << 32));
+  trace_stamp(a, 1);
   const int rank = kMixed ? res.rank : MAXR;
   const int n_mt = kMixed ? (rank + 15) >> 4 : MT;
   const int d = a.d_model;
@@ -1246,8 +1269,9 @@ void shrink_kernel(ApplyArgs a) {
   const int wave = tid >> 6;
   const int row = lane & 15;
   const int kq = (lane >> 4) * 8;
-  const int tl = wave * 16 + row;  // this lane's token slot in the block
-  const int32_t tok = tl < blk.count ? a.plan.bperm[static_cast<int64_t>(b) * kBlockTokens + tl] : -1;
+  const int tl = wave * 16 + row;  // this lane's token slot in the block (MFMA layout)
+  const int32_t* bp = a.plan.bperm + static_cast<int64_t>(b) * kBlockTokens;
+  const int32_t tok = tl < blk.count ? bp[tl] : -1;
   const bool wave_live = wave * 16 < blk.count;
   // Every load below is unconditional, at an address clamped into the
   // operand (a missing token reads X row 0, a rank row past the adapter's
@@ -1255,7 +1279,21 @@ void shrink_kernel(ApplyArgs a) {
   // is not part of the product is zeroed where the data is used.  Straight
   // loads let the compiler wait for exactly the slice it needs while the
   // next one stays in flight.
-  const T* xr = static_cast<const T*>(a.x) + static_cast<int64_t>(tok >= 0 ? tok : 0) * a.ldx;
+  // X is loaded in whole rows (16 lanes per 256-byte row of a slice; lane
+  // moves 8 elements of rows xrow + 4i of its wave's tile) into the wave's
+  // LDS tile and read back in the MFMA layout: X loaded straight in the MFMA
+  // layout moves 64 bytes of 16 rows per instruction, 4.6 vs 6.2 TB/s for
+  // the same bytes, measured on MI355X.
+  const int xrow = lane >> 4;
+  const int xcol = (lane & 15) * 8;
+  const T* xr[XL];
+#pragma unroll
+  for (int i = 0; i < XL; ++i) {
+    const int t = wave * 16 + xrow + 4 * i;
+    const int32_t tk = t < blk.count ? bp[t] : -1;
+    xr[i] = static_cast<const T*>(a.x) + static_cast<int64_t>(tk >= 0 ? tk : 0) * a.ldx;
+  }
+  T* sx = s_x[wave];
   // A slice loads: thread t moves 8 elements of rows t/16 + 16p.
   const int arow = tid >> 4;
   const int acol = (tid & 15) * 8;
@@ -1263,7 +1301,7 @@ void shrink_kernel(ApplyArgs a) {
   const int arow0 = min(arow, rank - 1) * d;
   struct Slice {
     u32x4 a[MT];
-    V8 x[KS];
+    u32x4 x[XL];
   };
   auto load_slice = [&](Slice& sl, int ks0) {
 #pragma unroll
@@ -1272,8 +1310,7 @@ void shrink_kernel(ApplyArgs a) {
       sl.a[p] = load16_global(res.ptr + off);
     }
 #pragma unroll
-    for (int s = 0; s < KS; ++s)
-      sl.x[s] = __builtin_bit_cast(V8, load16_global(xr + min(ks0 + s * 32 + kq, k1 - 8)));
+    for (int i = 0; i < XL; ++i) sl.x[i] = load16_global(xr[i] + min(ks0 + xcol, k1 - 8));
   };
   f32x4 acc[MT];
 #pragma unroll
@@ -1287,13 +1324,16 @@ void shrink_kernel(ApplyArgs a) {
       const bool ok = ks0 + acol < k1 && (!kMixed || p * 16 + arow < rank);
       *reinterpret_cast<u32x4*>(&s_a[buf][(p * 16 + arow) * kSliceStride + acol]) = ok ? sl.a[p] : u32x4{0u, 0u, 0u, 0u};
     }
+#pragma unroll
+    for (int i = 0; i < XL; ++i) *reinterpret_cast<u32x4*>(&sx[(xrow + 4 * i) * kSliceStride + xcol]) = sl.x[i];
     // The slice is in LDS for every wave; the other buffer was last read
     // before this barrier, so the next slice may be written into it.
     lds_barrier();
     if (wave_live && live) {
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        const V8 xf = (tok >= 0 && ks0 + s * 32 + kq < k1) ? sl.x[s] : zero8<T>();
+        const V8 xv = __builtin_bit_cast(V8, *reinterpret_cast<const u32x4*>(&sx[row * kSliceStride + s * 32 + kq]));
+        const V8 xf = (tok >= 0 && ks0 + s * 32 + kq < k1) ? xv : zero8<T>();
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
           if (!kMixed || m < n_mt) {
@@ -1325,6 +1365,7 @@ void shrink_kernel(ApplyArgs a) {
       run_slice(s1, 1, slice_k((i + 1) % n_sl), i + 1 < n_sl, i + 3 < kShrinkSlices, slice_k((i + 3) % n_sl));
     }
   }
+  trace_stamp(a, 2);
   // acc[m]: ranks m*16 + 4*(lane/16) + [0, 4) of token slot tl.
   const int rq = (lane >> 4) * 4;
   T* H = static_cast<T*>(a.h);
@@ -1349,6 +1390,7 @@ void shrink_kernel(ApplyArgs a) {
   uint32_t* counter = &a.consumed[static_cast<int64_t>(b) * kCounterStride];
   if (tid == 0) s_last = atomic_add_u(counter, 1u) == static_cast<unsigned>(n_kc - 1) ? 1 : 0;
   __syncthreads();
+  trace_stamp(a, 3);
   if (s_last == 0) return;
   // Last workgroup of the block: H = rn(alpha * sum_c part[c]) in d-range
   // order, then the counter is reset for the next call.  The partials are
@@ -1391,13 +1433,16 @@ void shrink_kernel(ApplyArgs a) {
     }
   }
   if (tid == 0) atomic_store_u(counter, 0u);
+  trace_stamp(a, 4);
 }
 
 template <typename T>
-hipError_t launch_shrink_t(const ApplyArgs& a, hipStream_t stream) {
-  const int64_t n = static_cast<int64_t>(a.n_slots) * a.n_chunks;
+hipError_t launch_shrink_t(const ApplyArgs& a0, hipStream_t stream) {
+  const int64_t n = static_cast<int64_t>(a0.n_slots) * a0.n_chunks;
   if (n <= 0) return hipSuccess;
   const dim3 grid(static_cast<unsigned>(n));
+  ApplyArgs a = a0;
+  if (a.trace != nullptr && n * kTraceWords > a.trace_words) a.trace = nullptr;
   switch (a.rank) {
     case 8: shrink_kernel<T, 8, false><<<grid, kThreads, 0, stream>>>(a); break;
     case 16: shrink_kernel<T, 16, false><<<grid, kThreads, 0, stream>>>(a); break;

@@ -1,7 +1,7 @@
 """Phase breakdown of the fused decode kernels, from a traced build.
 
     python -m adapterslotsplusplus_amd.build --trace
-    python -m adapterslotsplusplus_amd.trace_phases [--call o_proj|qkv|cfg5_o] [--out FILE]
+    python -m adapterslotsplusplus_amd.trace_phases [--call o_proj|qkv|cfg5_o|cfg4_shrink] [--out FILE]
 
 The traced library (-DWP_TRACE) records, per workgroup, the 100 MHz
 real-time counter at the phase boundaries of one fused launch (thread 0,
@@ -15,6 +15,13 @@ table of each phase's duration (median, p10, p90 over workgroups) and of the
 times, from the first workgroup's entry, at which each role reaches each
 stamp; the same call's duration from HIP events on the normal library is
 measured separately by bench.py.
+
+--call cfg4_shrink traces the large-plan shrink launch of the cfg4 prefill
+chunk instead (shrink() over T=8192 tokens of 16 adapters, r=64, fp16, d=4096,
+8 layers of distinct weights): per workgroup the entry, block resolution,
+slice loop, partial store and count, and for each block's last workgroup
+the d-range sum into H; with each workgroup's compute unit (from its
+hardware ids), the workgroups per compute unit and when each unit finished.
 """
 from __future__ import annotations
 
@@ -35,9 +42,11 @@ def _pct(v, q):
 
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    ap.add_argument("--call", default="o_proj", choices=["o_proj", "qkv", "cfg5_o"])
+    ap.add_argument("--call", default="o_proj", choices=["o_proj", "qkv", "cfg5_o", "cfg4_shrink"])
     ap.add_argument("--out", default=None)
     args = ap.parse_args(argv)
+    if args.call == "cfg4_shrink":
+        return trace_cfg4_shrink(args)
     from . import build as wp_build
 
     if not os.path.exists(wp_build.TRACE_LIB_PATH):
@@ -134,6 +143,119 @@ def main(argv=None):
     row("expand", "MFMA + Y store acknowledged", dur(expand, 4, 5))
     row("expand", "gate open, from the first entry", rel(expand, 3))
     row("expand", "Y stored, from the first entry", rel(expand, 5))
+    text = "\n".join(lines)
+    print(text)
+    if args.out:
+        with open(args.out, "w") as f:
+            f.write(text + "\n")
+
+
+def _load_traced():
+    from . import build as wp_build
+
+    if not os.path.exists(wp_build.TRACE_LIB_PATH):
+        raise SystemExit("build the traced library first: python -m adapterslotsplusplus_amd.build --trace")
+    from . import _lib
+
+    if _lib._lib is not None and _lib.LIB_PATH != wp_build.TRACE_LIB_PATH:
+        raise SystemExit("the normal library is already loaded in this process")
+    _lib.LIB_PATH = wp_build.TRACE_LIB_PATH
+    return _lib
+
+
+def trace_cfg4_shrink(args):
+    _lib = _load_traced()
+    import torch
+
+    from . import workloads as wl
+    from .config import WarpPipeConfig
+    from .engine import WarpPipeEngine
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    T, L, r, h, n_layers, dt = 8192, 16, 64, 4096, 8, torch.float16
+    lens = wl.lognormal_segments(T, L, 6.0, 1.0, seed=4)
+    idx = torch.repeat_interleave(torch.arange(L), torch.tensor(lens)).to(dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(11)
+
+    def rn(shape, std):
+        return (torch.randn(*shape, generator=gen, device=dev, dtype=torch.float32) * std).to(dt)
+
+    # One store layer per model layer: the shrink reads each layer's A.
+    engine = WarpPipeEngine(WarpPipeConfig(layer_stride=L))
+    lib = _lib.load()
+    xs = [rn((T, h), 1.) for _ in range(n_layers)]
+    zb = torch.zeros(8, r, dtype=dt, device=dev)
+    for lay in range(n_layers):
+        for i in range(L):
+            engine.register_adapter(i, rn((r, h), .02), zb, 0.25, rank=r, layer=lay)
+    Hs = [torch.empty(T, r, dtype=dt, device=dev) for _ in range(n_layers)]
+    assert engine.build_seg_bounds(idx)
+    words = 1 << 20
+    buf = torch.zeros(words, dtype=torch.int64, device=dev)
+
+    def call(lay):
+        engine.shrink(xs[lay], h, r, T, out=Hs[lay], layer=lay)
+
+    for lay in range(n_layers):
+        call(lay)
+    torch.cuda.synchronize()
+    for lay in range(n_layers - 1):
+        call(lay)
+    torch.cuda.synchronize()
+    _lib.check(lib.wp_set_trace(engine._handle, buf.data_ptr(), words), "set_trace")
+    call(n_layers - 1)
+    torch.cuda.synchronize()
+    _lib.check(lib.wp_set_trace(engine._handle, None, 0), "set_trace")
+    assert engine.device_errors() == 0
+    tr = buf.view(-1, 8).cpu()
+    live = (tr[:, 7] & 0xFF) == 3
+    rows = tr[live].tolist()
+    t0 = min(x[0] for x in rows)
+    us = 0.01
+
+    def cu_key(hw):
+        xcc = (hw >> 32) & 0xF
+        h32 = hw & 0xFFFFFFFF
+        return (xcc, (h32 >> 13) & 0x7, (h32 >> 12) & 1, (h32 >> 8) & 0xF)
+
+    def rel(i, sel=None):
+        return [(x[i] - t0) * us for x in (sel or rows) if x[i] > 0]
+
+    def dur(i, j, sel=None):
+        return [(x[j] - x[i]) * us for x in (sel or rows) if x[i] > 0 and x[j] > 0]
+
+    last = [x for x in rows if x[4] > 0]
+    end = max(max(x[3] for x in rows), max((x[4] for x in last), default=0))
+    per_cu = {}
+    for x in rows:
+        per_cu.setdefault(cu_key(x[6]), []).append(x)
+    counts = {}
+    for k, v in per_cu.items():
+        counts.setdefault(len(v), []).append(max(max(y[3], y[4]) for y in v))
+    lines = [f"### Phases of one cfg4 `shrink` launch (T={T}, {L} adapters lognormal(6,1) seed 4, r={r}, d={h}, fp16, "
+             f"{n_layers} layers of distinct weights; traced build)", "",
+             f"Workgroups with work: {len(rows)} on {len(per_cu)} compute units ({len(last)} last arrivers); "
+             f"first entry to last stamp {(end - t0) * us:.2f} us.", "",
+             "| phase | median us | p10 | p90 | max |", "|---|---|---|---|---|"]
+
+    def row(phase, v):
+        lines.append(f"| {phase} | {_pct(v, .5):.2f} | {_pct(v, .1):.2f} | {_pct(v, .9):.2f} | {max(v) if v else 0:.2f} |")
+
+    row("entry, from the first entry (dispatch)", rel(0))
+    row("block resolved (entry -> plan and adapter loaded)", dur(0, 1))
+    row("slice loop (-> last MFMA)", dur(1, 2))
+    row("partial store acknowledged + counter", dur(2, 3))
+    row("last arriver: d-range sum + H store", dur(3, 4, last))
+    row("slice loop done, from the first entry", rel(2))
+    row("counted, from the first entry", rel(3))
+    row("H stored (last arrivers), from the first entry", rel(4, last))
+    lines += ["", "| workgroups per compute unit | compute units | finish from first entry: median us | max |",
+              "|---|---|---|---|"]
+    for n in sorted(counts):
+        f = [(v - t0) * us for v in counts[n]]
+        lines.append(f"| {n} | {len(f)} | {_pct(f, .5):.2f} | {max(f):.2f} |")
     text = "\n".join(lines)
     print(text)
     if args.out:
