@@ -175,6 +175,19 @@ def graph_us(fn, reps, warmup=3):
     return e0.elapsed_time(e1) * 1e3 / reps, g
 
 
+def calibration_copy(dev):
+    """One device copy of COPY_BYTES (read and written once): the reference
+    point that scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes."""
+    import torch
+
+    src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 def emit(out):
     print(json.dumps(out), flush=True)
 
@@ -426,6 +439,7 @@ def run_cfg4(args):
             engine.add_lora_packed(ly["y_o"], ly["x"], ly["wa_o"], ly["wb_o"], 0.25)
 
     us, _ = graph_us(calls, max(5, args.steps))
+    calibration_copy(dev)
     b_q = wl.algorithmic_bytes(T, h, 3 * h, [r] * 16)
     b_o = wl.algorithmic_bytes(T, h, h, [r] * 16)
     f_q = wl.algorithmic_flops(T, h, 3 * h, [r] * T)
@@ -771,13 +785,7 @@ def main():
     del layers
     torch.cuda.empty_cache()
 
-    # Calibration copy for the PMC runs: reads and writes COPY_BYTES once.
-    src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
-    dst = torch.empty_like(src)
-    torch.cuda.synchronize()
-    dst.copy_(src)
-    torch.cuda.synchronize()
-    del src, dst
+    calibration_copy(dev)
 
     out = {
         "metric": METRIC,
