@@ -36,7 +36,7 @@ DEVICE_ERR_CAPACITY = 16
 # Every entry point include/warppipe_mi355x.h declares.
 EXPORTED = (
     "wp_last_error", "wp_abi_version", "wp_rank_supported", "wp_block_tokens", "wp_create", "wp_destroy",
-    "wp_register_adapter", "wp_evict_adapter", "wp_has_adapter", "wp_set_entry_offset", "wp_build_segments",
+    "wp_register_adapter", "wp_register_adapter_ref", "wp_evict_adapter", "wp_has_adapter", "wp_set_entry_offset", "wp_build_segments",
     "wp_build_seg_bounds", "wp_read_segments", "wp_read_plan", "wp_read_device_errors",
     "wp_shrink", "wp_expand", "wp_shrink_expand", "wp_add_lora", "wp_prefetch_adapter", "wp_is_prefetch_ready",
     "wp_release_prefetch", "wp_add_lora_static", "wp_wait_prefetch", "wp_set_spin_limit",
@@ -81,6 +81,7 @@ def load():
         "wp_create": ([P(WpConfig), P(p)], ctypes.c_int),
         "wp_destroy": ([p], ctypes.c_int),
         "wp_register_adapter": ([p, i32, p, p, i32, i32, i32, f32, i32, i32, p], ctypes.c_int),
+        "wp_register_adapter_ref": ([p, i32, p, p, i32, i32, i32, f32, i32, p], ctypes.c_int),
         "wp_evict_adapter": ([p, i32, p], ctypes.c_int),
         "wp_has_adapter": ([p, i32], ctypes.c_int),
         "wp_set_entry_offset": ([p, i32, i32], ctypes.c_int),

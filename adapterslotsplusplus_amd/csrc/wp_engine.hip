@@ -84,6 +84,7 @@ struct Adapter {
   void* hB = nullptr;
   size_t a_bytes = 0, b_bytes = 0;
   hipEvent_t copied = nullptr;  // recorded after the registration copy
+  bool borrowed = false;        // dA/dB are the caller's (registered by reference): never freed here
 };
 
 // A staging slot.  Kernels reach its buffers only through the adapter table:
@@ -461,8 +462,8 @@ int evict_impl(wp_engine* e, int32_t id, hipStream_t stream) {
   // Kernels enqueued from here on find no weights for the id; those enqueued
   // before finish before the stream-ordered frees.
   if ((rc = table_write(e, id, Entry{}, stream)) != WP_OK) return rc;
-  if (ad.dA) WP_HIP(hipFreeAsync(ad.dA, stream));
-  if (ad.dB) WP_HIP(hipFreeAsync(ad.dB, stream));
+  if (ad.dA && !ad.borrowed) WP_HIP(hipFreeAsync(ad.dA, stream));
+  if (ad.dB && !ad.borrowed) WP_HIP(hipFreeAsync(ad.dB, stream));
   if (ad.host) {
     hipEvent_t ev = nullptr;
     WP_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
@@ -689,8 +690,8 @@ int wp_destroy(wp_engine* e) {
   (void)hipDeviceSynchronize();
   for (auto& kv : e->adapters) {
     Adapter& ad = kv.second;
-    if (ad.dA) (void)hipFree(ad.dA);
-    if (ad.dB) (void)hipFree(ad.dB);
+    if (ad.dA && !ad.borrowed) (void)hipFree(ad.dA);
+    if (ad.dB && !ad.borrowed) (void)hipFree(ad.dB);
     if (ad.host) (void)hipHostFree(ad.host);
     if (ad.copied) (void)hipEventDestroy(ad.copied);
   }
@@ -758,6 +759,46 @@ int wp_register_adapter(wp_engine* e, int32_t adapter_id, const void* A, const v
     WP_HIP(hipEventCreateWithFlags(&ad.copied, hipEventDisableTiming));
     WP_HIP(hipEventRecord(ad.copied, stream));
   }
+  e->adapters[adapter_id] = ad;
+  return table_write(e, adapter_id, registered_entry(ad), stream);
+}
+
+int wp_register_adapter_ref(wp_engine* e, int32_t adapter_id, const void* A, const void* B, int32_t rank,
+                            int32_t d_model, int32_t out_features, float alpha_scale, int32_t dtype, void* stream_) {
+  if (!e) return fail(WP_ERR_INVALID, "register_adapter_ref: engine is NULL");
+  if (!rank_ok(rank)) return fail(WP_ERR_INVALID, "register_adapter: unsupported rank %d (only 8/16/32/64)", rank);
+  if (dtype != WP_DTYPE_F16 && dtype != WP_DTYPE_BF16) return fail(WP_ERR_INVALID, "register_adapter: bad dtype");
+  if (d_model <= 0 || d_model % 8 != 0) return fail(WP_ERR_INVALID, "register_adapter: d_model must be a positive multiple of 8");
+  if (out_features <= 0 || out_features % 4 != 0)
+    return fail(WP_ERR_INVALID, "register_adapter: out_features must be a positive multiple of 4");
+  if (!A || !B) return fail(WP_ERR_INVALID, "register_adapter: null weights");
+  if (!aligned(A, 16) || !aligned(B, 16))
+    return fail(WP_ERR_INVALID, "AdapterStore::register_adapter: A/B pointer not 16-byte aligned");
+  DeviceGuard g(e->device);
+  // The kernels read the pointers directly: they must be device memory of
+  // this engine's device.
+  for (const void* p : {A, B}) {
+    hipPointerAttribute_t at{};
+    if (hipPointerGetAttributes(&at, p) != hipSuccess || at.type != hipMemoryTypeDevice || at.device != e->device) {
+      (void)hipGetLastError();
+      return fail(WP_ERR_INVALID, "register_adapter_ref: A/B must be device memory of device %d", e->device);
+    }
+  }
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  if (stream_capturing(stream)) return fail(WP_ERR_STATE, "register_adapter cannot run during graph capture");
+  int rc = evict_impl(e, adapter_id, stream);
+  if (rc != WP_OK) return rc;
+  Adapter ad;
+  ad.rank = rank;
+  ad.d = d_model;
+  ad.o = out_features;
+  ad.dtype = dtype;
+  ad.alpha = alpha_scale;
+  ad.a_bytes = sizeof(uint16_t) * static_cast<size_t>(rank) * d_model;
+  ad.b_bytes = sizeof(uint16_t) * static_cast<size_t>(out_features) * rank;
+  ad.dA = const_cast<void*>(A);
+  ad.dB = const_cast<void*>(B);
+  ad.borrowed = true;
   e->adapters[adapter_id] = ad;
   return table_write(e, adapter_id, registered_entry(ad), stream);
 }

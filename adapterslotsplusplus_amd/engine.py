@@ -140,12 +140,15 @@ class WarpPipeEngine:
             raise RuntimeError(f"{what} is on {t.device}, the engine on {self.device}")
 
     # ------------------------------------------------------- adapter store --
-    def register_adapter(self, adapter_id, A, B, alpha_scale, rank=None, layer=None):
+    def register_adapter(self, adapter_id, A, B, alpha_scale, rank=None, layer=None, copy=True):
         """A [rank, d], B [o, rank], contiguous fp16/bf16 (reference engine.py:12-14,
         bindings:110-119).  CUDA tensors: the adapter is device-resident.  CPU
         tensors: it goes to the pinned host store and is usable once prefetched.
         layer (multi-layer store, config.layer_stride > 0): the layer these
-        weights belong to."""
+        weights belong to.  copy=False (CUDA tensors only): the store keeps
+        the tensors themselves, as the reference's pointer registry does
+        (adapter_store.h:21-27) -- no copy, in-place updates to them are seen
+        by later calls; the engine holds a reference to them until eviction."""
         sid = self._store_id(adapter_id, layer)
         rank = int(rank or self.config.rank)
         if A.is_cuda != B.is_cuda:
@@ -164,9 +167,16 @@ class WarpPipeEngine:
             raise RuntimeError(
                 f"A must be [rank={rank}, d] and B [o, rank={rank}]; got {tuple(A.shape)} and {tuple(B.shape)}")
         host = 0 if A.is_cuda else 1
-        _lib.check(self._lib.wp_register_adapter(self._handle, sid, _ptr(A), _ptr(B), rank, d_model,
-                                                 out_features, float(alpha_scale), dt, host, self._stream()),
-                   "register_adapter")
+        if not copy:
+            if host:
+                raise RuntimeError("register_adapter(copy=False) needs CUDA tensors")
+            _lib.check(self._lib.wp_register_adapter_ref(self._handle, sid, _ptr(A), _ptr(B), rank, d_model,
+                                                         out_features, float(alpha_scale), dt, self._stream()),
+                       "register_adapter")
+        else:
+            _lib.check(self._lib.wp_register_adapter(self._handle, sid, _ptr(A), _ptr(B), rank, d_model,
+                                                     out_features, float(alpha_scale), dt, host, self._stream()),
+                       "register_adapter")
         # Keeps the source alive until the stream-ordered copy has run (the
         # reference holds the tensors until eviction as well, bindings:118).
         self._held[sid] = (A, B) if host == 0 else None

@@ -98,6 +98,16 @@ int wp_register_adapter(wp_engine* e, int32_t adapter_id, const void* A, const v
                         int32_t d_model, int32_t out_features, float alpha_scale, int32_t dtype,
                         int32_t host_resident, void* stream);
 
+/* AdapterStore::register_adapter as the reference keeps it (csrc/memory/
+ * adapter_store.h:21-27: a registry of the caller's pointers, nothing copied):
+ * A [rank, d] and B [o, rank] are device memory of the engine's device that
+ * the caller keeps alive, unchanged in layout, until the id is evicted or
+ * registered again and the work enqueued before that has finished; kernels
+ * read them in place, so updates the caller makes to them are seen by later
+ * calls.  Evicting such an id frees nothing.  Re-registering an id replaces it. */
+int wp_register_adapter_ref(wp_engine* e, int32_t adapter_id, const void* A, const void* B, int32_t rank,
+                            int32_t d_model, int32_t out_features, float alpha_scale, int32_t dtype, void* stream);
+
 /* Replaces WarpPipeExtension::evict_adapter (bindings:121-124).  Silent for an
  * unknown id (adapter_store.h:29).  Also releases a staging slot held by the id. */
 int wp_evict_adapter(wp_engine* e, int32_t adapter_id, void* stream);
