@@ -128,6 +128,27 @@ hipError_t launch_expand(int dtype_bf16, const ApplyArgs& a, hipStream_t stream)
 // may capture it in a graph).
 hipError_t launch_fill_u32(uint32_t* p, uint32_t v, size_t n, hipStream_t stream);
 
+// The base linear plus its per-token LoRA delta in one launch (see
+// linear_kernel): a is an add_lora call's arguments (stacked weights, the
+// kShrinkOnly split, a.h the token-indexed H rows, a.y the output), l the
+// GEMM's.
+struct LinearArgs {
+  const void* w;        // [n_out, ldw] base weight (the I/O type)
+  int64_t ldw;
+  const void* bias;     // [n_out] or null
+  int32_t n_out;        // multiple of 16
+  int32_t tokens;       // rows of x and y
+  int32_t groups;       // token groups of 128
+  int32_t splits;       // K-ranges per column tile
+  int32_t k_range;      // columns of x per K-range (multiple of 128)
+  int32_t pad;
+  float* gpart;         // [groups][n_out / 16][splits][128][16] fp32 partials
+  uint32_t* tile_cnt;   // [groups * n_out / 16] counters (zero between calls)
+  uint32_t* hflag;      // [n_slots] H-ready flags (zero between calls)
+  uint32_t* hcnt;       // [n_slots] readers counted on each flag (zero between calls)
+};
+hipError_t launch_linear(int dtype_bf16, const ApplyArgs& a, const LinearArgs& l, hipStream_t stream);
+
 // Output columns one expand workgroup produces.
 int expand_cols_per_workgroup();
 // Waves per SIMD the fused kernel for `rank` (0: mixed) runs at, single- or

@@ -1517,12 +1517,314 @@ hipError_t launch_role(int dtype_bf16, const ApplyArgs& a, hipStream_t stream) {
   return dtype_bf16 ? launch_rank<__bf16, ROLE, 1>(a, stream) : launch_rank<_Float16, ROLE, 1>(a, stream);
 }
 
+// ------------------------------------------------------- linear + LoRA ----
+//
+// y = rn(rn(x . W^T + bias) + H_tok . B_tok^T), H = rn(scale . x . A_tok^T):
+// a decode step's base linear and its per-token LoRA delta (add_lora's
+// stacked weights, device plan of 16-token blocks) in one launch.  Roles, in
+// dispatch order; a role waits only on roles dispatched before it, so the
+// waits end whatever the residency:
+//   * shrink workgroups: the fused kernels' (block, rank group, d-range)
+//     partials of H into the partial buffer;
+//   * one reducer per block: the block's H rows (token-indexed, device-
+//     coherent stores) from its partials, kPartialEmpty restored, then the
+//     block's H flag set;
+//   * GEMM workgroups (token group g of kLinTokens, column tile of kLinCols
+//     outputs, K-range s of l.splits): x . W^T over the K-range into the GEMM
+//     partial buffer.  X goes through a wave-private LDS tile in whole rows
+//     and W through a shared, double-buffered one (K-slices of kSliceK); each
+//     wave owns 32 tokens.  The tile's last workgroup to count sums the
+//     partials in K order, adds the bias and rounds (the base output), waits
+//     for every block's H flag, adds each block's H . B^T (one MFMA per 32
+//     ranks) into the tokens' rows, rounds and stores y; it then counts itself
+//     on every block's flag, and the flag's last reader clears it.
+constexpr int kLinTokens = 128;
+constexpr int kLinCols = 16;
+constexpr int kLinWavesPerSimd = 3;  // its LDS (43.5 KB) holds three workgroups per compute unit
+
+template <typename T>
+__device__ __forceinline__ void coherent_store_pair(T* p, float x, float y) {
+  typename VecOf<T>::v2 o;
+  o[0] = static_cast<T>(x);
+  o[1] = static_cast<T>(y);
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __builtin_bit_cast(uint32_t, o), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <typename T, int RANK>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kLinWavesPerSimd)))
+void linear_kernel(const uint32_t* header, const Block* __restrict__ blocks, const int32_t* __restrict__ bperm,
+                   int32_t n_shrink, ApplyArgs a, LinearArgs l) {
+  using V8 = typename VecOf<T>::v8;
+  constexpr int KS = (RANK + 31) / 32;
+  constexpr int XL = 32 * kSliceK / (64 * 8);      // a wave's whole-row X loads per slice (8)
+  constexpr int WL = kLinCols * kSliceK / (kThreads * 8);  // W loads per thread per slice (1)
+  static_assert(WL == 1, "one W load per thread and slice");
+  // sx: each wave's 32 X rows of the slice; sw: the slice's W rows, double
+  // buffered.  The epilogue's fp32 tile reuses sx.
+  __shared__ T sx[kLinTokens * kSliceStride];
+  __shared__ T sw[2][kLinCols * kSliceStride];
+  __shared__ int s_flag;
+  const int tid = static_cast<int>(threadIdx.x);
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int row = lane & 15;
+  const int kq = (lane >> 4) * 8;
+  const int wg = static_cast<int>(blockIdx.x);
+  // Blocks the grid has reducer slots for; a plan with more (only ids the
+  // call cannot resolve make one) is reported, and the rest skipped.
+  const int n_plan = static_cast<int>(header[kHdrNumBlocks]);
+  const int n_blocks = min(n_plan, a.n_slots);
+  if (wg == 0 && tid == 0 && n_plan > a.n_slots) flag_error(a.plan.header, kErrCapacity);
+  const uint32_t poison = header[kHdrPoison];
+
+  if (wg < n_shrink) {
+    // --- shrink: the kShrinkOnly role's split (32-row rank groups).
+    const int per = a.n_chunks * a.n_rgroups;
+    const int b = wg / per;
+    const int part = wg - b * per;
+    const int rg = part / a.n_chunks;
+    const int c = part - rg * a.n_chunks;
+    if (b >= n_blocks || poison != 0u) return;
+    const Block blk = blocks[b];
+    const int32_t tok0 = bperm[static_cast<int64_t>(b) * kBlockTokens + row];
+    const int32_t t0 = row < blk.count ? tok0 : -1;
+    const Resolved<T> res = resolve_a<T>(a, blk);
+    if (res.err != 0 && part == 0 && tid == 0) flag_error(a.plan.header, res.err);
+    shrink_body<T, kShrinkRowsFused / 16>(a, b, c, 0, rg * kShrinkRowsFused, blk, t0, res,
+                                          reinterpret_cast<f32x4*>(sx));
+    return;
+  }
+  if (wg < n_shrink + a.n_slots) {
+    // --- reducer of block b: H rows, then the flag.
+    const int b = wg - n_shrink;
+    if (b >= n_blocks) return;
+    const Block blk = blocks[b];
+    if (poison == 0u) {
+      const Resolved<T> res = resolve_a<T>(a, blk);
+      const int wrote = res.ptr != nullptr ? res.rank : 0;
+      if (wrote > 0) {
+        bool ok = true;
+        if (blk.count * wrote * a.n_chunks > 2048) ok = wait_partials<false>(a, blk, wrote, &s_flag);
+        if (ok) {
+          T* H = static_cast<T*>(a.h);
+          const int32_t* toks = bperm + static_cast<int64_t>(b) * kBlockTokens;
+          collect_partials<8>(a, blk, wrote / 2, res.alpha, [&](int j, int r0, f32x2 v) {
+            coherent_store_pair<T>(H + static_cast<int64_t>(toks[j]) * a.ldh + r0, v[0], v[1]);
+          });
+          __syncthreads();
+          clear_partials(a, blk, wrote, tid, kThreads);
+        }
+      }
+    }
+    // The H stores have landed (s_waitcnt) before the flag.
+    wait_vm();
+    __syncthreads();
+    if (tid == 0) atomic_store_u(&l.hflag[b], 1u);
+    return;
+  }
+
+  // --- GEMM.
+  const int n_tiles = l.n_out / kLinCols;
+  const int gw = wg - n_shrink - a.n_slots;
+  const int ks = gw % l.splits;
+  const int jt = (gw / l.splits) % n_tiles;
+  const int g = gw / (l.splits * n_tiles);
+  const int K = a.d_model;
+  const int kb = ks * l.k_range;
+  const int ke = min(kb + l.k_range, K);
+  const int n_sl = (ke - kb) / kSliceK;
+  const int xrow = lane >> 4;
+  const int xcol = (lane & 15) * 8;
+  const T* X = static_cast<const T*>(a.x);
+  const T* Wt = static_cast<const T*>(l.w);
+  // This lane's X rows (clamped to the last token: rows past T are computed
+  // and never stored) and its W row.
+  const T* xr[XL];
+#pragma unroll
+  for (int i = 0; i < XL; ++i) {
+    const int t = g * kLinTokens + wave * 32 + xrow + 4 * i;
+    xr[i] = X + static_cast<int64_t>(min(t, l.tokens - 1)) * a.ldx;
+  }
+  const T* wr = Wt + static_cast<int64_t>(jt * kLinCols + (tid >> 4)) * l.ldw + (tid & 15) * 8;
+  T* sxw = sx + wave * 32 * kSliceStride;
+  struct Slice {
+    u32x4 x[XL];
+    u32x4 w;
+  };
+  auto load_slice = [&](Slice& sl, int i) {
+    const int k = kb + min(i, n_sl - 1) * kSliceK;
+#pragma unroll
+    for (int q = 0; q < XL; ++q) sl.x[q] = load16_global(xr[q] + k + xcol);
+    sl.w = load16_global(wr + k);
+  };
+  f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  auto run_slice = [&](Slice& sl, int buf, int i) {
+#pragma unroll
+    for (int q = 0; q < XL; ++q) *reinterpret_cast<u32x4*>(&sxw[(xrow + 4 * q) * kSliceStride + xcol]) = sl.x[q];
+    *reinterpret_cast<u32x4*>(&sw[buf][(tid >> 4) * kSliceStride + (tid & 15) * 8]) = sl.w;
+    lds_barrier();
+    if (i < n_sl) {
+#pragma unroll
+      for (int s = 0; s < kSliceK / 32; ++s) {
+        const V8 wf = __builtin_bit_cast(V8, *reinterpret_cast<const u32x4*>(&sw[buf][row * kSliceStride + s * 32 + kq]));
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+          const V8 xf = __builtin_bit_cast(
+              V8, *reinterpret_cast<const u32x4*>(&sxw[(m * 16 + row) * kSliceStride + s * 32 + kq]));
+          acc[m] = mfma16(wf, xf, acc[m]);
+        }
+      }
+    }
+    load_slice(sl, i + 2);
+  };
+  Slice s0, s1;
+  load_slice(s0, 0);
+  load_slice(s1, 1);
+  for (int i = 0; i < n_sl; i += 2) {
+    run_slice(s0, 0, i);
+    run_slice(s1, 1, i + 1);
+  }
+  // acc[m]: output columns jt*16 + 4*(lane/16) + [0, 4) of token
+  // g*128 + wave*32 + m*16 + lane%16.  Stored coherently; counted below.
+  const int rq = (lane >> 4) * 4;
+  const int64_t tile = static_cast<int64_t>(g) * n_tiles + jt;
+  float* gp = l.gpart + tile * l.splits * (kLinTokens * kLinCols);
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+    coherent_store_f4(gp + static_cast<int64_t>(ks) * (kLinTokens * kLinCols) + (wave * 32 + m * 16 + row) * kLinCols + rq,
+                      acc[m]);
+  wait_vm();
+  __syncthreads();
+  if (tid == 0) s_flag = atomic_add_u(&l.tile_cnt[tile], 1u) == static_cast<unsigned>(l.splits - 1) ? 1 : 0;
+  __syncthreads();
+  if (s_flag == 0) return;
+
+  // --- epilogue of the tile (one workgroup): base output, then the delta.
+  float* et = reinterpret_cast<float*>(sx);  // [kLinTokens][kLinCols] fp32
+  constexpr int kUnits = kLinTokens * kLinCols / 4 / kThreads;  // f32x4 units per thread (2)
+#pragma unroll
+  for (int i = 0; i < kUnits; ++i) {
+    const int u = tid + i * kThreads;
+    f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < l.splits; ++s) sum += coherent_load_f4(gp + static_cast<int64_t>(s) * (kLinTokens * kLinCols) + u * 4);
+    const int c4 = (u * 4) % kLinCols;
+    if (l.bias != nullptr) {
+      const T* bias = static_cast<const T*>(l.bias) + jt * kLinCols + c4;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) sum[q] += static_cast<float>(bias[q]);
+    }
+    // The base output is rounded to the I/O type, as the base linear's is.
+#pragma unroll
+    for (int q = 0; q < 4; ++q) sum[q] = static_cast<float>(static_cast<T>(sum[q]));
+    *reinterpret_cast<f32x4*>(et + u * 4) = sum;
+  }
+  if (tid == 0) atomic_store_u(&l.tile_cnt[tile], 0u);
+  // Every block's H flag (one wave polls, bounded; after a give-up, or
+  // while the partial buffer is poisoned, the delta is left out).
+  if (tid < 64) {
+    int ok = poison == 0u ? 1 : 0;
+    for (unsigned spins = 0; ok; ++spins) {
+      bool here = true;
+      for (int b = lane; b < n_blocks; b += 64) here = here && atomic_load_u(&l.hflag[b]) != 0u;
+      if (__all(here)) break;
+      if (spins >= a.spin_limit || poisoned(a.plan.header)) {
+        ok = 0;
+        if (lane == 0 && spins >= a.spin_limit) give_up(a.plan.header);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+    // A give-up elsewhere in the call leaves H unreliable: no delta then.
+    if (lane == 0) s_flag = ok && !poisoned(a.plan.header);
+  }
+  __syncthreads();
+  if (s_flag != 0) {
+    const T* H = static_cast<const T*>(a.h);
+    for (int b = wave; b < n_blocks; b += kWaves) {
+      const Block blk = blocks[b];
+      const Resolved<T> rb = resolve_b<T>(a, blk, 0);
+      if (rb.ptr == nullptr) continue;
+      // A operand: B rows jt*16 + row; B operand: the block's token rows of H.
+      const int32_t tk = row < blk.count ? bperm[static_cast<int64_t>(b) * kBlockTokens + row] : -1;
+      f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const int k = s * 32 + kq;
+        const V8 bf = k < RANK ? load8(rb.ptr + static_cast<int64_t>(jt * kLinCols + row) * RANK + k) : zero8<T>();
+        V8 hf = zero8<T>();
+        if (tk >= 0 && k < RANK) {
+          const T* hp = H + static_cast<int64_t>(tk) * a.ldh + k;
+          const u32x2 lo = __builtin_bit_cast(u32x2, coherent_load8(hp));
+          const u32x2 hi = __builtin_bit_cast(u32x2, coherent_load8(hp + 4));
+          hf = __builtin_bit_cast(V8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+        }
+        d = mfma16(bf, hf, d);
+      }
+      // d: columns rq..rq+3 of token tk.  Tokens of other groups and padding
+      // rows are not this tile's.
+      const int tl = tk - g * kLinTokens;
+      if (tk >= 0 && tl >= 0 && tl < kLinTokens) {
+        float* dst = et + tl * kLinCols + rq;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) dst[q] += d[q];
+      }
+    }
+  }
+  __syncthreads();
+  T* Y = static_cast<T*>(a.y);
+#pragma unroll
+  for (int i = 0; i < kUnits; ++i) {
+    const int u = tid + i * kThreads;
+    const int tl = (u * 4) / kLinCols;
+    const int c4 = (u * 4) % kLinCols;
+    const int t = g * kLinTokens + tl;
+    if (t < l.tokens) store4(Y + static_cast<int64_t>(t) * a.ldy + jt * kLinCols + c4, *reinterpret_cast<const f32x4*>(et + u * 4));
+  }
+  // This tile has read every flag and H row it needs.
+  const unsigned readers = static_cast<unsigned>(l.groups * n_tiles);
+  for (int b = tid; b < n_blocks; b += kThreads) {
+    if (atomic_add_u(&l.hcnt[b], 1u) == readers - 1) {
+      atomic_store_u(&l.hcnt[b], 0u);
+      atomic_store_u(&l.hflag[b], 0u);
+    }
+  }
+}
+
+template <typename T>
+hipError_t launch_linear_t(const ApplyArgs& a, const LinearArgs& l, int32_t n_shrink, hipStream_t stream) {
+  const int64_t n = static_cast<int64_t>(n_shrink) + a.n_slots +
+                    static_cast<int64_t>(l.groups) * (l.n_out / kLinCols) * l.splits;
+  const dim3 grid(static_cast<unsigned>(n));
+  switch (a.rank) {
+    case 8: linear_kernel<T, 8><<<grid, kThreads, 0, stream>>>(a.plan.header, a.plan.blocks, a.plan.bperm, n_shrink, a, l); break;
+    case 16: linear_kernel<T, 16><<<grid, kThreads, 0, stream>>>(a.plan.header, a.plan.blocks, a.plan.bperm, n_shrink, a, l); break;
+    case 32: linear_kernel<T, 32><<<grid, kThreads, 0, stream>>>(a.plan.header, a.plan.blocks, a.plan.bperm, n_shrink, a, l); break;
+    case 64: linear_kernel<T, 64><<<grid, kThreads, 0, stream>>>(a.plan.header, a.plan.blocks, a.plan.bperm, n_shrink, a, l); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 __global__ __launch_bounds__(kThreads) void fill_u32_kernel(uint32_t* __restrict__ p, uint32_t v, size_t n) {
   const size_t stride = static_cast<size_t>(gridDim.x) * kThreads;
   for (size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; i < n; i += stride) p[i] = v;
 }
 
 }  // namespace
+
+hipError_t launch_linear(int dtype_bf16, const ApplyArgs& a, const LinearArgs& l, hipStream_t stream) {
+  // The shrink side is the kShrinkOnly split; the GEMM side needs whole
+  // K-slices and column tiles, and token groups covering the rows.
+  if (a.srows != kShrinkRowsFused || a.n_chunks < 1 || a.n_chunks > kMaxChunks || a.w.n_a != 1 ||
+      a.w.mode != kStacked || a.tiles != 1 || l.n_out % kLinCols != 0 || a.d_model % kSliceK != 0 ||
+      l.k_range % kSliceK != 0 || l.splits < 1 || static_cast<int64_t>(l.splits) * l.k_range < a.d_model ||
+      static_cast<int64_t>(l.splits - 1) * l.k_range >= a.d_model || l.tokens < 1 ||
+      static_cast<int64_t>(l.groups) * kLinTokens < l.tokens || (l.ldw % 8) != 0 || (a.ldx % 8) != 0)
+    return hipErrorInvalidValue;
+  const int32_t n_shrink = a.n_slots * a.n_chunks * a.n_rgroups;
+  return dtype_bf16 ? launch_linear_t<__bf16>(a, l, n_shrink, stream) : launch_linear_t<_Float16>(a, l, n_shrink, stream);
+}
 
 hipError_t launch_fill_u32(uint32_t* p, uint32_t v, size_t n, hipStream_t stream) {
   if (n == 0) return hipSuccess;

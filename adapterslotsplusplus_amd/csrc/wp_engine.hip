@@ -180,6 +180,9 @@ constexpr int kUploadRing = 4;
 // Adapter-table size when the configuration gives none.
 constexpr int32_t kDefaultTableIds = 1 << 16;
 constexpr int32_t kMaxTableIds = 1 << 22;
+// Column-tile counters of linear_lora: (token groups x output columns / 16)
+// of one call at most.
+constexpr int kLinCounters = 1 << 16;
 // Staging slots an engine may have (publications are applied by one thread each).
 constexpr int kMaxStagingSlots = 256;
 
@@ -219,6 +222,8 @@ struct wp_engine {
   void* hbuf = nullptr;         // [tok_cap][kMaxSlices x kMaxRank] 2-byte H of large-plan add_lora calls
   SlotPub* pubs = nullptr;      // [num_staging_slots] staging publications
   uint32_t* retired = nullptr;  // [num_staging_slots] highest released generation per slot
+  uint32_t* lin_cnt = nullptr;  // [kLinCounters] column-tile counters of linear_lora (zero between calls)
+  uint32_t* lin_flag = nullptr; // [2][block_cap] H flags and their reader counts (zero between calls)
   Entry* dtable = nullptr;      // [table_cap] id-indexed adapter table of build_seg_bounds plans
   int table_cap = 0;
   int seg_cap = 0, block_cap = 0, tok_cap = 0, entry_cap = 0;
@@ -622,6 +627,7 @@ int wp_create(const wp_config* cfg_in, wp_engine** out) {
   const size_t o_ent = carve(sizeof(Entry) * e->entry_cap);
   const size_t o_pub = carve(sizeof(SlotPub) * std::max(cfg.num_staging_slots, 1));
   const size_t o_ret = carve(sizeof(uint32_t) * std::max(cfg.num_staging_slots, 1));
+  const size_t o_lin = carve(sizeof(uint32_t) * (kLinCounters + 2 * static_cast<size_t>(e->block_cap)));
   const size_t o_tab = carve(sizeof(Entry) * std::max(e->table_cap, 1));
   const size_t o_spart = carve(sizeof(float) * kMaxChunks * static_cast<size_t>(e->tok_cap) * kMaxRank);
   const size_t hbuf_bytes = sizeof(uint16_t) * static_cast<size_t>(e->tok_cap) * kMaxSlices * kMaxRank;
@@ -638,6 +644,8 @@ int wp_create(const wp_config* cfg_in, wp_engine** out) {
   e->plan_entries = reinterpret_cast<Entry*>(e->ws + o_ent);
   e->pubs = reinterpret_cast<SlotPub*>(e->ws + o_pub);
   e->retired = reinterpret_cast<uint32_t*>(e->ws + o_ret);
+  e->lin_cnt = reinterpret_cast<uint32_t*>(e->ws + o_lin);
+  e->lin_flag = e->lin_cnt + kLinCounters;
   e->dtable = reinterpret_cast<Entry*>(e->ws + o_tab);
   e->spart = reinterpret_cast<float*>(e->ws + o_spart);
   e->hbuf = e->ws + o_hbuf;
@@ -1331,6 +1339,71 @@ int wp_add_lora(wp_engine* e, void* y, const void* x, const void* wa, int64_t wa
                 int64_t y_row_stride, int32_t dtype, void* stream) {
   return add_lora_impl(e, "add_lora", y, x, 1, &wa, &wa_stride0, num_loras, n_slices, wb, wb_stride0, out_features,
                        y_col_offsets, scale, rank, d_model, T, y_row_stride, dtype, stream);
+}
+
+int wp_linear_lora(wp_engine* e, void* y, const void* x, const void* w, int64_t w_row_stride, const void* bias,
+                   const void* wa, int64_t wa_stride0, const void* wb, int64_t wb_stride0, int32_t num_loras,
+                   float scale, int32_t rank, int32_t d_in, int32_t d_out, int64_t T, int32_t dtype, void* stream_) {
+  const char* who = "linear_lora";
+  if (!e) return fail(WP_ERR_INVALID, "%s: engine is NULL", who);
+  ApplyArgs a{};
+  const int32_t off0 = 0;
+  int rc = stacked_call_args(who, y, x, 1, &wa, &wa_stride0, num_loras, 1, &wb, &wb_stride0, &d_out, &off0, scale,
+                             rank, d_in, d_out, dtype, &a);
+  if (rc != WP_OK) return rc;
+  if ((rc = check_io(who, dtype, w, "w")) != WP_OK) return rc;
+  if (!w) return fail(WP_ERR_INVALID, "%s: null weight", who);
+  if (!aligned(y, 16)) return fail(WP_ERR_INVALID, "%s: y must be 16-byte aligned", who);
+  if (bias && !aligned(bias, 2)) return fail(WP_ERR_INVALID, "%s: bias must be 2-byte aligned", who);
+  if (w_row_stride < d_in || w_row_stride % 8 != 0)
+    return fail(WP_ERR_INVALID, "%s: weight row stride %lld must be >= d_in and a multiple of 8", who,
+                (long long)w_row_stride);
+  if (T < 1) return fail(WP_ERR_INVALID, "%s: x has no rows", who);
+  if (e->plan_kind == 0) return fail(WP_ERR_STATE, "%s: no segment table (call build_seg_bounds first)", who);
+  if (e->plan_T > T)
+    return fail(WP_ERR_INVALID, "%s: segments reach token %lld but x has %lld rows", who, (long long)e->plan_T,
+                (long long)T);
+  // Decode-sized plans (16-token blocks) and whole 128-column K-slices and
+  // 16-column output tiles only; the caller runs the linear and add_lora
+  // otherwise.
+  if (e->plan_bt > 16 || d_in % 128 != 0 || d_out % 16 != 0 || T > kSmallPlanTokens) return WP_NOT_HANDLED;
+  DeviceGuard g(e->device);
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  a.tiles = 1;
+  a.ptok = e->ptok;
+  a.part = e->part;
+  a.consumed = e->consumed;
+  a.spin_limit = e->spin_limit;
+  a.plan = plan_view(e);
+  a.n_slots = block_bound(e, num_loras);
+  a.h = e->hbuf;
+  a.ldh = rank;
+  shrink_small_split(d_in, rank, &a);
+  LinearArgs l{};
+  l.w = w;
+  l.ldw = w_row_stride;
+  l.bias = bias;
+  l.n_out = d_out;
+  l.tokens = static_cast<int32_t>(T);
+  l.groups = static_cast<int32_t>(ceil_div(T, 128));
+  // K-ranges: about two GEMM workgroups per compute unit, whole K-slices,
+  // within the partial buffer.
+  const int64_t tiles = static_cast<int64_t>(l.groups) * (d_out / 16);
+  if (tiles > kLinCounters) return WP_NOT_HANDLED;
+  const int64_t slices = d_in / 128;
+  int64_t splits = std::max<int64_t>(1, std::min<int64_t>(slices, (2 * static_cast<int64_t>(e->n_cu) + tiles / 2) / tiles));
+  const uint64_t part_floats = static_cast<uint64_t>(kMaxChunks) * e->tok_cap * kMaxRank;
+  while (splits > 1 && static_cast<uint64_t>(tiles) * splits * 128 * 16 > part_floats) --splits;
+  if (static_cast<uint64_t>(tiles) * splits * 128 * 16 > part_floats) return WP_NOT_HANDLED;
+  l.k_range = static_cast<int32_t>(ceil_div(slices, splits) * 128);
+  l.splits = static_cast<int32_t>(ceil_div(d_in, l.k_range));
+  l.gpart = e->spart;
+  l.tile_cnt = e->lin_cnt;
+  l.hflag = e->lin_flag;
+  l.hcnt = e->lin_flag + e->block_cap;
+  if (a.n_slots > e->block_cap) return fail(WP_ERR_CAPACITY, "%s: more block slots than the engine holds", who);
+  WP_HIP(launch_linear(dtype == WP_DTYPE_BF16, a, l, stream));
+  return WP_OK;
 }
 
 int wp_add_lora_nslice(wp_engine* e, void* y, const void* x, int32_t n_slices, const void* const* wa,

@@ -358,6 +358,52 @@ class WarpPipeEngine:
                                                      o_arr, y_arr, rank, int(Y.size(0)), int(Y.size(-1)), dt,
                                                      self._stream()), "shrink_expand_slices")
 
+    def linear_lora(self, x, weight, bias, wa_t_all, wb_t_all, scale, out=None):
+        """The base linear and its per-token LoRA delta in one launch (not in the
+        reference, whose draft wrapper runs F.linear and then bgmv_shrink /
+        bgmv_expand into its output, serve_multitenant.py:56-87):
+        y = rn(rn(x . W^T + bias) + rn(scale . x . A[idx]^T) . B[idx]^T) over
+        the last build_seg_bounds table.  x [T, in]; weight [out, in]; bias
+        [out] or None; wa_t_all [L, 1, r, in], wb_t_all [L, 1, out, r].
+        Returns y ([T, out], new unless `out` is given), or None when the
+        shapes have no kernel (the caller then runs F.linear and
+        add_lora_packed)."""
+        self._on_device(x, "x")
+        self._on_device(weight, "weight")
+        for t, nm in ((wa_t_all, "wa_t_all"), (wb_t_all, "wb_t_all")):
+            self._on_device(t, nm)
+        dt = _dtype_code(x, "x")
+        if weight.dtype != x.dtype or wa_t_all.dtype != x.dtype or wb_t_all.dtype != x.dtype or (
+                bias is not None and bias.dtype != x.dtype):
+            raise RuntimeError("linear_lora: x, weight, bias and the LoRA weights must share one dtype")
+        x2 = x.reshape(-1, x.size(-1))
+        if not x2.is_contiguous() or not wa_t_all.is_contiguous() or not wb_t_all.is_contiguous():
+            raise RuntimeError("linear_lora: x and the LoRA weights must be contiguous")
+        if weight.dim() != 2 or weight.stride(1) != 1:
+            raise RuntimeError("linear_lora: weight must be [out, in] with unit column stride")
+        T, d_in = int(x2.size(0)), int(x2.size(1))
+        d_out = int(weight.size(0))
+        rank = int(wb_t_all.size(-1))
+        L = int(wa_t_all.size(0))
+        if int(weight.size(1)) != d_in or int(wa_t_all.size(-1)) != d_in or int(wa_t_all.size(-2)) != rank:
+            raise RuntimeError("linear_lora: weight / wa_t_all do not match x's width")
+        if int(wb_t_all.size(0)) != L or int(wb_t_all.size(-2)) != d_out:
+            raise RuntimeError("linear_lora: wb_t_all must be [L, 1, out, r]")
+        if bias is not None:
+            self._on_device(bias, "bias")
+            if bias.numel() != d_out or not bias.is_contiguous():
+                raise RuntimeError("linear_lora: bias must be a contiguous [out] tensor")
+        y = out if out is not None else torch.empty(T, d_out, dtype=x.dtype, device=x.device)
+        self._on_device(y, "out")
+        if tuple(y.shape) != (T, d_out) or not y.is_contiguous() or y.dtype != x.dtype:
+            raise RuntimeError("linear_lora: out must be a contiguous [T, out] tensor of x's dtype")
+        rc = _lib.check(self._lib.wp_linear_lora(self._handle, _ptr(y), _ptr(x2), _ptr(weight), int(weight.stride(0)),
+                                                 _ptr(bias) if bias is not None else None, _ptr(wa_t_all),
+                                                 int(wa_t_all.stride(0)), _ptr(wb_t_all), int(wb_t_all.stride(0)), L,
+                                                 float(scale), rank, d_in, d_out, T, dt, self._stream()),
+                        "linear_lora")
+        return y if rc == _lib.WP_OK else None
+
     def add_lora_packed(self, y, x, wa_t_all, wb_t_all, scale, y_offset=None, y_slice_size=None) -> bool:
         """y += (scale * x . A[idx]^T) . B[idx]^T for the tokens of the last
         build_seg_bounds table (reference engine.py:56-62, bindings:195-234).

@@ -43,11 +43,16 @@ class DraftLoRAContext:
     tokens: the fixed number of flattened rows a step's linears see (B * S);
     idx holds one adapter id per row (-1: no LoRA for that row)."""
 
-    def __init__(self, engine: WarpPipeEngine, tokens: int, scale: float = 2.0, device=None):
+    def __init__(self, engine: WarpPipeEngine, tokens: int, scale: float = 2.0, device=None,
+                 fused_linear: bool = False):
         self.engine = engine
         self.tokens = int(tokens)
         self.scale = float(scale)
         self.mode = "lora"
+        # True: each wrapped linear runs its base GEMM and LoRA delta as one
+        # engine launch (engine.linear_lora), falling back to F.linear +
+        # add_lora_packed for shapes without that kernel.
+        self.fused_linear = bool(fused_linear)
         dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
         self.idx = torch.zeros(self.tokens, dtype=torch.int64, device=dev)
 
@@ -91,6 +96,16 @@ class WarpPipeLoRALinear(nn.Module):
         self.register_buffer("wb_t_all", B.detach().unsqueeze(1).contiguous(), persistent=False)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.ctx.mode != "none" and self.ctx.fused_linear:
+            x2d = x.reshape(-1, self.in_features)
+            if not x2d.is_contiguous():
+                x2d = x2d.contiguous()
+            if x2d.size(0) != self.ctx.tokens:
+                raise RuntimeError(
+                    f"WarpPipeLoRALinear: {x2d.size(0)} rows, but the step's routing covers {self.ctx.tokens} tokens")
+            y = self.ctx.engine.linear_lora(x2d, self.weight, self.bias, self.wa_t_all, self.wb_t_all, self.ctx.scale)
+            if y is not None:
+                return y.view(*x.shape[:-1], self.out_features)
         y = F.linear(x, self.weight, self.bias)
         if self.ctx.mode == "none":
             return y

@@ -655,8 +655,9 @@ def run_draft(args):
     lora_mods = [m for m in model.modules() if hasattr(m, "wa_t_all")]
     res = {}
     with torch.inference_mode():
-        for mode in ("none", "lora", "forked"):
-            ctx.mode = "lora" if mode == "forked" else mode
+        for mode in ("none", "lora", "forked", "fused"):
+            ctx.mode = "lora" if mode in ("forked", "fused") else mode
+            ctx.fused_linear = mode == "fused"
             for m in lora_mods:
                 if mode == "forked":
                     m.forward = (lambda mm: (lambda xx: forked(mm, xx)))(m)
@@ -671,11 +672,17 @@ def run_draft(args):
             res[mode] = us
         for m in lora_mods:
             m.__dict__.pop("forward", None)
+        ctx.fused_linear = False
     emit({"workload": "draft step: 22 x (q, k, v, o) bf16 linears h=2048 on T=128 (32 tenants x 4), "
                       "WarpPipeLoRALinear r=32 on all 88, routing table + forward in one graph",
           "us_per_step_base_only": round(res["none"], 1), "us_per_step_with_lora": round(res["lora"], 1),
           "lora_us_per_step": round(res["lora"] - res["none"], 1),
           "lora_us_per_call": round((res["lora"] - res["none"]) / 88, 2),
+          "fused_linear": {"us_per_step": round(res["fused"], 1),
+                           "lora_us_per_call": round((res["fused"] - res["none"]) / 88, 2),
+                           "note": "each projection's base GEMM and LoRA delta as one launch (engine.linear_lora, "
+                                   "DraftLoRAContext(fused_linear=True)); lora_us_per_call is the step's time over the "
+                                   "base-only step per projection"},
           "forked_delta": {"us_per_step": round(res["forked"], 1),
                            "lora_us_per_call": round((res["forked"] - res["none"]) / 88, 2),
                            "note": "delta on a forked stream beside the base GEMM, added after the join "

@@ -181,6 +181,22 @@ int wp_expand(wp_engine* e, const void* H, void* Y, int32_t out_features, int32_
 int wp_shrink_expand(wp_engine* e, const void* X, void* Y, int32_t d_model, int32_t out_features, int32_t rank,
                      int64_t T, int64_t y_row_stride, int32_t y_col_offset, int32_t dtype, void* stream);
 
+/* A base linear and its per-token LoRA delta in one launch: replaces the
+ * sequence the reference's draft-model wrapper runs per projection
+ * (BGMVLoRALinear.forward, benchmarks/e2e/serve_multitenant.py:56-87: the
+ * base F.linear, then bgmv_shrink and bgmv_expand into its output):
+ *   y[T, d_out] = rn( rn(x . W^T + bias) + rn(scale . x . A_i^T) . B_i^T )
+ * per token, i its adapter in the last build_seg_bounds table (tokens with
+ * id -1: the base output alone).  W is [d_out, w_row_stride] (torch's Linear
+ * layout), bias [d_out] or NULL; wa / wb are add_lora's stacked weights
+ * (wa_t_all [num_loras, 1, rank, d_in], wb_t_all [num_loras, 1, d_out,
+ * rank]); x [T, d_in] and y [T, d_out] contiguous.  WP_NOT_HANDLED (the
+ * caller runs the linear and add_lora instead) for a rank without kernels,
+ * T over 512, d_in not a multiple of 128 or d_out not a multiple of 16. */
+int wp_linear_lora(wp_engine* e, void* y, const void* x, const void* w, int64_t w_row_stride, const void* bias,
+                   const void* wa, int64_t wa_stride0, const void* wb, int64_t wb_stride0, int32_t num_loras,
+                   float scale, int32_t rank, int32_t d_in, int32_t d_out, int64_t T, int32_t dtype, void* stream);
+
 /* shrink_expand over several layers of a multi-layer store in one launch (no
  * reference counterpart): slice s applies, to every token of the last
  * build_seg_bounds table, the adapter registered under id_offsets[s] + the
