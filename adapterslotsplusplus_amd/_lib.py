@@ -41,7 +41,7 @@ EXPORTED = (
     "wp_shrink", "wp_expand", "wp_shrink_expand", "wp_add_lora", "wp_prefetch_adapter", "wp_is_prefetch_ready",
     "wp_release_prefetch", "wp_add_lora_static", "wp_wait_prefetch", "wp_set_spin_limit",
     "wp_add_lora_nslice", "wp_prefetch_adapters", "wp_release_prefetches", "wp_wait_prefetches", "wp_set_trace",
-    "wp_shrink_expand_slices", "wp_linear_lora",
+    "wp_shrink_expand_slices", "wp_linear_lora", "wp_read_probe",
 )
 
 
@@ -106,6 +106,7 @@ def load():
         "wp_linear_lora": ([p, p, p, p, i64, p, p, i64, p, i64, i32, f32, i32, i32, i32, i64, i32, p], ctypes.c_int),
         "wp_add_lora_nslice": ([p, p, p, i32, p, p, p, p, p, p, i32, f32, i32, i32, i64, i64, i32, p], ctypes.c_int),
         "wp_set_spin_limit": ([p, ctypes.c_uint32], ctypes.c_int),
+        "wp_read_probe": ([p, p, i64, p, p], ctypes.c_int),
         "wp_add_lora_static": ([p, p, p, i32, i64, p, i64, i32, i32, p, p, p, p, f32, i32, i32, i64, i32, p],
                                ctypes.c_int),
     }

@@ -149,6 +149,13 @@ struct LinearArgs {
 };
 hipError_t launch_linear(int dtype_bf16, const ApplyArgs& a, const LinearArgs& l, hipStream_t stream);
 
+// Streams `bytes` (a multiple of 16) from p with 16-byte non-temporal loads
+// over `workgroups` workgroups of 512 threads and stores nothing but an
+// improbable fold into sink (512 x 16 bytes); bytes == 0 launches one
+// workgroup that does nothing.  A measurement of the device's read rate and
+// launch cost, not part of any call.
+hipError_t launch_read_probe(const void* p, size_t bytes, void* sink, int workgroups, hipStream_t stream);
+
 // Output columns one expand workgroup produces.
 int expand_cols_per_workgroup();
 // Waves per SIMD the fused kernel for `rank` (0: mixed) runs at, single- or

@@ -1812,6 +1812,15 @@ int wp_set_trace(wp_engine* e, void* buffer, int64_t n_words) {
   return WP_OK;
 }
 
+int wp_read_probe(wp_engine* e, const void* buffer, int64_t bytes, void* sink, void* stream) {
+  if (!e) return fail(WP_ERR_INVALID, "read_probe: engine is NULL");
+  if (bytes < 0 || bytes % 16 != 0 || (bytes > 0 && !aligned(buffer, 16)) || !sink || !aligned(sink, 16))
+    return fail(WP_ERR_INVALID, "read_probe: a 16-byte aligned buffer of a multiple of 16 bytes and a 8 KiB sink");
+  DeviceGuard g(e->device);
+  WP_HIP(launch_read_probe(buffer, static_cast<size_t>(bytes), sink, 2 * e->n_cu, static_cast<hipStream_t>(stream)));
+  return WP_OK;
+}
+
 int wp_set_spin_limit(wp_engine* e, uint32_t polls) {
   if (!e) return fail(WP_ERR_INVALID, "set_spin_limit: engine is NULL");
   e->spin_limit = polls == 0xFFFFFFFFu ? kDefaultSpinLimit : polls;

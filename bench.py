@@ -175,6 +175,41 @@ def graph_us(fn, reps, warmup=3):
     return e0.elapsed_time(e1) * 1e3 / reps, g
 
 
+def measure_floor(engine, dev, n_calls, sizes, reps):
+    """Per-launch time of the library's read probe (wp_read_probe: 16-byte
+    non-temporal loads over two workgroups per compute unit) reading each of
+    `sizes` bytes, over n_calls distinct buffers in one graph (no call finds
+    its bytes in cache), and of an empty launch.  Reading a call's bytes once
+    in one launch is a floor under that call's kernel: the call also writes Y
+    and has the shrink -> expand dependency to hide."""
+    import ctypes
+
+    import torch
+
+    from adapterslotsplusplus_amd import _lib
+
+    lib = _lib.load()
+    stride = (max(sizes) + 255) // 256 * 256
+    buf = torch.empty(n_calls * stride, dtype=torch.uint8, device=dev).fill_(1)
+    sink = torch.zeros(8192, dtype=torch.uint8, device=dev)
+    base = buf.data_ptr()
+
+    def probe(off, nbytes):
+        return lambda: _lib.check(lib.wp_read_probe(engine._handle, ctypes.c_void_p(base + off), nbytes,
+                                                    ctypes.c_void_p(sink.data_ptr()),
+                                                    ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
+                                  "read_probe")
+
+    out = {}
+    for nbytes in sizes:
+        nb = nbytes // 16 * 16
+        out[nbytes] = launch_duration_us([probe(i * stride, nb) for i in range(n_calls)], reps)
+    out[0] = launch_duration_us([probe(0, 0) for _ in range(n_calls)], reps)
+    del buf, sink
+    torch.cuda.empty_cache()
+    return out
+
+
 def calibration_copy(dev):
     """One device copy of COPY_BYTES (read and written once): the reference
     point that scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes."""
@@ -792,6 +827,10 @@ def main():
     del layers
     torch.cuda.empty_cache()
 
+    log("floor: read probe")
+    fl = measure_floor(engine, dev, n_layers, [bytes_qkv, bytes_o], reps)
+    floor_step_us = n_layers * (fl[bytes_qkv] + fl[bytes_o])
+
     calibration_copy(dev)
 
     out = {
@@ -831,6 +870,18 @@ def main():
                     "us_per_launch": round(o_us, 3), "bytes_per_launch": bytes_o,
                     "achieved": round(bytes_o / (o_us * 1e-6) / 1e9, 2)},
             },
+        },
+        # What one launch needs just to read a call's bytes (wp_read_probe over
+        # distinct buffers, graph of 40 launches), and an empty launch: the
+        # step's calls cannot take less than floor_step_us.
+        "floor": {
+            "qkv_read_us": round(fl[bytes_qkv], 3),
+            "o_proj_read_us": round(fl[bytes_o], 3),
+            "empty_launch_us": round(fl[0], 3),
+            "floor_step_us": round(floor_step_us, 1),
+            "floor_step_frac_of_hbm_peak": round(bytes_step / (floor_step_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+            "step_frac_of_floor": round(floor_step_us / (ms_step * 1e3), 4),
+            "qkv_frac_of_floor": round(fl[bytes_qkv] / qkv_us, 4),
         },
     }
     if not args.no_secondary:

@@ -300,6 +300,14 @@ int wp_wait_prefetches(wp_engine* e, const int32_t* adapter_ids, int32_t n, void
  * repaired the buffer. */
 int wp_set_spin_limit(wp_engine* e, uint32_t polls);
 
+/* Measurement, no reference counterpart: reads `bytes` (a multiple of 16) of
+ * device memory at `buffer` once, with 16-byte non-temporal loads over two
+ * workgroups per compute unit, on `stream`; `sink` is 8 KiB of device memory
+ * the kernel may write.  bytes == 0 launches an empty kernel.  bench.py times
+ * it to state the floor of a call: the time one launch takes to read that
+ * call's bytes, and the launch cost alone. */
+int wp_read_probe(wp_engine* e, const void* buffer, int64_t bytes, void* sink, void* stream);
+
 /* Diagnostics: in a library built with WP_TRACE (adapterslotsplusplus_amd.build
  * --trace), fused launches whose grid fits record 8 timestamps per workgroup
  * into the device buffer (n_words 64-bit words; NULL stops tracing).  In a
