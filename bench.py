@@ -212,7 +212,9 @@ def measure_floor(engine, dev, n_calls, sizes, reps):
 
 def calibration_copy(dev):
     """One device copy of COPY_BYTES (read and written once): the reference
-    point that scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes."""
+    point that scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes.
+    Returns its rate in GB/s (bytes read + written over the copy's time; the
+    first copy, the one the counters see, then two more timed)."""
     import torch
 
     src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
@@ -220,7 +222,16 @@ def calibration_copy(dev):
     torch.cuda.synchronize()
     dst.copy_(src)
     torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(2):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    gbs = 2 * 2 * COPY_BYTES / (e0.elapsed_time(e1) * 1e-3) / 1e9
     del src, dst
+    return gbs
 
 
 def emit(out):
@@ -807,6 +818,32 @@ def main():
     torch.cuda.synchronize()
     ms_step = ev0.elapsed_time(ev1) / args.steps
     value = bytes_step / (ms_step * 1e-3) / 1e9
+    assert engine.device_errors() == 0
+    del g
+
+    # The same step with the tokens sorted by adapter (the same per-adapter
+    # token counts, fewer and longer runs): the plan groups tokens by adapter
+    # either way, so the apply kernels see the same blocks.
+    sorted_us = None
+    if not args.no_secondary:
+        log("sorted routing")
+        idx_unsorted = idx.clone()
+        idx.copy_(torch.sort(idx_unsorted).values)
+        gs = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gs):
+            step()
+        for _ in range(args.warmup):
+            gs.replay()
+        torch.cuda.synchronize()
+        ev0.record()
+        for _ in range(args.steps):
+            gs.replay()
+        ev1.record()
+        torch.cuda.synchronize()
+        sorted_us = ev0.elapsed_time(ev1) * 1e3 / args.steps
+        assert engine.device_errors() == 0
+        del gs
+        idx.copy_(idx_unsorted)
 
     # Per-launch durations of the two fused kernels (one launch per call),
     # over the 40 distinct layers so no call hits in cache.
@@ -831,7 +868,7 @@ def main():
     fl = measure_floor(engine, dev, n_layers, [bytes_qkv, bytes_o], reps)
     floor_step_us = n_layers * (fl[bytes_qkv] + fl[bytes_o])
 
-    calibration_copy(dev)
+    copy_gbs = calibration_copy(dev)
 
     out = {
         "metric": METRIC,
@@ -882,6 +919,8 @@ def main():
             "floor_step_frac_of_hbm_peak": round(bytes_step / (floor_step_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
             "step_frac_of_floor": round(floor_step_us / (ms_step * 1e3), 4),
             "qkv_frac_of_floor": round(fl[bytes_qkv] / qkv_us, 4),
+            "read_GB_s_qkv_bytes": round(bytes_qkv / (fl[bytes_qkv] * 1e-6) / 1e9, 1),
+            "copy_GB_s_256MiB": round(copy_gbs, 1),
         },
     }
     if not args.no_secondary:
@@ -898,6 +937,9 @@ def main():
         out["cfg5_us_per_step"] = c5["44_launches_nslice"]["us_per_step"]
         out["cfg1_us_per_call"] = c1["us_per_call"]
         out["secondary"] = {
+            "cfg2_sorted_routing": {"us_per_step": round(sorted_us, 2),
+                                    "GB_s": round(bytes_step / (sorted_us * 1e-6) / 1e9, 2),
+                                    "workload": "the cfg2 step with the same tokens sorted by adapter"},
             "flatness": {**flat, "workload": "cfg2 shapes, 8 layers x (qkv, o_proj) per graph, N resident adapters"},
             "cfg5_draft_step": {**c5, "workload": "h=2048, 22 layers x (q, k, v, o), T=128 (32 tenants x 4), r=32, "
                                                   "bf16, build_seg_bounds + the calls in one graph; cfg5_us_per_step "

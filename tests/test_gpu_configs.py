@@ -36,11 +36,15 @@ def test_cfg1_reference_cpu_case():
     add_lora_check(engine, idx, x, y0, wa, [wb], [0], 1.0, "cfg1")
 
 
-def test_cfg2_llama7b_decode_calls():
+@pytest.mark.parametrize("order", ["unsorted", "sorted"])
+def test_cfg2_llama7b_decode_calls(order):
     """configs[1]: 256 Zipf(1.1)-routed tokens, 64 adapters, r=32, bf16;
-    the o_proj call and the packed-qkv call (3 slices at offsets 0/4096/8192)."""
+    the o_proj call and the packed-qkv call (3 slices at offsets 0/4096/8192),
+    with the tokens in routing order and sorted by adapter."""
     c = wl.CFG2
     idx = wl.zipf_indices(c["T"], c["n_adapters"], c["zipf_s"], c["routing_seed"])
+    if order == "sorted":
+        idx = torch.sort(idx).values
     qkv, o = wl.llama7b_decode_layer_pair(c["T"], c["n_adapters"], c["rank"], c["dtype"], seed=20)
     x = wl.normal((c["T"], 4096), 1.0, c["dtype"], 30)
     engine = WarpPipeEngine()
