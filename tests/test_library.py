@@ -74,3 +74,4 @@ def test_null_engine_arguments_are_errors_not_crashes():
     assert lib.wp_prefetch_adapter(None, 0, ctypes.byref(slot)) == _lib.WP_ERR_INVALID
     with pytest.raises(RuntimeError, match="engine is NULL"):
         _lib.check(lib.wp_evict_adapter(None, 0, None), "evict_adapter")
+    assert lib.wp_read_probe(None, None, 0, None, None) == _lib.WP_ERR_INVALID
