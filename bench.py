@@ -719,6 +719,44 @@ def run_draft(args):
         for m in lora_mods:
             m.__dict__.pop("forward", None)
         ctx.fused_linear = False
+
+    # The same draft model with q/k/v packed: one base GEMM over their
+    # stacked weights and one LoRA launch with one adapter pair per
+    # projection (WarpPipeLoRAPackedLinear), o_proj as before.
+    from adapterslotsplusplus_amd.lora_linear import WarpPipeLoRAPackedLinear, WarpPipeLoRALinear
+
+    class PackedBlock(nn.Module):
+        def __init__(self, i):
+            super().__init__()
+            bases = []
+            for n in ("q_proj", "k_proj", "v_proj"):
+                lin = nn.Linear(h, h, bias=False, device=dev, dtype=dt)
+                with torch.no_grad():
+                    lin.weight.copy_(rn((h, h), 0.02))
+                bases.append(lin)
+            ws = [weights[f"{i}.{n}"] for n in ("q_proj", "k_proj", "v_proj")]
+            self.qkv = WarpPipeLoRAPackedLinear(bases, [w[0] for w in ws], [w[1] for w in ws], ctx)
+            o = nn.Linear(h, h, bias=False, device=dev, dtype=dt)
+            with torch.no_grad():
+                o.weight.copy_(rn((h, h), 0.02))
+            self.o_proj = WarpPipeLoRALinear(o, *weights[f"{i}.o_proj"], ctx)
+
+        def forward(self, x):
+            q, k, v = self.qkv(x)
+            return x + self.o_proj(F.silu(q + k + v))
+
+    packed = nn.Sequential(*[PackedBlock(i) for i in range(n_layers)]).eval()
+    res_p = {}
+    with torch.inference_mode():
+        for mode in ("none", "lora"):
+            ctx.mode = mode
+
+            def step_p():
+                ctx.begin_step()
+                return packed(x)
+
+            us, _ = graph_us(step_p, max(5, args.steps))
+            res_p[mode] = us
     emit({"workload": "draft step: 22 x (q, k, v, o) bf16 linears h=2048 on T=128 (32 tenants x 4), "
                       "WarpPipeLoRALinear r=32 on all 88, routing table + forward in one graph",
           "us_per_step_base_only": round(res["none"], 1), "us_per_step_with_lora": round(res["lora"], 1),
@@ -732,7 +770,14 @@ def run_draft(args):
           "forked_delta": {"us_per_step": round(res["forked"], 1),
                            "lora_us_per_call": round((res["forked"] - res["none"]) / 88, 2),
                            "note": "delta on a forked stream beside the base GEMM, added after the join "
-                                   "(not used by WarpPipeLoRALinear)"}})
+                                   "(not used by WarpPipeLoRALinear)"},
+          "packed_qkv": {"us_per_step_base_only": round(res_p["none"], 1),
+                         "us_per_step_with_lora": round(res_p["lora"], 1),
+                         "lora_us_per_step": round(res_p["lora"] - res_p["none"], 1),
+                         "lora_us_per_layer": round((res_p["lora"] - res_p["none"]) / n_layers, 2),
+                         "note": "q/k/v as one WarpPipeLoRAPackedLinear (one base GEMM over the stacked weights, "
+                                 "one LoRA launch with an adapter pair per projection), o_proj as "
+                                 "WarpPipeLoRALinear: 44 LoRA launches per step"}})
 
 
 def main():
