@@ -864,6 +864,19 @@ def main():
     ms_step = ev0.elapsed_time(ev1) / args.steps
     value = bytes_step / (ms_step * 1e-3) / 1e9
     assert engine.device_errors() == 0
+
+    # Each of 200 further replays timed on its own (an event pair around
+    # every replay): the median and the spread beside the mean above.
+    n_med = 200
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n_med)]
+    for e0_, e1_ in evs:
+        e0_.record()
+        g.replay()
+        e1_.record()
+    torch.cuda.synchronize()
+    per = sorted(e0_.elapsed_time(e1_) * 1e3 for e0_, e1_ in evs)
+    step_median = {"replays": n_med, "median_us": round(per[n_med // 2], 2), "p10_us": round(per[n_med // 10], 2),
+                   "p90_us": round(per[(9 * n_med) // 10], 2)}
     del g
 
     # The same step with the tokens sorted by adapter (the same per-adapter
@@ -925,6 +938,7 @@ def main():
         "ms_per_step": round(ms_step, 4),
         "us_per_step": round(ms_step * 1e3, 2),
         "frac_of_hbm_peak": round(value / PEAK_HBM_GBS, 4),
+        "us_per_step_individually_timed": step_median,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
