@@ -1161,13 +1161,33 @@ int stacked_call_args(const char* who, void* y, const void* x, int32_t n_a, cons
 // slices) give each workgroup several chunks, so that the block's partials are
 // summed fewer times -- and the shrink side in 32-row groups for those
 // multi-chunk calls (half the shrink workgroups, so more of the expand side is
-// resident from the start), 16-row groups otherwise.
+// resident from the start), 16-row groups otherwise; except that calls small
+// enough run one chunk per expand workgroup (below).
 void fused_split(ApplyArgs* a, int rank, int d_model, int n_cu) {
+  const int64_t resident = static_cast<int64_t>(n_cu) * fused_waves_per_simd(rank, 0);
   a->n_sub = static_cast<int>(ceil_div(a->n_ochunks, kExpandWorkgroups));
+  if (a->n_sub > 1) {
+    // Several slices, but a grid small enough that the single-chunk kernel
+    // (16-row shrink groups, one output chunk per expand workgroup, every
+    // workgroup's B and Y loaded before the wait) needs at most twice the
+    // workgroups the device holds at once: that kernel, not the multi-chunk
+    // one that loads its later chunks only after the partials are in.
+    // Measured on MI355X: cfg5's q/k/v (one A per slice) 44-launch step
+    // 535 -> 462 us, cfg2 flatness at 1..16 resident adapters 183 -> 168 us
+    // (N=1); allowing three times the residency slowed cfg2's qkv call
+    // (18.0 -> 19.8 us).
+    ApplyArgs one = *a;
+    shrink_split(d_model, rank, kShrinkRows, a->w.n_a, a->hs, a->n_slots, a->n_ochunks, resident, &one);
+    const int64_t per_block = static_cast<int64_t>(one.n_chunks) * one.n_rgroups * a->w.n_a + a->n_ochunks;
+    if (a->n_slots * per_block <= 2 * resident) {
+      one.n_sub = 1;
+      *a = one;
+      return;
+    }
+  }
   const int multi = a->n_sub > 1 ? 1 : 0;
   shrink_split(d_model, rank, multi ? kShrinkRowsFused : kShrinkRows, a->w.n_a, a->hs, a->n_slots,
-               ceil_div(a->n_ochunks, a->n_sub), multi ? 0 : static_cast<int64_t>(n_cu) * fused_waves_per_simd(rank, multi),
-               a);
+               ceil_div(a->n_ochunks, a->n_sub), multi ? 0 : resident, a);
 }
 
 }  // namespace

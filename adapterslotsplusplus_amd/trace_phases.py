@@ -1,7 +1,7 @@
 """Phase breakdown of the fused decode kernels, from a traced build.
 
     python -m adapterslotsplusplus_amd.build --trace
-    python -m adapterslotsplusplus_amd.trace_phases [--call o_proj|qkv|cfg5_o|cfg4_shrink] [--out FILE]
+    python -m adapterslotsplusplus_amd.trace_phases [--call o_proj|qkv|cfg5_o|cfg5_qkv|cfg4_shrink] [--out FILE]
 
 The traced library (-DWP_TRACE) records, per workgroup, the 100 MHz
 real-time counter at the phase boundaries of one fused launch (thread 0,
@@ -42,7 +42,7 @@ def _pct(v, q):
 
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    ap.add_argument("--call", default="o_proj", choices=["o_proj", "qkv", "cfg5_o", "cfg4_shrink"])
+    ap.add_argument("--call", default="o_proj", choices=["o_proj", "qkv", "cfg5_o", "cfg5_qkv", "cfg4_shrink"])
     ap.add_argument("--out", default=None)
     args = ap.parse_args(argv)
     if args.call == "cfg4_shrink":
@@ -64,7 +64,7 @@ def main(argv=None):
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    if args.call == "cfg5_o":
+    if args.call in ("cfg5_o", "cfg5_qkv"):
         T, L, r, h, n_layers = 128, 32, 32, 2048, 40
         idx = torch.repeat_interleave(torch.arange(L), 4).to(dev)
     else:
@@ -78,8 +78,11 @@ def main(argv=None):
     def rn(shape, std):
         return (torch.randn(*shape, generator=gen, device=dev, dtype=torch.float32) * std).to(dt)
 
-    n_slices = 3 if args.call == "qkv" else 1
-    layers = [dict(wa=rn((L, 1, r, h), .02), wb=[rn((L, 1, h, r), .02) for _ in range(n_slices)],
+    n_slices = 3 if args.call in ("qkv", "cfg5_qkv") else 1
+    # cfg5_qkv: one A per slice (add_lora_packed_nslice's form), the others one shared A.
+    per_slice_a = args.call == "cfg5_qkv"
+    layers = [dict(wa=[rn((L, 1, r, h), .02) for _ in range(n_slices)] if per_slice_a else rn((L, 1, r, h), .02),
+                   wb=[rn((L, 1, h, r), .02) for _ in range(n_slices)],
                    x=rn((T, h), 1.), y=rn((T, n_slices * h), 1.)) for _ in range(n_layers)]
     engine = WarpPipeEngine()
     lib = _lib.load()
