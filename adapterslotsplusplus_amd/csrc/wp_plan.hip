@@ -233,18 +233,24 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
   const int tid = threadIdx.x;
   const int e0 = tid * E;
 
+  // 1. ids, loaded first so that their latency overlaps the maintenance's
+  //    (the routing does not depend on the adapter table).
+  long long ids[E];
+#pragma unroll
+  for (int k = 0; k < E; ++k) {
+    const int i = tid + k * NT;
+    ids[k] = 0;
+    if (i < T)
+      ids[k] = idx_is_int64 ? static_cast<const long long*>(idx)[i]
+                            : static_cast<long long>(static_cast<const int*>(idx)[i]);
+  }
+
   // 0. Publications into the adapter table; the partial buffer's repair.
   maintain(header, m, s_scan);
 
-  // 1. ids -> LDS.
-  for (int i = tid; i < CAP; i += NT) {
-    long long v = 0;
-    if (i < T) {
-      v = idx_is_int64 ? static_cast<const long long*>(idx)[i]
-                       : static_cast<long long>(static_cast<const int*>(idx)[i]);
-    }
-    s_id[i] = v;
-  }
+  // ids -> LDS.
+#pragma unroll
+  for (int k = 0; k < E; ++k) s_id[tid + k * NT] = ids[k];
   lds_barrier();
 
   // 2. Run starts in token order (reference :484): s_a[r] = first token of run r.
