@@ -238,10 +238,11 @@ def emit(out):
     print(json.dumps(out), flush=True)
 
 
-def measure_flatness(reps):
-    """cfg2 shapes with N resident adapters, N = 1..128 (Zipf(1.1), seed 1):
-    8 layers x {qkv, o_proj} with distinct weights per layer, one graph per N.
-    Returns the rows and max/min of the latency."""
+def measure_flatness(reps, sort=False):
+    """cfg2 shapes with N resident adapters, N = 1..128 (Zipf(1.1), seed 1;
+    sort: the same tokens sorted by adapter): 8 layers x {qkv, o_proj} with
+    distinct weights per layer, one graph per N.  Returns the rows and
+    max/min of the latency."""
     import torch
 
     from adapterslotsplusplus_amd import WarpPipeEngine
@@ -260,6 +261,8 @@ def measure_flatness(reps):
     rows = []
     for N in (1, 2, 4, 8, 16, 32, 64, 128):
         idx = wl.zipf_indices(T, N, 1.1, 1).to(dev)
+        if sort:
+            idx = torch.sort(idx).values
         touched = len(set(idx.tolist()))
         layers = [dict(wa_q=rn((N, 1, r, h), .02), wb_q=[rn((N, 1, h, r), .02) for _ in range(3)],
                        wa_o=rn((N, 1, r, h), .02), wb_o=rn((N, 1, h, r), .02), x=rn((T, h), 1.),
@@ -275,7 +278,7 @@ def measure_flatness(reps):
         nbytes = n_layers * (wl.algorithmic_bytes(T, h, 3 * h, [r] * touched) + wl.algorithmic_bytes(T, h, h, [r] * touched))
         rows.append({"resident": N, "touched": touched, "us_per_16_calls": round(us, 2),
                      "us_per_80_call_step": round(us * 5, 1), "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1)})
-        log(f"flatness N={N}: {rows[-1]}")
+        log(f"flatness{' (sorted)' if sort else ''} N={N}: {rows[-1]}")
         del layers
         torch.cuda.empty_cache()
     assert engine.device_errors() == 0
@@ -285,14 +288,16 @@ def measure_flatness(reps):
 
 def run_flatness(args):
     res = measure_flatness(max(5, args.steps))
+    res_s = measure_flatness(max(5, args.steps), sort=True)
     emit({"workload": "cfg2 flatness: resident adapters 1..128, 8 layers x (qkv, o_proj) + build_seg_bounds per graph",
-          **res})
+          **res, "sorted_routing": res_s})
 
 
-def measure_cfg1_gpu(reps):
+def measure_cfg1_gpu(reps, sort=False):
     """BASELINE configs[0] on the GPU: h=4096, r=16, 4 adapters, 64 uniformly
-    routed tokens, fp16, scale 1; us per add_lora call (a graph of 40 calls
-    over distinct copies of the inputs)."""
+    routed tokens (sort: the same tokens sorted by adapter), fp16, scale 1;
+    us per add_lora call (a graph of 40 calls over distinct copies of the
+    inputs)."""
     import torch
 
     from adapterslotsplusplus_amd import WarpPipeEngine
@@ -300,6 +305,8 @@ def measure_cfg1_gpu(reps):
 
     dt = torch.float16
     idx = wl.uniform_indices(64, 4, seed=0)
+    if sort:
+        idx = torch.sort(idx).values
     x = wl.normal((64, 4096), 1.0, dt, 10)
     wa = wl.normal((4, 1, 16, 4096), 0.02, dt, 11)
     wb = wl.normal((4, 1, 4096, 16), 0.02, dt, 12)
@@ -326,6 +333,7 @@ def run_cfg1(args):
     from oracle import segments as so
 
     gpu = measure_cfg1_gpu(max(5, args.steps))
+    gpu_s = measure_cfg1_gpu(max(5, args.steps), sort=True)
     dt = torch.float16
     idx = wl.uniform_indices(64, 4, seed=0)
     x = wl.normal((64, 4096), 1.0, dt, 10)
@@ -348,6 +356,7 @@ def run_cfg1(args):
     cpu_us = times[len(times) // 2] * 1e6
     emit({"workload": "cfg1: T=64, h=4096, r=16, 4 adapters uniform (seed 0), fp16, one add_lora call",
           "bytes_per_call": nbytes, "gpu_us_per_call": gpu["us_per_call"], "gpu_GB_s": gpu["GB_s"],
+          "gpu_sorted_routing": {"us_per_call": gpu_s["us_per_call"], "GB_s": gpu_s["GB_s"]},
           "cpu_baseline": {"us_per_call": round(cpu_us, 1), "GB_s": round(nbytes / (cpu_us * 1e-6) / 1e9, 3),
                            "cores": cores, "kind": "port", "runs": len(times)}})
 
@@ -410,6 +419,17 @@ def run_cfg3(args):
         per[name] = {"us_per_call": round(u / len(sel), 2), "bytes_per_call": b,
                      "GB_s": round(b / (u / len(sel) * 1e-6) / 1e9, 1)}
 
+    # The same calls with the tokens sorted by adapter (every engine's plan
+    # rebuilt outside the graph; the graph reads the plan from HBM).
+    idx_sorted = torch.sort(idx).values.to(dev)
+    for t in targets:
+        assert t["eng"].build_seg_bounds(idx_sorted)
+    torch.cuda.synchronize()
+    us_sorted, _ = graph_us(calls, max(5, args.steps))
+    for t in targets:
+        assert t["eng"].build_seg_bounds(idx.to(dev))
+    torch.cuda.synchronize()
+
     # The same targets through shrink_expand(): both halves in one launch.
     def fused_calls():
         for t in targets:
@@ -445,6 +465,8 @@ def run_cfg3(args):
     emit({"workload": f"cfg3: 13B mixed-rank decode, T=512, 128 adapters ({len(touched)} touched), ranks {{8,16,32,64}}, "
                       f"bf16, {n_layers} layers x (gate, up, down), shrink + expand per target",
           "us_per_layer": round(us / n_layers, 2), "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1), "per_target": per,
+          "sorted_routing": {"us_per_layer": round(us_sorted / n_layers, 2),
+                             "GB_s": round(nbytes / (us_sorted * 1e-6) / 1e9, 1)},
           "shrink_expand_one_launch": {"us_per_layer": round(uf / n_layers, 2),
                                        "GB_s": round(nbytes / (uf * 1e-6) / 1e9, 1)},
           "gate_up_one_launch": {"us_per_layer": round(us_s / n_layers, 2),
@@ -990,8 +1012,11 @@ def main():
         flat = measure_flatness(reps)
         log("secondary: cfg5 draft step")
         c5 = measure_cfg5(reps, max(2, args.warmup))
+        log("secondary: flatness, sorted routing")
+        flat_s = measure_flatness(reps, sort=True)
         log("secondary: cfg1")
         c1 = measure_cfg1_gpu(reps)
+        c1_s = measure_cfg1_gpu(reps, sort=True)
         out["flatness_max_over_min"] = flat["max_over_min_latency"]
         out["cfg5_us_per_step"] = c5["44_launches_nslice"]["us_per_step"]
         out["cfg1_us_per_call"] = c1["us_per_call"]
@@ -999,11 +1024,13 @@ def main():
             "cfg2_sorted_routing": {"us_per_step": round(sorted_us, 2),
                                     "GB_s": round(bytes_step / (sorted_us * 1e-6) / 1e9, 2),
                                     "workload": "the cfg2 step with the same tokens sorted by adapter"},
-            "flatness": {**flat, "workload": "cfg2 shapes, 8 layers x (qkv, o_proj) per graph, N resident adapters"},
+            "flatness": {**flat, "workload": "cfg2 shapes, 8 layers x (qkv, o_proj) per graph, N resident adapters",
+                         "sorted_routing": flat_s},
             "cfg5_draft_step": {**c5, "workload": "h=2048, 22 layers x (q, k, v, o), T=128 (32 tenants x 4), r=32, "
                                                   "bf16, build_seg_bounds + the calls in one graph; cfg5_us_per_step "
                                                   "is the 44-launch form (q/k/v in one call, one A per slice)"},
-            "cfg1": {**c1, "workload": "T=64, h=4096, r=16, 4 adapters uniform (seed 0), fp16, one add_lora call"},
+            "cfg1": {**c1, "workload": "T=64, h=4096, r=16, 4 adapters uniform (seed 0), fp16, one add_lora call",
+                     "sorted_routing": c1_s},
         }
     if not args.no_cpu_baseline:
         log("cpu baseline")

@@ -22,11 +22,15 @@ def add_lora_check(engine, idx, x, y0, wa, wbs, offs, scale, what):
     assert_close(y, bgmv.add_lora(y0, x, wa, wbs, scale, segs, offs), what)
 
 
-def test_cfg1_reference_cpu_case():
-    """h=4096, r=16, 4 adapters, 64 uniformly routed tokens, fp16, scale 1, y0 = 0."""
-    announce("cfg1")
+@pytest.mark.parametrize("order", ["unsorted", "sorted"])
+def test_cfg1_reference_cpu_case(order):
+    """configs[0]: h=4096, r=16, 4 adapters, 64 uniformly routed tokens, fp16, scale 1, y0 = 0;
+    the tokens in routing order and sorted by adapter."""
+    announce(f"cfg1 {order}")
     dt = torch.float16
     idx = wl.uniform_indices(64, 4, seed=0)
+    if order == "sorted":
+        idx = torch.sort(idx).values
     x = wl.normal((64, 4096), 1.0, dt, 10)
     wa = wl.normal((4, 1, 16, 4096), 0.02, dt, 11)
     wb = wl.normal((4, 1, 4096, 16), 0.02, dt, 12)
@@ -58,16 +62,20 @@ def test_cfg2_llama7b_decode_calls(order):
     assert engine.device_errors() == 0
 
 
+@pytest.mark.parametrize("order", ["unsorted", "sorted"])
 @pytest.mark.parametrize("layer", ["gate", "down"])
-def test_cfg3_mixed_rank_13b(layer):
+def test_cfg3_mixed_rank_13b(layer, order):
     """h=5120, I=13824, 128 adapters with ranks uniform in
-    {8,16,32,64} (seed 2), 512 Zipf(1.1)-routed tokens (seed 3), bf16."""
-    announce(f"cfg3 {layer}")
+    {8,16,32,64} (seed 2), 512 Zipf(1.1)-routed tokens (seed 3), bf16; the
+    tokens in routing order and sorted by adapter."""
+    announce(f"cfg3 {layer} {order}")
     dt = torch.bfloat16
     d_in, d_out = (5120, 13824) if layer == "gate" else (13824, 5120)
     g = torch.Generator().manual_seed(2)
     ranks = [int(v) for v in torch.tensor([8, 16, 32, 64])[torch.randint(0, 4, (128,), generator=g)]]
     idx = wl.zipf_indices(512, 128, 1.1, seed=3)
+    if order == "sorted":
+        idx = torch.sort(idx).values
     engine = WarpPipeEngine()
     adapters = {}
     touched = set(idx.tolist())
