@@ -1294,6 +1294,7 @@ hipError_t launch_role(int dtype_bf16, const ApplyArgs& a, hipStream_t stream) {
 constexpr int kLinTokens = 128;
 constexpr int kLinCols = 16;
 constexpr int kLinWavesPerSimd = 3;  // its LDS (43.5 KB) holds three workgroups per compute unit
+constexpr int kLinDeltaBlocks = 8;   // blocks a wave of the epilogue has in flight (half at rank 64)
 
 template <typename T>
 __device__ __forceinline__ void coherent_store_pair(T* p, float x, float y) {
@@ -1318,6 +1319,7 @@ void linear_kernel(const uint32_t* header, const Block* __restrict__ blocks, con
   __shared__ T sx[kLinTokens * kSliceStride];
   __shared__ T sw[2][kLinCols * kSliceStride];
   __shared__ int s_flag;
+  __shared__ int s_hok;  // the epilogue's H flags seen (s_flag still holds the last-arriver test)
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -1330,6 +1332,7 @@ void linear_kernel(const uint32_t* header, const Block* __restrict__ blocks, con
   const int n_blocks = min(n_plan, a.n_slots);
   if (wg == 0 && tid == 0 && n_plan > a.n_slots) flag_error(a.plan.header, kErrCapacity);
   const uint32_t poison = header[kHdrPoison];
+  trace_stamp(a, 0);
 
   if (wg < n_shrink) {
     // --- shrink: the kShrinkOnly role's split (32-row rank groups).
@@ -1344,6 +1347,8 @@ void linear_kernel(const uint32_t* header, const Block* __restrict__ blocks, con
     const int32_t t0 = row < blk.count ? tok0 : -1;
     const Resolved<T> res = resolve_a<T>(a, blk);
     if (res.err != 0 && part == 0 && tid == 0) flag_error(a.plan.header, res.err);
+    trace_tag(a, 1u | (static_cast<uint64_t>(b) << 8));
+    trace_stamp(a, 1);
     shrink_body<T, kShrinkRowsFused / 16>(a, b, c, 0, rg * kShrinkRowsFused, blk, t0, res,
                                           reinterpret_cast<f32x4*>(sx));
     return;
@@ -1353,12 +1358,15 @@ void linear_kernel(const uint32_t* header, const Block* __restrict__ blocks, con
     const int b = wg - n_shrink;
     if (b >= n_blocks) return;
     const Block blk = blocks[b];
+    trace_tag(a, 4u | (static_cast<uint64_t>(b) << 8));
     if (poison == 0u) {
       const Resolved<T> res = resolve_a<T>(a, blk);
       const int wrote = res.ptr != nullptr ? res.rank : 0;
+      trace_stamp(a, 1);
       if (wrote > 0) {
         bool ok = true;
         if (blk.count * wrote * a.n_chunks > 2048) ok = wait_partials<false>(a, blk, wrote, &s_flag);
+        trace_stamp(a, 2);
         if (ok) {
           T* H = static_cast<T*>(a.h);
           const int32_t* toks = bperm + static_cast<int64_t>(b) * kBlockTokens;
@@ -1373,6 +1381,7 @@ void linear_kernel(const uint32_t* header, const Block* __restrict__ blocks, con
     // The H stores have landed (s_waitcnt) before the flag.
     wait_vm();
     __syncthreads();
+    trace_stamp(a, 3);
     if (tid == 0) atomic_store_u(&l.hflag[b], 1u);
     return;
   }
@@ -1383,6 +1392,7 @@ void linear_kernel(const uint32_t* header, const Block* __restrict__ blocks, con
   const int ks = gw % l.splits;
   const int jt = (gw / l.splits) % n_tiles;
   const int g = gw / (l.splits * n_tiles);
+  trace_tag(a, 5u | (static_cast<uint64_t>(g * n_tiles + jt) << 8) | (static_cast<uint64_t>(ks) << 32));
   const int K = a.d_model;
   const int kb = ks * l.k_range;
   const int ke = min(kb + l.k_range, K);
@@ -1438,6 +1448,39 @@ void linear_kernel(const uint32_t* header, const Block* __restrict__ blocks, con
     run_slice(s0, 0, i);
     run_slice(s1, 1, i + 1);
   }
+  trace_stamp(a, 1);
+  // Epilogue state (if this workgroup turns out to be its tile's last): the
+  // blocks of this wave, NB at a time, their token rows and their B rows
+  // jt*16 + row (the delta MFMA's A operand).  A lane's token is -1 past its
+  // block or when the block's adapter is out of range.
+  constexpr int kUnits = kLinTokens * kLinCols / 4 / kThreads;  // f32x4 units per thread (2)
+  constexpr int kSumBatch = 8;                                  // K-split partials per load batch
+  constexpr int NB = RANK <= 32 ? kLinDeltaBlocks : kLinDeltaBlocks / 2;
+  Block blk[NB];
+  int32_t tk[NB];
+  V8 bf[NB][KS];
+  auto load_blocks = [&](int b0) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int b = b0 + i;
+      blk[i] = b < n_blocks ? blocks[b] : Block{-1, 0, 0, -1};
+      tk[i] = b < n_blocks ? bperm[static_cast<int64_t>(b) * kBlockTokens + row] : -1;
+    }
+  };
+  auto load_b = [&]() {
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const Resolved<T> rb = resolve_b<T>(a, blk[i], 0);
+      if (row >= blk[i].count || rb.ptr == nullptr) tk[i] = -1;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const int k = s * 32 + kq;
+        bf[i][s] = rb.ptr != nullptr && k < RANK
+                       ? load8(rb.ptr + static_cast<int64_t>(jt * kLinCols + row) * RANK + k)
+                       : zero8<T>();
+      }
+    }
+  };
   // acc[m]: output columns jt*16 + 4*(lane/16) + [0, 4) of token
   // g*128 + wave*32 + m*16 + lane%16.  Stored coherently; counted below.
   const int rq = (lane >> 4) * 4;
@@ -1449,28 +1492,52 @@ void linear_kernel(const uint32_t* header, const Block* __restrict__ blocks, con
                       acc[m]);
   wait_vm();
   __syncthreads();
+  trace_stamp(a, 2);
   if (tid == 0) s_flag = atomic_add_u(&l.tile_cnt[tile], 1u) == static_cast<unsigned>(l.splits - 1) ? 1 : 0;
   __syncthreads();
+  trace_stamp(a, 3);
   if (s_flag == 0) return;
 
   // --- epilogue of the tile (one workgroup): base output, then the delta.
+  // The first batch of K-split partials goes out with this wave's first
+  // blocks and token rows, then their B rows; the H flags are polled once
+  // the base is summed, and only the H rows load after that.
   float* et = reinterpret_cast<float*>(sx);  // [kLinTokens][kLinCols] fp32
-  constexpr int kUnits = kLinTokens * kLinCols / 4 / kThreads;  // f32x4 units per thread (2)
+  f32x4 sum[kUnits];
+  auto load_sums = [&](int s0, f32x4(&v)[kSumBatch][kUnits]) {
+#pragma unroll
+    for (int q = 0; q < kSumBatch; ++q)
+#pragma unroll
+      for (int i = 0; i < kUnits; ++i)
+        v[q][i] = s0 + q < l.splits ? coherent_load_f4(gp + static_cast<int64_t>(s0 + q) * (kLinTokens * kLinCols) +
+                                                       (tid + i * kThreads) * 4)
+                                    : f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+#pragma unroll
+  for (int i = 0; i < kUnits; ++i) sum[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < l.splits; s0 += kSumBatch) {
+    f32x4 v[kSumBatch][kUnits];
+    load_sums(s0, v);
+    if (s0 == 0) load_blocks(wave * NB);
+#pragma unroll
+    for (int i = 0; i < kUnits; ++i)
+#pragma unroll
+      for (int q = 0; q < kSumBatch; ++q) sum[i] += v[q][i];
+  }
+  load_b();
 #pragma unroll
   for (int i = 0; i < kUnits; ++i) {
     const int u = tid + i * kThreads;
-    f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < l.splits; ++s) sum += coherent_load_f4(gp + static_cast<int64_t>(s) * (kLinTokens * kLinCols) + u * 4);
     const int c4 = (u * 4) % kLinCols;
     if (l.bias != nullptr) {
       const T* bias = static_cast<const T*>(l.bias) + jt * kLinCols + c4;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) sum[q] += static_cast<float>(bias[q]);
+      for (int q = 0; q < 4; ++q) sum[i][q] += static_cast<float>(bias[q]);
     }
     // The base output is rounded to the I/O type, as the base linear's is.
 #pragma unroll
-    for (int q = 0; q < 4; ++q) sum[q] = static_cast<float>(static_cast<T>(sum[q]));
-    *reinterpret_cast<f32x4*>(et + u * 4) = sum;
+    for (int q = 0; q < 4; ++q) sum[i][q] = static_cast<float>(static_cast<T>(sum[i][q]));
+    *reinterpret_cast<f32x4*>(et + u * 4) = sum[i];
   }
   if (tid == 0) atomic_store_u(&l.tile_cnt[tile], 0u);
   // Every block's H flag (one wave polls, bounded; after a give-up, or
@@ -1489,38 +1556,48 @@ void linear_kernel(const uint32_t* header, const Block* __restrict__ blocks, con
       __builtin_amdgcn_s_sleep(2);
     }
     // A give-up elsewhere in the call leaves H unreliable: no delta then.
-    if (lane == 0) s_flag = ok && !poisoned(a.plan.header);
+    if (lane == 0) s_hok = ok && !poisoned(a.plan.header);
   }
+  trace_stamp(a, 4);
   __syncthreads();
-  if (s_flag != 0) {
+  trace_stamp(a, 5);
+  if (s_hok != 0) {
     const T* H = static_cast<const T*>(a.h);
-    for (int b = wave; b < n_blocks; b += kWaves) {
-      const Block blk = blocks[b];
-      const Resolved<T> rb = resolve_b<T>(a, blk, 0);
-      if (rb.ptr == nullptr) continue;
-      // A operand: B rows jt*16 + row; B operand: the block's token rows of H.
-      const int32_t tk = row < blk.count ? bperm[static_cast<int64_t>(b) * kBlockTokens + row] : -1;
-      f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        const int k = s * 32 + kq;
-        const V8 bf = k < RANK ? load8(rb.ptr + static_cast<int64_t>(jt * kLinCols + row) * RANK + k) : zero8<T>();
-        V8 hf = zero8<T>();
-        if (tk >= 0 && k < RANK) {
-          const T* hp = H + static_cast<int64_t>(tk) * a.ldh + k;
-          const u32x2 lo = __builtin_bit_cast(u32x2, coherent_load8(hp));
-          const u32x2 hi = __builtin_bit_cast(u32x2, coherent_load8(hp + 4));
-          hf = __builtin_bit_cast(V8, u32x4{lo[0], lo[1], hi[0], hi[1]});
-        }
-        d = mfma16(bf, hf, d);
+    // NB blocks per wave at a time; each token is in one block, so the
+    // waves add into distinct rows of et.
+    for (int b0 = wave * NB; b0 < n_blocks; b0 += kWaves * NB) {
+      if (b0 != wave * NB) {
+        load_blocks(b0);
+        load_b();
       }
-      // d: columns rq..rq+3 of token tk.  Tokens of other groups and padding
-      // rows are not this tile's.
-      const int tl = tk - g * kLinTokens;
-      if (tk >= 0 && tl >= 0 && tl < kLinTokens) {
-        float* dst = et + tl * kLinCols + rq;
+      V8 hf[NB][KS];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) dst[q] += d[q];
+      for (int i = 0; i < NB; ++i) {
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          const int k = s * 32 + kq;
+          hf[i][s] = zero8<T>();
+          if (tk[i] >= 0 && k < RANK) {
+            const T* hp = H + static_cast<int64_t>(tk[i]) * a.ldh + k;
+            const u32x2 lo = __builtin_bit_cast(u32x2, coherent_load8(hp));
+            const u32x2 hi = __builtin_bit_cast(u32x2, coherent_load8(hp + 4));
+            hf[i][s] = __builtin_bit_cast(V8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) d = mfma16(bf[i][s], hf[i][s], d);
+        // d: columns rq..rq+3 of token tk.  Tokens of other groups and
+        // padding rows are not this tile's.
+        const int tl = tk[i] - g * kLinTokens;
+        if (tk[i] >= 0 && tl >= 0 && tl < kLinTokens) {
+          float* dst = et + tl * kLinCols + rq;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) dst[q] += d[q];
+        }
       }
     }
   }
@@ -1534,6 +1611,7 @@ void linear_kernel(const uint32_t* header, const Block* __restrict__ blocks, con
     const int t = g * kLinTokens + tl;
     if (t < l.tokens) store4(Y + static_cast<int64_t>(t) * a.ldy + jt * kLinCols + c4, *reinterpret_cast<const f32x4*>(et + u * 4));
   }
+  trace_stamp(a, 6);
   // This tile has read every flag and H row it needs.
   const unsigned readers = static_cast<unsigned>(l.groups * n_tiles);
   for (int b = tid; b < n_blocks; b += kThreads) {
@@ -1545,10 +1623,12 @@ void linear_kernel(const uint32_t* header, const Block* __restrict__ blocks, con
 }
 
 template <typename T>
-hipError_t launch_linear_t(const ApplyArgs& a, const LinearArgs& l, int32_t n_shrink, hipStream_t stream) {
-  const int64_t n = static_cast<int64_t>(n_shrink) + a.n_slots +
+hipError_t launch_linear_t(const ApplyArgs& a0, const LinearArgs& l, int32_t n_shrink, hipStream_t stream) {
+  const int64_t n = static_cast<int64_t>(n_shrink) + a0.n_slots +
                     static_cast<int64_t>(l.groups) * (l.n_out / kLinCols) * l.splits;
   const dim3 grid(static_cast<unsigned>(n));
+  ApplyArgs a = a0;
+  if (a.trace != nullptr && n * kTraceWords > a.trace_words) a.trace = nullptr;
   switch (a.rank) {
     case 8: linear_kernel<T, 8><<<grid, kThreads, 0, stream>>>(a.plan.header, a.plan.blocks, a.plan.bperm, n_shrink, a, l); break;
     case 16: linear_kernel<T, 16><<<grid, kThreads, 0, stream>>>(a.plan.header, a.plan.blocks, a.plan.bperm, n_shrink, a, l); break;

@@ -132,6 +132,11 @@ __device__ __forceinline__ void flag_error(uint32_t* header, uint32_t bits) { at
 // (role 3 | block << 8 | d-range << 32): 0 entry, 1 block resolved, 2 slice
 // loop done, 3 partial stored and counted, 4 the last arriver's H stored;
 // word 6: the wave's hardware ids (HW_ID low word, XCC id << 32).
+// linear_kernel: shrink workgroups (role 1) as the fused ones; block reducers
+// (role 4 | block << 8) 0 entry, 1 block resolved, 2 partials there, 3 H
+// stored before the flag; GEMM workgroups (role 5 | tile << 8 | K-split <<
+// 32) 0 entry, 1 K-range done, 2 partial stored, 3 counted, and the tile's
+// last one 4 base summed and H flags seen, 5 barrier, 6 y stored.
 #ifdef WP_TRACE
 __device__ __forceinline__ void trace_stamp(const ApplyArgs& a, int i) {
   if (a.trace != nullptr && threadIdx.x == 0) {

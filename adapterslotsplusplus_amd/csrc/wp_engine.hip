@@ -1394,6 +1394,8 @@ int wp_linear_lora(wp_engine* e, void* y, const void* x, const void* w, int64_t 
   a.part = e->part;
   a.consumed = e->consumed;
   a.spin_limit = e->spin_limit;
+  a.trace = e->trace;
+  a.trace_words = e->trace_words;
   a.plan = plan_view(e);
   a.n_slots = block_bound(e, num_loras);
   a.h = e->hbuf;

@@ -1,7 +1,7 @@
 """Phase breakdown of the fused decode kernels, from a traced build.
 
     python -m adapterslotsplusplus_amd.build --trace
-    python -m adapterslotsplusplus_amd.trace_phases [--call o_proj|qkv|cfg5_o|cfg5_qkv|cfg4_shrink] [--out FILE]
+    python -m adapterslotsplusplus_amd.trace_phases [--call o_proj|qkv|cfg5_o|cfg5_qkv|cfg4_shrink|linear] [--out FILE]
 
 The traced library (-DWP_TRACE) records, per workgroup, the 100 MHz
 real-time counter at the phase boundaries of one fused launch (thread 0,
@@ -42,11 +42,14 @@ def _pct(v, q):
 
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    ap.add_argument("--call", default="o_proj", choices=["o_proj", "qkv", "cfg5_o", "cfg5_qkv", "cfg4_shrink"])
+    ap.add_argument("--call", default="o_proj",
+                    choices=["o_proj", "qkv", "cfg5_o", "cfg5_qkv", "cfg4_shrink", "linear"])
     ap.add_argument("--out", default=None)
     args = ap.parse_args(argv)
     if args.call == "cfg4_shrink":
         return trace_cfg4_shrink(args)
+    if args.call == "linear":
+        return trace_linear(args)
     from . import build as wp_build
 
     if not os.path.exists(wp_build.TRACE_LIB_PATH):
@@ -146,6 +149,109 @@ def main(argv=None):
     row("expand", "MFMA + Y store acknowledged", dur(expand, 4, 5))
     row("expand", "gate open, from the first entry", rel(expand, 3))
     row("expand", "Y stored, from the first entry", rel(expand, 5))
+    text = "\n".join(lines)
+    print(text)
+    if args.out:
+        with open(args.out, "w") as f:
+            f.write(text + "\n")
+
+
+def trace_linear(args):
+    """One linear_lora launch at the draft shape (T=128 = 32 tenants x 4
+    tokens, 2048 x 2048 bf16 with bias, r=32), 40 layers of distinct weights:
+    shrink workgroups (entry, block resolved, first tile, partials stored),
+    block reducers (entry, partials there, H stored before the flag) and GEMM
+    workgroups (entry, K-range done, partial stored, counted; each tile's last
+    one: K-split partials, B rows and H flags loaded and the base summed, then
+    H rows loaded, delta added and y stored)."""
+    _lib = _load_traced()
+    import torch
+
+    from .engine import WarpPipeEngine
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    T, L, r, h, n_layers = 128, 32, 32, 2048, 40
+    dt = torch.bfloat16
+    idx = torch.repeat_interleave(torch.arange(L), 4).to(dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(78)
+
+    def rn(shape, std):
+        return (torch.randn(*shape, generator=gen, device=dev, dtype=torch.float32) * std).to(dt)
+
+    layers = [dict(x=rn((T, h), 1.), w=rn((h, h), .02), b=rn((h,), .1), wa=rn((L, 1, r, h), .02),
+                   wb=rn((L, 1, h, r), .02), y=torch.empty(T, h, dtype=dt, device=dev)) for _ in range(n_layers)]
+    engine = WarpPipeEngine()
+    lib = _lib.load()
+    words = 1 << 20
+    buf = torch.zeros(words, dtype=torch.int64, device=dev)
+    assert engine.build_seg_bounds(idx)
+
+    def call(ly):
+        assert engine.linear_lora(ly["x"], ly["w"], ly["b"], ly["wa"], ly["wb"], 0.5, out=ly["y"]) is not None
+
+    for _ in range(2):
+        for ly in layers:
+            call(ly)
+    torch.cuda.synchronize()
+    for ly in layers[:-1]:
+        call(ly)
+    torch.cuda.synchronize()
+    _lib.check(lib.wp_set_trace(engine._handle, buf.data_ptr(), words), "set_trace")
+    call(layers[-1])
+    torch.cuda.synchronize()
+    _lib.check(lib.wp_set_trace(engine._handle, None, 0), "set_trace")
+    assert engine.device_errors() == 0
+    tr = buf.view(-1, 8).cpu()
+    tags = tr[:, 7]
+    live = tags != 0
+    tr = tr[live]
+    role = (tags[live] & 0xFF).tolist()
+    t0 = int(tr[:, 0].min())
+    ticks_us = 0.01
+    rows = tr.tolist()
+    shrink = [x for x, ro in zip(rows, role) if ro == 1]
+    red = [x for x, ro in zip(rows, role) if ro == 4]
+    gemm = [x for x, ro in zip(rows, role) if ro == 5]
+    last = [x for x in gemm if x[6] > 0]
+
+    def rel(lst, i):
+        return [(x[i] - t0) * ticks_us for x in lst if x[i] > 0]
+
+    def dur(lst, i, j):
+        return [(x[j] - x[i]) * ticks_us for x in lst if x[i] > 0 and x[j] > 0]
+
+    end = max(x[6] for x in last) if last else t0
+    lines = [f"### Phases of one `linear_lora` launch (T={T} = 32 tenants x 4 tokens, {h} x {h} bf16 with bias, "
+             f"r={r}, {n_layers} layers of distinct weights; traced build)", "",
+             f"Workgroups with work: {len(shrink)} shrink, {len(red)} block reducers, {len(gemm)} GEMM "
+             f"({len(last)} tile epilogues); first entry to last stamp {(end - t0) * ticks_us:.2f} us.", "",
+             "| role | phase | median us | p10 | p90 |", "|---|---|---|---|---|"]
+
+    def row(name, phase, v):
+        lines.append(f"| {name} | {phase} | {_pct(v, .5):.2f} | {_pct(v, .1):.2f} | {_pct(v, .9):.2f} |")
+
+    row("shrink", "entry, from the first entry (dispatch)", rel(shrink, 0))
+    row("shrink", "block resolved (entry ->)", dur(shrink, 0, 1))
+    row("shrink", "A and X stream + MFMA (-> first tile done)", dur(shrink, 1, 2))
+    row("shrink", "reduce + partial store acknowledged", dur(shrink, 2, 3))
+    row("shrink", "partials stored, from the first entry", rel(shrink, 3))
+    row("reducer", "entry, from the first entry (dispatch)", rel(red, 0))
+    row("reducer", "block resolved (entry ->)", dur(red, 0, 1))
+    row("reducer", "partials there (-> gate)", dur(red, 1, 2))
+    row("reducer", "H rows stored and acknowledged", dur(red, 2, 3))
+    row("reducer", "H flag set, from the first entry", rel(red, 3))
+    row("GEMM", "entry, from the first entry (dispatch)", rel(gemm, 0))
+    row("GEMM", "K-range loads + MFMA (entry ->)", dur(gemm, 0, 1))
+    row("GEMM", "partial stored and acknowledged", dur(gemm, 1, 2))
+    row("GEMM", "tile counter returned", dur(gemm, 2, 3))
+    row("GEMM", "counted, from the first entry", rel(gemm, 3))
+    row("epilogue", "K-split partials, B rows and H flags (-> base summed, rounded)", dur(last, 3, 4))
+    row("epilogue", "workgroup barrier", dur(last, 4, 5))
+    row("epilogue", "H rows, delta MFMA, y stored", dur(last, 5, 6))
+    row("epilogue", "base summed, from the first entry", rel(last, 4))
+    row("epilogue", "y stored, from the first entry", rel(last, 6))
     text = "\n".join(lines)
     print(text)
     if args.out:
