@@ -983,7 +983,8 @@ int wp_build_seg_bounds(wp_engine* e, const void* idx, int32_t idx_is_int64, int
   DeviceGuard g(e->device);
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   const int bt = plan_block_tokens(T);
-  const Maint m = maint_view(e);
+  Maint m = maint_view(e);
+  m.trace = e->trace_words >= 8 ? e->trace : nullptr;
   WP_HIP(launch_plan(idx, idx_is_int64 ? 1 : 0, static_cast<int>(T), e->header, e->segs, e->blocks, e->perm,
                      e->bperm, e->seg_cap, e->block_cap, bt, &m, stream));
   // Slots whose copy had landed are in the table once this build has run

@@ -80,6 +80,22 @@ __device__ __forceinline__ int upper_index(const int* a, int n, int q) {
   return lo;
 }
 
+// Traced builds (-DWP_TRACE): thread 0 records the 100 MHz real-time counter
+// at the plan build's phase boundaries into m.trace[0..7], after waiting for
+// its memory operations: 0 entry, 1 ids in LDS (maintenance done), 2 run
+// starts, 3 segment table stored, 4 runs sorted, 5 perm stored, 6 block
+// table stored, 7 block token lists and header stored.
+#ifdef WP_TRACE
+__device__ __forceinline__ void plan_stamp(const Maint& m, int i) {
+  if (m.trace != nullptr && threadIdx.x == 0) {
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    m.trace[i] = wall_clock64();
+  }
+}
+#else
+__device__ __forceinline__ void plan_stamp(const Maint&, int) {}
+#endif
+
 // ---------------------------------------------------------- maintenance ----
 
 __device__ __forceinline__ uint64_t agent_load64(const void* p) {
@@ -232,6 +248,7 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
 
   const int tid = threadIdx.x;
   const int e0 = tid * E;
+  plan_stamp(m, 0);
 
   // 1. ids, loaded first so that their latency overlaps the maintenance's
   //    (the routing does not depend on the adapter table).
@@ -252,6 +269,7 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
 #pragma unroll
   for (int k = 0; k < E; ++k) s_id[tid + k * NT] = ids[k];
   lds_barrier();
+  plan_stamp(m, 1);
 
   // 2. Run starts in token order (reference :484): s_a[r] = first token of run r.
   bool is_start[E];
@@ -270,6 +288,7 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
   }
   if (tid == 0) s_a[n_runs] = T;
   lds_barrier();
+  plan_stamp(m, 2);
 
   // 3. Exported table.  Pieces per run: ceil(len/32) when id >= 0 (reference
   //    :485-489); slot bases by exclusive scan in token-start order (:494-503).
@@ -309,6 +328,7 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
     s.pad = 0;
     segments[q] = s;
   }
+  plan_stamp(m, 3);
 
   // 4. Sort the runs with id >= 0 by (adapter id, run index).
   unsigned long long key[E];
@@ -373,6 +393,7 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
     }
   }
 
+  plan_stamp(m, 4);
   // 5. perm: the tokens of the sorted runs, concatenated.
   int len_e[E];
   int start_e[E];
@@ -428,6 +449,7 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
     }
   }
 
+  plan_stamp(m, 5);
   // 6. Groups (one per adapter) and their blocks of bt tokens.
   int n_groups = 0;
   int gb = block_exclusive_scan<NT>(gcount, s_scan, &n_groups);  // ends every read of s_roff / s_rstart
@@ -477,6 +499,7 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
     b.entry = s_a[g];
     blocks[q] = b;
   }
+  plan_stamp(m, 6);
   // Block-padded token lists, from the LDS copy of perm.
   for (int u = tid; u < blk_out * bt; u += NT) {
     const int q = u / bt;
@@ -495,6 +518,7 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
     header[kHdrT] = static_cast<uint32_t>(T);
     header[kHdrBlockTokens] = static_cast<uint32_t>(bt);
   }
+  plan_stamp(m, 7);
 }
 
 }  // namespace

@@ -186,6 +186,7 @@ struct Maint {
   int32_t n_pubs;
   int32_t table_cap;     // entries in `table`
   Entry* table;          // id-indexed adapter table
+  uint64_t* trace;       // traced builds (WP_TRACE) only: 8 phase timestamps of the plan build, or null
 };
 
 struct PlanView {

@@ -1,7 +1,7 @@
 """Phase breakdown of the fused decode kernels, from a traced build.
 
     python -m adapterslotsplusplus_amd.build --trace
-    python -m adapterslotsplusplus_amd.trace_phases [--call o_proj|qkv|cfg5_o|cfg5_qkv|cfg4_shrink|linear] [--out FILE]
+    python -m adapterslotsplusplus_amd.trace_phases [--call o_proj|qkv|cfg5_o|cfg5_qkv|cfg4_shrink|linear|plan] [--out FILE]
 
 The traced library (-DWP_TRACE) records, per workgroup, the 100 MHz
 real-time counter at the phase boundaries of one fused launch (thread 0,
@@ -43,13 +43,15 @@ def _pct(v, q):
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--call", default="o_proj",
-                    choices=["o_proj", "qkv", "cfg5_o", "cfg5_qkv", "cfg4_shrink", "linear"])
+                    choices=["o_proj", "qkv", "cfg5_o", "cfg5_qkv", "cfg4_shrink", "linear", "plan"])
     ap.add_argument("--out", default=None)
     args = ap.parse_args(argv)
     if args.call == "cfg4_shrink":
         return trace_cfg4_shrink(args)
     if args.call == "linear":
         return trace_linear(args)
+    if args.call == "plan":
+        return trace_plan(args)
     from . import build as wp_build
 
     if not os.path.exists(wp_build.TRACE_LIB_PATH):
@@ -252,6 +254,56 @@ def trace_linear(args):
     row("epilogue", "H rows, delta MFMA, y stored", dur(last, 5, 6))
     row("epilogue", "base summed, from the first entry", rel(last, 4))
     row("epilogue", "y stored, from the first entry", rel(last, 6))
+    text = "\n".join(lines)
+    print(text)
+    if args.out:
+        with open(args.out, "w") as f:
+            f.write(text + "\n")
+
+
+def trace_plan(args):
+    """build_seg_bounds (the one-workgroup plan kernel) on the cfg2 routing
+    (T=256, Zipf(1.1) over 64 adapters), the cfg5 routing (T=128, 32 tenants x
+    4) and a T=2048 Zipf routing: the phase boundaries of one build each,
+    median over 20 traced builds."""
+    _lib = _load_traced()
+    import torch
+
+    from . import workloads as wl
+    from .engine import WarpPipeEngine
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    engine = WarpPipeEngine()
+    lib = _lib.load()
+    buf = torch.zeros(8, dtype=torch.int64, device=dev)
+    cases = [("cfg2 routing, T=256", wl.zipf_indices(256, 64, 1.1, 1)),
+             ("cfg5 routing, T=128", torch.repeat_interleave(torch.arange(32), 4)),
+             ("Zipf(1.1) over 64, T=2048", wl.zipf_indices(2048, 64, 1.1, 1))]
+    names = ["ids in LDS, maintenance done", "run starts", "segment table stored", "runs sorted",
+             "perm stored", "block table stored", "block token lists and header stored"]
+    lines = ["### Phases of one `build_seg_bounds` plan build (traced build; median of 20 builds, us)", "",
+             "| phase | " + " | ".join(c[0] for c in cases) + " |", "|---|" + "---|" * len(cases)]
+    cols = []
+    for _, idx in cases:
+        idx = idx.to(dev)
+        for _ in range(3):
+            assert engine.build_seg_bounds(idx)
+        torch.cuda.synchronize()
+        runs = []
+        _lib.check(lib.wp_set_trace(engine._handle, buf.data_ptr(), 8), "set_trace")
+        for _ in range(20):
+            buf.zero_()
+            assert engine.build_seg_bounds(idx)
+            torch.cuda.synchronize()
+            runs.append(buf.cpu().tolist())
+        _lib.check(lib.wp_set_trace(engine._handle, None, 0), "set_trace")
+        cols.append([_pct([(r[i + 1] - r[i]) * 0.01 for r in runs], .5) for i in range(7)] +
+                    [_pct([(r[7] - r[0]) * 0.01 for r in runs], .5)])
+    for i, nm in enumerate(names):
+        lines.append(f"| {nm} | " + " | ".join(f"{c[i]:.2f}" for c in cols) + " |")
+    lines.append("| entry to end | " + " | ".join(f"{c[7]:.2f}" for c in cols) + " |")
+    assert engine.device_errors() == 0
     text = "\n".join(lines)
     print(text)
     if args.out:
