@@ -833,6 +833,7 @@ __device__ __forceinline__ void reduce_to_h(const ApplyArgs& a, int b, const Blo
     o[1] = static_cast<T>(v[1]);
     *reinterpret_cast<typename VecOf<T>::v2*>(H + static_cast<int64_t>(toks[j]) * a.ldh + r0) = o;
   });
+  trace_stamp(a, 4);
   __syncthreads();
   clear_partials(a, blk, wrote, threadIdx.x, kThreads);
 }

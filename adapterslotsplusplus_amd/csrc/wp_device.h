@@ -128,7 +128,8 @@ __device__ __forceinline__ void flag_error(uint32_t* header, uint32_t bits) { at
 // timing a little).  Stamps: 0 entry, 1 plan loaded; shrink workgroups 2 first
 // token tile's MFMAs done, 3 partials stored and acknowledged; expand
 // workgroups 2 B and Y loaded, 3 gate open, 4 partials collected, 5 Y
-// stored.  Word 7: role (1 shrink, 2 expand) | block << 8.  shrink_kernel
+// stored; shrink()'s block reducers (role 2) 4 H stored.  Word 7: role (1
+// shrink, 2 expand or reducer) | block << 8.  shrink_kernel
 // (role 3 | block << 8 | d-range << 32): 0 entry, 1 block resolved, 2 slice
 // loop done, 3 partial stored and counted, 4 the last arriver's H stored;
 // word 6: the wave's hardware ids (HW_ID low word, XCC id << 32).

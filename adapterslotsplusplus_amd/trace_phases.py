@@ -1,7 +1,7 @@
 """Phase breakdown of the fused decode kernels, from a traced build.
 
     python -m adapterslotsplusplus_amd.build --trace
-    python -m adapterslotsplusplus_amd.trace_phases [--call o_proj|qkv|cfg5_o|cfg5_qkv|cfg4_shrink|linear|plan] [--out FILE]
+    python -m adapterslotsplusplus_amd.trace_phases [--call o_proj|qkv|cfg5_o|cfg5_qkv|cfg4_shrink|linear|plan|cfg3_shrink] [--out FILE]
 
 The traced library (-DWP_TRACE) records, per workgroup, the 100 MHz
 real-time counter at the phase boundaries of one fused launch (thread 0,
@@ -43,7 +43,7 @@ def _pct(v, q):
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--call", default="o_proj",
-                    choices=["o_proj", "qkv", "cfg5_o", "cfg5_qkv", "cfg4_shrink", "linear", "plan"])
+                    choices=["o_proj", "qkv", "cfg5_o", "cfg5_qkv", "cfg4_shrink", "linear", "plan", "cfg3_shrink"])
     ap.add_argument("--out", default=None)
     args = ap.parse_args(argv)
     if args.call == "cfg4_shrink":
@@ -52,6 +52,8 @@ def main(argv=None):
         return trace_linear(args)
     if args.call == "plan":
         return trace_plan(args)
+    if args.call == "cfg3_shrink":
+        return trace_cfg3_shrink(args)
     from . import build as wp_build
 
     if not os.path.exists(wp_build.TRACE_LIB_PATH):
@@ -304,6 +306,100 @@ def trace_plan(args):
         lines.append(f"| {nm} | " + " | ".join(f"{c[i]:.2f}" for c in cols) + " |")
     lines.append("| entry to end | " + " | ".join(f"{c[7]:.2f}" for c in cols) + " |")
     assert engine.device_errors() == 0
+    text = "\n".join(lines)
+    print(text)
+    if args.out:
+        with open(args.out, "w") as f:
+            f.write(text + "\n")
+
+
+def trace_cfg3_shrink(args):
+    """shrink() at the cfg3 shapes (T=512 Zipf(1.1) over 128 adapters, ranks
+    uniform in {8,16,32,64}, bf16, registered adapters; gate 5120 -> r and
+    down 13824 -> r), 8 engines of distinct weights per shape: the
+    decode-sized split's shrink workgroups (entry, block resolved, first
+    tile's MFMAs, partials stored) and its block reducers (entry, H stored)."""
+    _lib = _load_traced()
+    import torch
+
+    from . import workloads as wl
+    from .engine import WarpPipeEngine
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    T, dt, n_eng = 512, torch.bfloat16, 8
+    g = torch.Generator().manual_seed(2)
+    ranks = [int(v) for v in torch.tensor([8, 16, 32, 64])[torch.randint(0, 4, (128,), generator=g)]]
+    idx = wl.zipf_indices(T, 128, 1.1, seed=3).to(dev)
+    touched = sorted(set(idx.tolist()))
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(79)
+
+    def rn(shape, std):
+        return (torch.randn(*shape, generator=gen, device=dev, dtype=torch.float32) * std).to(dt)
+
+    lib = _lib.load()
+    words = 1 << 20
+    buf = torch.zeros(words, dtype=torch.int64, device=dev)
+    lines = []
+    for name, d_in in (("gate", 5120), ("down", 13824)):
+        engs = []
+        for _ in range(n_eng):
+            e = WarpPipeEngine()
+            for i in touched:
+                e.register_adapter(i, rn((ranks[i], d_in), .02), rn((64, ranks[i]), .02), 1.0, rank=ranks[i])
+            assert e.build_seg_bounds(idx)
+            engs.append((e, rn((T, d_in), 1.), torch.zeros(T, 64, dtype=dt, device=dev)))
+        for _ in range(2):
+            for e, X, H in engs:
+                e.shrink(X, d_in, 0, T, out=H)
+        torch.cuda.synchronize()
+        for e, X, H in engs[:-1]:
+            e.shrink(X, d_in, 0, T, out=H)
+        e, X, H = engs[-1]
+        buf.zero_()
+        torch.cuda.synchronize()
+        _lib.check(lib.wp_set_trace(e._handle, buf.data_ptr(), words), "set_trace")
+        e.shrink(X, d_in, 0, T, out=H)
+        torch.cuda.synchronize()
+        _lib.check(lib.wp_set_trace(e._handle, None, 0), "set_trace")
+        assert e.device_errors() == 0
+        tr = buf.view(-1, 8).cpu()
+        tags = tr[:, 7]
+        live = tags != 0
+        tr = tr[live]
+        role = (tags[live] & 0xFF).tolist()
+        t0 = int(tr[:, 0].min())
+        rows = tr.tolist()
+        shrink = [x for x, ro in zip(rows, role) if ro == 1]
+        red = [x for x, ro in zip(rows, role) if ro == 2]
+
+        def rel(lst, i):
+            return [(x[i] - t0) * 0.01 for x in lst if x[i] > 0]
+
+        def dur(lst, i, j):
+            return [(x[j] - x[i]) * 0.01 for x in lst if x[i] > 0 and x[j] > 0]
+
+        end = max(max(x[3] for x in shrink), max((x[4] for x in red), default=0))
+        lines += [f"### `shrink()` at the cfg3 {name} shape (T={T}, d={d_in}, {len(touched)} adapters of ranks "
+                  f"8-64, bf16; traced build)", "",
+                  f"Workgroups with work: {len(shrink)} shrink, {len(red)} block reducers; first entry to last stamp "
+                  f"{(end - t0) * 0.01:.2f} us.", "",
+                  "| role | phase | median us | p10 | p90 |", "|---|---|---|---|---|"]
+
+        def row(nm, phase, v):
+            lines.append(f"| {nm} | {phase} | {_pct(v, .5):.2f} | {_pct(v, .1):.2f} | {_pct(v, .9):.2f} |")
+
+        row("shrink", "entry, from the first entry (dispatch)", rel(shrink, 0))
+        row("shrink", "block resolved (entry ->)", dur(shrink, 0, 1))
+        row("shrink", "A and X stream + MFMA (-> first tile done)", dur(shrink, 1, 2))
+        row("shrink", "reduce + partial store acknowledged", dur(shrink, 2, 3))
+        row("shrink", "partials stored, from the first entry", rel(shrink, 3))
+        row("reducer", "entry, from the first entry (dispatch)", rel(red, 0))
+        row("reducer", "partials summed, H stored (block resolved ->)", dur(red, 1, 4))
+        row("reducer", "H stored, from the first entry", rel(red, 4))
+        lines.append("")
+        del engs
     text = "\n".join(lines)
     print(text)
     if args.out:
