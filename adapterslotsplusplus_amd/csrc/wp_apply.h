@@ -30,6 +30,9 @@ struct ApplyArgs {
   int32_t pad_rank;   // 1: the shrink side writes all hs1 rows of a slice, zeros past the adapter's rank
                       // (table mode with one A per slice and mixed ranks: every slice's partial has one width)
   int32_t ptok;       // rows per chunk of `part` (plan positions)
+  int32_t red_first;  // shrink() of decode-sized plans: 1 = the block reducers are dispatched before the
+                      // shrink workgroups they wait for (only when they take at most half of the resident
+                      // workgroups, so that those always find room)
   float* part;        // fp32 partial H by plan position: [n_chunks][ptok][hs], kPartialEmpty between calls
   uint32_t* consumed; // per block (stride kCounterStride): fused calls count expand workgroups done reading,
                       // shrink() counts d-range workgroups done; zero between calls
@@ -161,5 +164,8 @@ int expand_cols_per_workgroup();
 // Waves per SIMD the fused kernel for `rank` (0: mixed) runs at, single- or
 // multi-chunk: with the CU count, how many of its workgroups are resident.
 int fused_waves_per_simd(int rank, int multi);
+// Waves per SIMD of shrink() on decode-sized plans (its resident workgroups
+// per compute unit).
+int shrink_small_waves_per_simd();
 
 }  // namespace wp

@@ -896,13 +896,17 @@ void apply_kernel(const uint32_t* header, const Block* __restrict__ blocks,
   T* s_h = reinterpret_cast<T*>(smem.buf());
   const int S = ROLE == kExpandOnly ? 0 : n_shrink;
   const int wg = static_cast<int>(blockIdx.x);
-  const bool shrink_role = ROLE != kExpandOnly && wg < S;
+  // shrink() with a.red_first: the block reducers are workgroups
+  // 0..n_slots-1, resident from the start, and the shrink workgroups follow.
+  const bool red_first = ROLE == kShrinkOnly && a.red_first != 0;
+  const bool shrink_role = ROLE != kExpandOnly && (red_first ? wg >= a.n_slots : wg < S);
   int b, part;
   if (shrink_role) {
-    b = wg / per_shrink;
-    part = wg - b * per_shrink;
+    const int sw = red_first ? wg - a.n_slots : wg;
+    b = sw / per_shrink;
+    part = sw - b * per_shrink;
   } else {
-    const int e = wg - S;
+    const int e = red_first ? wg : wg - S;
     b = e / per_block;
     part = e - b * per_block;
   }
@@ -1705,6 +1709,8 @@ int traced_build() { return 1; }
 #else
 int traced_build() { return 0; }
 #endif
+int shrink_small_waves_per_simd() { return waves_per_simd<0, kShrinkOnly, 1>(); }
+
 int fused_waves_per_simd(int rank, int multi) {
   const bool wide = rank == 0 || rank == 64;
   if (multi) return wide ? waves_per_simd<64, kFusedMulti, 1>() : waves_per_simd<32, kFusedMulti, 1>();

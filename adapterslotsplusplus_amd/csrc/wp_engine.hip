@@ -1233,6 +1233,10 @@ int wp_shrink(wp_engine* e, const void* X, void* H, int32_t d_model, int32_t ran
     // block (the fused calls' shrink side), not one workgroup per block and
     // d-range streaming every rank row.
     shrink_small_split(d_model, rank, &a);
+    // The reducers first when they take at most half of the resident
+    // workgroups: they then poll while the shrink workgroups stream instead
+    // of being dispatched after them.
+    a.red_first = 2 * static_cast<int64_t>(a.n_slots) <= static_cast<int64_t>(e->n_cu) * shrink_small_waves_per_simd() ? 1 : 0;
     WP_HIP(launch_shrink_small(dtype == WP_DTYPE_BF16, a, stream));
   } else {
     shrink_range_split(d_model, &a);
