@@ -1,4 +1,5 @@
 """Shared helpers of the GPU parity tests."""
+import os
 import sys
 
 import torch
@@ -6,6 +7,13 @@ import torch
 # Tolerance of the north star: bf16/fp16 I/O with fp32 accumulation.
 RTOL = 1e-2
 ATOL = 1e-3
+
+
+def seeds(default: int) -> range:
+    """Seeds of a randomized parity test: `default` of them, or
+    WP_TEST_SEEDS (for a wider sweep, e.g. WP_TEST_SEEDS=200 python -m pytest
+    tests -m gpu -k random)."""
+    return range(int(os.environ.get("WP_TEST_SEEDS", default)))
 
 
 def announce(msg: str) -> None:

@@ -10,7 +10,7 @@ import torch
 from adapterslotsplusplus_amd import WarpPipeEngine
 from oracle import bgmv
 from oracle import segments as so
-from tests.helpers import announce, assert_close, randn
+from tests.helpers import announce, assert_close, randn, seeds
 
 pytestmark = pytest.mark.gpu
 
@@ -547,7 +547,7 @@ def _random_case(seed):
     return T, d, rank, L, widths, offs, col, idx, dtype, scale
 
 
-@pytest.mark.parametrize("seed", range(16))
+@pytest.mark.parametrize("seed", seeds(16))
 def test_add_lora_random_shapes(seed):
     T, d, rank, L, widths, offs, width, idx, dtype, scale = _random_case(seed)
     announce(f"random add_lora seed {seed}: T={T} d={d} r={rank} L={L} slices={widths} offs={offs} {dtype}")
@@ -569,7 +569,7 @@ def test_add_lora_random_shapes(seed):
     assert engine.device_errors() == 0
 
 
-@pytest.mark.parametrize("seed", range(8))
+@pytest.mark.parametrize("seed", seeds(8))
 def test_store_random_shapes(seed):
     """Seeded adapter-store calls: registered adapters of random ranks (mixed,
     rank=0, on device-built plans; one rank on host-built plans), random ids,

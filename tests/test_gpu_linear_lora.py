@@ -10,7 +10,7 @@ import torch
 from adapterslotsplusplus_amd import WarpPipeEngine
 from oracle import bgmv
 from oracle import segments as so
-from tests.helpers import announce, randn
+from tests.helpers import announce, randn, seeds
 
 pytestmark = pytest.mark.gpu
 
@@ -78,7 +78,7 @@ def test_draft_shape(dtype, bias):
     assert engine.device_errors() == 0
 
 
-@pytest.mark.parametrize("case", range(10))
+@pytest.mark.parametrize("case", seeds(10))
 def test_random_shapes_one_engine(case):
     """Seeded shapes across token groups (T up to 512), K-splits, ranks and
     dtypes, ids -1 among them; one engine for all calls of a case (the

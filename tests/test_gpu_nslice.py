@@ -3,6 +3,7 @@ add_lora_packed_nslice: packed q/k/v and gate/up layers), the hook's
 override of it, and the packed draft-model linear -- all against the CPU
 oracle (oracle.bgmv.add_lora_nslice: one independent add_lora per slice) on
 the same seeded inputs."""
+import numpy as np
 import pytest
 import torch
 import torch.nn as nn
@@ -13,7 +14,7 @@ from adapterslotsplusplus_amd import punica_wrapper as pw
 from adapterslotsplusplus_amd.lora_linear import DraftLoRAContext, WarpPipeLoRAPackedLinear
 from oracle import bgmv
 from oracle import segments as so
-from tests.helpers import announce, assert_close, randn
+from tests.helpers import announce, assert_close, randn, seeds
 
 pytestmark = pytest.mark.gpu
 
@@ -53,6 +54,30 @@ def test_nslice_decode_shapes(name, T, L, widths, dtype):
     y = run(engine, idx, x, was, wbs, y0, 0.5, offs)
     segs = so.seg_bounds(idx.tolist()).tolist()
     assert_close(y, bgmv.add_lora_nslice(y0, x, was, wbs, 0.5, segs, offs), name)
+    assert engine.device_errors() == 0
+
+
+@pytest.mark.parametrize("seed", seeds(8))
+def test_nslice_random_shapes(seed):
+    """Seeded one-A-per-slice calls: 2-4 slices of random widths side by side,
+    T across the 512-token switch, runs of random ids (some -1), both
+    dtypes, ranks 8-64."""
+    rng = np.random.default_rng(9000 + seed)
+    T = int(rng.choice([1, 5, 64, 128, 200, 256, 300, 512, 600]))
+    L = int(rng.integers(1, 70))
+    rank = int(rng.choice([8, 16, 32, 64]))
+    d = int(rng.choice([128, 1032, 2048, 4096]))
+    ns = int(rng.integers(2, 5))
+    widths = [int(rng.integers(1, 1100)) * 4 for _ in range(ns)]
+    dtype = torch.bfloat16 if seed % 2 else torch.float16
+    idx = torch.from_numpy(np.repeat(rng.integers(-1, L, size=T), rng.integers(1, 6, size=T))[:T])
+    announce(f"nslice random seed {seed}: T={T} L={L} r={rank} d={d} widths={widths} {dtype}")
+    idx, x, was, wbs, y0 = inputs(T, L, rank, d, widths, dtype, 9100 + seed, idx)
+    offs = [sum(widths[:i]) for i in range(ns)]
+    engine = WarpPipeEngine()
+    y = run(engine, idx, x, was, wbs, y0, 0.5, offs)
+    segs = so.seg_bounds(idx.tolist()).tolist()
+    assert_close(y, bgmv.add_lora_nslice(y0, x, was, wbs, 0.5, segs, offs), f"seed {seed}")
     assert engine.device_errors() == 0
 
 
