@@ -56,9 +56,11 @@ constexpr uint32_t kDefaultSpinLimit = 1u << 17;
 // Blocks hold at most bt (<= kBlockTokens) tokens.  The same launch first
 // does what `m` asks (publications into the adapter table; the partial
 // buffer's repair after a give-up); m may be null.
+// bentries (may be null): each block's adapter-table entry at the table
+// version left in header[kHdrPlanVer] (Weights::a_base in table mode).
 hipError_t launch_plan(const void* idx, int idx_is_int64, int T, uint32_t* header, Segment* segments, Block* blocks,
-                       int32_t* perm, int32_t* bperm, int seg_cap, int block_cap, int bt, const Maint* m,
-                       hipStream_t stream);
+                       int32_t* perm, int32_t* bperm, Entry* bentries, int seg_cap, int block_cap, int bt,
+                       const Maint* m, hipStream_t stream);
 // The plan build's maintenance alone (one workgroup), for eager calls that
 // run between plan builds.
 hipError_t launch_maintain(uint32_t* header, const Maint& m, hipStream_t stream);
@@ -80,6 +82,9 @@ struct EntryWrites {
   int32_t n_retire;
   uint32_t* retire[kMaxEntryWrites];
   uint32_t retire_gen[kMaxEntryWrites];
+  // Plan header whose table version (kHdrTableVer) is raised once the
+  // writes are done, or null.
+  uint32_t* header;
 };
 hipError_t launch_entry_writes(const EntryWrites& w, hipStream_t stream);
 

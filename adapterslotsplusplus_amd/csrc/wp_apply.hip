@@ -510,11 +510,12 @@ struct OutChunk {
 // kSliceH: a slice may have its own H (one A per slice, or expand() of such
 // a call's H); otherwise every slice reads H from column 0.  TS: as resolve_b.
 template <typename T, bool kSliceH, bool TS = false>
-__device__ __forceinline__ OutChunk<T> out_chunk(const ApplyArgs& a, const Block& blk, int oc) {
+__device__ __forceinline__ OutChunk<T> out_chunk(const ApplyArgs& a, const Block& blk, int oc,
+                                                 PreEntry pre = PreEntry{}) {
   int s = 0;
   while (s + 1 < a.w.n_slices && oc >= a.w.oc_start[s + 1]) ++s;
   OutChunk<T> c;
-  c.res = resolve_b<T, TS>(a, blk, s);
+  c.res = resolve_b<T, TS>(a, blk, s, pre);
   c.o_first = (oc - a.w.oc_start[s]) * kOC;
   c.o_size = a.w.o_size[s];
   c.y_off = a.w.y_off[s];
@@ -634,7 +635,7 @@ __device__ __forceinline__ void compute_chunk(const ApplyArgs& a, int b, const B
 // kernel within its registers.
 template <typename T, int RANK, int ROLE, int TILES, bool PA, bool MIX = false>
 __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, const Block& blk, int32_t tok0,
-                                            T* s_h, T* s_stage, int* s_flag) {
+                                            T* s_h, T* s_stage, int* s_flag, PreEntry pre = PreEntry{}) {
   using V8 = typename VecOf<T>::v8;
   constexpr int KS = (RANK + 31) / 32;
   constexpr bool kFusedRole = ROLE == kFused || ROLE == kFusedMulti;
@@ -645,11 +646,11 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
   constexpr bool kSliceH = PA || ROLE == kExpandOnly;
   const int n_owg = (a.n_ochunks + a.n_sub - 1) / a.n_sub;
   T* stage = s_stage + (threadIdx.x >> 6) * 16 * kStageStride;
-  OutChunk<T> cur = out_chunk<T, kSliceH, PA>(a, blk, p);
+  OutChunk<T> cur = out_chunk<T, kSliceH, PA>(a, blk, p, pre);
   if (cur.res.err != 0 && cur.o_first == 0 && threadIdx.x == 0) flag_error(a.plan.header, cur.res.err);
   // Rank rows the block's shrink side writes (0: it could not resolve the
   // adapter and writes nothing).
-  int wrote = kFusedRole ? resolve_a<T, PA>(a, blk).rank : 0;
+  int wrote = kFusedRole ? resolve_a<T, PA>(a, blk, 0, pre).rank : 0;
   // One A per slice: the slices whose shrink side writes (the same
   // resolution as theirs), the columns each writes (W: the rank, or all hs1
   // of a zero-padded slice) and each one's alpha.
@@ -763,7 +764,7 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
         const int oc = p + (j + 1) * n_owg;
         cn[j].res.ptr = nullptr;
         if (j + 1 < a.n_sub && oc < a.n_ochunks) {
-          cn[j] = out_chunk<T, kSliceH, PA>(a, blk, oc);
+          cn[j] = out_chunk<T, kSliceH, PA>(a, blk, oc, pre);
           if (cn[j].res.err != 0 && cn[j].o_first == 0 && threadIdx.x == 0) flag_error(a.plan.header, cn[j].res.err);
           if (cn[j].res.ptr != nullptr) load_chunk<T, RANK, kDyn>(a, cn[j], tok0, bfn[j], yqn[j]);
         }
@@ -775,7 +776,7 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
       for (int i = 3; i < a.n_sub; ++i) {
         const int oc = p + i * n_owg;
         if (oc >= a.n_ochunks) break;
-        cur = out_chunk<T, kSliceH, PA>(a, blk, oc);
+        cur = out_chunk<T, kSliceH, PA>(a, blk, oc, pre);
         if (cur.res.err != 0 && cur.o_first == 0 && threadIdx.x == 0) flag_error(a.plan.header, cur.res.err);
         load_chunk<T, RANK, kDyn>(a, cur, tok0, bf, yq);
         if (cur.res.ptr != nullptr) compute_chunk<T, RANK, true, 1>(a, b, blk, tok0, cur, bf, yq, s_h, hsl, stage);
@@ -787,7 +788,7 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
         const int oc = p + i * n_owg;
         if (oc >= a.n_ochunks) break;
         if (i > 0) {
-          cur = out_chunk<T, kSliceH, PA>(a, blk, oc);
+          cur = out_chunk<T, kSliceH, PA>(a, blk, oc, pre);
           if (cur.res.err != 0 && cur.o_first == 0 && threadIdx.x == 0) flag_error(a.plan.header, cur.res.err);
           load_chunk<T, RANK, kDyn>(a, cur, tok0, bf, yq);
         }
@@ -819,8 +820,9 @@ __device__ __forceinline__ void expand_body(const ApplyArgs& a, int b, int p, co
 // sums its partials into H[token] = rn(alpha * sum_c part[c]) and, once
 // every thread has read its words, restores kPartialEmpty over them.
 template <typename T>
-__device__ __forceinline__ void reduce_to_h(const ApplyArgs& a, int b, const Block& blk, int* s_flag) {
-  const Resolved<T> res = resolve_a<T>(a, blk);
+__device__ __forceinline__ void reduce_to_h(const ApplyArgs& a, int b, const Block& blk, int* s_flag,
+                                            PreEntry pre = PreEntry{}) {
+  const Resolved<T> res = resolve_a<T>(a, blk, 0, pre);
   // Rank rows the shrink side wrote (none if it could not resolve the adapter).
   const int wrote = res.ptr != nullptr ? res.rank : 0;
   if (wrote <= 0) return;
@@ -921,6 +923,21 @@ void apply_kernel(const uint32_t* header, const Block* __restrict__ blocks,
   const Block blk = blocks[b];
   const int row = threadIdx.x & 15;
   const int32_t tok0 = bperm[static_cast<int64_t>(b) * kBlockTokens + row];
+  // Table mode on a device plan: the block's entry as the plan build copied
+  // it, loaded with the descriptor, used while no table write has followed
+  // that build (one memory latency less before the first weight load).
+  // Only in shrink()'s and expand()'s roles and the mixed-rank fused kernels
+  // (table mode only): in the fixed-rank fused kernels, which stacked-weight
+  // decode calls use, the test alone cost 0.3 us per qkv call and the
+  // entry's registers a wave per SIMD at ranks 8-32 (cfg2 step 1217 -> 1227
+  // us, cfg5's 88 calls 697 -> 736 us, measured on MI355X).
+  PreEntry pre;
+  if constexpr (ROLE == kShrinkOnly || ROLE == kExpandOnly || RANK == 0) {
+    if (a.w.mode == kTable && a.w.a_base[0] != nullptr) {
+      pre.en = load_entry(static_cast<const Entry*>(a.w.a_base[0]) + b);
+      pre.ok = header[kHdrTableVer] == header[kHdrPlanVer];
+    }
+  }
   // A plan with more blocks than the grid's slots (only routings that name
   // ids the call cannot resolve produce one) is reported, not silently cut.
   if (b == a.n_slots - 1 && part == 0 && threadIdx.x == 0 && n_blocks > a.n_slots)
@@ -937,7 +954,7 @@ void apply_kernel(const uint32_t* header, const Block* __restrict__ blocks,
     const int k = part - sa * per_a;
     const int rg = k / a.n_chunks;
     const int c = k - rg * a.n_chunks;
-    const Resolved<T> res = resolve_a<T, PA>(a, blk, sa);
+    const Resolved<T> res = resolve_a<T, PA>(a, blk, sa, pre);
     // Each slice's first workgroup reports its resolution error.
     if (res.err != 0 && k == 0 && threadIdx.x == 0) flag_error(a.plan.header, res.err);
     if constexpr (ROLE == kFusedMulti || ROLE == kShrinkOnly) {
@@ -948,25 +965,25 @@ void apply_kernel(const uint32_t* header, const Block* __restrict__ blocks,
     return;
   }
   if constexpr (ROLE == kShrinkOnly) {
-    reduce_to_h<T>(a, b, blk, &s_flag);
+    reduce_to_h<T>(a, b, blk, &s_flag, pre);
   } else if constexpr (RANK != 0) {
-    expand_body<T, RANK, ROLE, TILES, PA>(a, b, part, blk, t0, s_h, smem.stage(), &s_flag);
+    expand_body<T, RANK, ROLE, TILES, PA>(a, b, part, blk, t0, s_h, smem.stage(), &s_flag, pre);
   } else if constexpr (PA) {
     // Mixed ranks with one A per slice (zero-padded slices): every block at
     // the largest rank, B read at each adapter's own row stride.
-    expand_body<T, kMaxRank, ROLE, TILES, PA>(a, b, part, blk, t0, s_h, smem.stage(), &s_flag);
+    expand_body<T, kMaxRank, ROLE, TILES, PA>(a, b, part, blk, t0, s_h, smem.stage(), &s_flag, pre);
   } else if constexpr (ROLE == kFusedMulti) {
     // Mixed ranks over several chunks per workgroup: one body at the largest
     // rank (four per-rank bodies here spill).
-    expand_body<T, kMaxRank, ROLE, TILES, false, true>(a, b, part, blk, t0, s_h, smem.stage(), &s_flag);
+    expand_body<T, kMaxRank, ROLE, TILES, false, true>(a, b, part, blk, t0, s_h, smem.stage(), &s_flag, pre);
   } else {
     // Mixed ranks: the block's adapter decides (resolved again inside).
-    const Resolved<T> r0 = resolve_b<T>(a, blk, 0);
+    const Resolved<T> r0 = resolve_b<T>(a, blk, 0, pre);
     switch (r0.rank) {
-      case 16: expand_body<T, 16, ROLE, TILES, PA>(a, b, part, blk, t0, s_h, smem.stage(), &s_flag); break;
-      case 32: expand_body<T, 32, ROLE, TILES, PA>(a, b, part, blk, t0, s_h, smem.stage(), &s_flag); break;
-      case 64: expand_body<T, 64, ROLE, TILES, PA>(a, b, part, blk, t0, s_h, smem.stage(), &s_flag); break;
-      default: expand_body<T, 8, ROLE, TILES, PA>(a, b, part, blk, t0, s_h, smem.stage(), &s_flag); break;
+      case 16: expand_body<T, 16, ROLE, TILES, PA>(a, b, part, blk, t0, s_h, smem.stage(), &s_flag, pre); break;
+      case 32: expand_body<T, 32, ROLE, TILES, PA>(a, b, part, blk, t0, s_h, smem.stage(), &s_flag, pre); break;
+      case 64: expand_body<T, 64, ROLE, TILES, PA>(a, b, part, blk, t0, s_h, smem.stage(), &s_flag, pre); break;
+      default: expand_body<T, 8, ROLE, TILES, PA>(a, b, part, blk, t0, s_h, smem.stage(), &s_flag, pre); break;
     }
   }
 }

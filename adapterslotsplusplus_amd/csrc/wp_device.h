@@ -207,11 +207,20 @@ struct Resolved {
   uint32_t err = 0;
 };
 
+// A block's adapter-table entry loaded ahead (Weights::a_base in table mode) and
+// whether it may be used; passed by value so that it stays in registers.
+struct PreEntry {
+  Entry en;
+  bool ok = false;
+};
+
 // A of A-slice sa (0 when every output slice shares one A).  TS: table mode
 // with one adapter per slice (each slice's entries at its own offset; other
-// table calls fold their one offset into a.w.entries).
+// table calls fold their one offset into a.w.entries).  pre: the block's
+// entry already loaded (Weights::a_base in table mode, checked by the caller).
 template <typename T, bool TS = false>
-__device__ __forceinline__ Resolved<T> resolve_a(const ApplyArgs& a, const Block& blk, int sa = 0) {
+__device__ __forceinline__ Resolved<T> resolve_a(const ApplyArgs& a, const Block& blk, int sa = 0,
+                                                 PreEntry pre = PreEntry{}) {
   Resolved<T> r;
   if (a.w.mode == kStacked) {
     if (blk.adapter_id < 0 || blk.adapter_id >= a.w.num_ids) {
@@ -227,7 +236,7 @@ __device__ __forceinline__ Resolved<T> resolve_a(const ApplyArgs& a, const Block
     r.err = kErrUnregistered;
     return r;
   }
-  const Entry en = load_entry(a.w.entries + (TS ? a.w.entry_off[sa] : 0) + blk.entry);
+  const Entry en = !TS && pre.ok ? pre.en : load_entry(a.w.entries + (TS ? a.w.entry_off[sa] : 0) + blk.entry);
   const int32_t rank = entry_rank(en.rank_dtype);
   // One test over both halves, so that both loads go out before the wait.
   if ((en.a_ptr == 0) | (en.b_ptr == 0) | (rank <= 0)) {
@@ -245,7 +254,8 @@ __device__ __forceinline__ Resolved<T> resolve_a(const ApplyArgs& a, const Block
 }
 
 template <typename T, bool TS = false>
-__device__ __forceinline__ Resolved<T> resolve_b(const ApplyArgs& a, const Block& blk, int slice) {
+__device__ __forceinline__ Resolved<T> resolve_b(const ApplyArgs& a, const Block& blk, int slice,
+                                                 PreEntry pre = PreEntry{}) {
   Resolved<T> r;
   if (a.w.mode == kStacked) {
     if (blk.adapter_id < 0 || blk.adapter_id >= a.w.num_ids) {
@@ -261,7 +271,8 @@ __device__ __forceinline__ Resolved<T> resolve_b(const ApplyArgs& a, const Block
     r.err = kErrUnregistered;
     return r;
   }
-  const Entry en = load_entry(a.w.entries + (TS ? a.w.entry_off[slice] : 0) + blk.entry);
+  const Entry en =
+      !TS && pre.ok ? pre.en : load_entry(a.w.entries + (TS ? a.w.entry_off[slice] : 0) + blk.entry);
   const int32_t rank = entry_rank(en.rank_dtype);
   // One test over both halves, so that both loads go out before the wait.
   if ((en.a_ptr == 0) | (en.b_ptr == 0) | (rank <= 0)) {

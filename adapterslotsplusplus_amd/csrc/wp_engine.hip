@@ -225,6 +225,8 @@ struct wp_engine {
   uint32_t* lin_cnt = nullptr;  // [kLinCounters] column-tile counters of linear_lora (zero between calls)
   uint32_t* lin_flag = nullptr; // [2][block_cap] H flags and their reader counts (zero between calls)
   Entry* dtable = nullptr;      // [table_cap] id-indexed adapter table of build_seg_bounds plans
+  Entry* bentries = nullptr;    // [block_cap] a build_seg_bounds plan's copy of each block's table entry
+  bool plan_bentries = false;   // the last build_seg_bounds plan wrote bentries
   int table_cap = 0;
   int seg_cap = 0, block_cap = 0, tok_cap = 0, entry_cap = 0;
   int ptok = 0;                 // plan positions of `part`: fused calls run on plans of <= kSmallPlanTokens
@@ -319,6 +321,7 @@ Maint maint_view(const wp_engine* e) {
 int table_write(wp_engine* e, int32_t id, const Entry& en, hipStream_t stream) {
   if (id < 0 || id >= e->table_cap) return WP_OK;
   EntryWrites w{};
+  w.header = e->header;
   w.n = 1;
   w.dst[0] = e->dtable + id;
   w.val[0] = en;
@@ -377,6 +380,7 @@ int release_slots_on(wp_engine* e, const int* slot_ids, int n, hipStream_t strea
   int done = 0;
   while (done < n) {
     EntryWrites w{};
+    w.header = e->header;
     std::vector<int> batch;
     for (; done < n && w.n + 2 <= kMaxEntryWrites; ++done) {
       const int s = slot_ids[done];
@@ -629,6 +633,7 @@ int wp_create(const wp_config* cfg_in, wp_engine** out) {
   const size_t o_ret = carve(sizeof(uint32_t) * std::max(cfg.num_staging_slots, 1));
   const size_t o_lin = carve(sizeof(uint32_t) * (kLinCounters + 2 * static_cast<size_t>(e->block_cap)));
   const size_t o_tab = carve(sizeof(Entry) * std::max(e->table_cap, 1));
+  const size_t o_bent = carve(sizeof(Entry) * e->block_cap);
   const size_t o_spart = carve(sizeof(float) * kMaxChunks * static_cast<size_t>(e->tok_cap) * kMaxRank);
   const size_t hbuf_bytes = sizeof(uint16_t) * static_cast<size_t>(e->tok_cap) * kMaxSlices * kMaxRank;
   const size_t o_hbuf = carve(hbuf_bytes);
@@ -647,6 +652,7 @@ int wp_create(const wp_config* cfg_in, wp_engine** out) {
   e->lin_cnt = reinterpret_cast<uint32_t*>(e->ws + o_lin);
   e->lin_flag = e->lin_cnt + kLinCounters;
   e->dtable = reinterpret_cast<Entry*>(e->ws + o_tab);
+  e->bentries = reinterpret_cast<Entry*>(e->ws + o_bent);
   e->spart = reinterpret_cast<float*>(e->ws + o_spart);
   e->hbuf = e->ws + o_hbuf;
   e->part = reinterpret_cast<float*>(e->ws + o_part);
@@ -985,8 +991,12 @@ int wp_build_seg_bounds(wp_engine* e, const void* idx, int32_t idx_is_int64, int
   const int bt = plan_block_tokens(T);
   Maint m = maint_view(e);
   m.trace = e->trace_words >= 8 ? e->trace : nullptr;
+  // Engines with registered adapters (table-mode calls) get each block's
+  // table entry copied by the plan build; stacked-weight engines skip it.
+  Entry* bent = e->adapters.empty() ? nullptr : e->bentries;
   WP_HIP(launch_plan(idx, idx_is_int64 ? 1 : 0, static_cast<int>(T), e->header, e->segs, e->blocks, e->perm,
-                     e->bperm, e->seg_cap, e->block_cap, bt, &m, stream));
+                     e->bperm, bent, e->seg_cap, e->block_cap, bt, &m, stream));
+  e->plan_bentries = bent != nullptr;
   // Slots whose copy had landed are in the table once this build has run
   // (event queries are not allowed while a graph is being captured).
   if (!stream_capturing(stream))
@@ -1087,6 +1097,8 @@ int table_weights(wp_engine* e, hipStream_t stream, Weights* w) {
   w->entries = e->dtable + std::min(e->entry_offset, e->table_cap);
   w->num_ids = std::max(0, e->table_cap - e->entry_offset);
   if (e->entry_count > 0) w->num_ids = std::min(w->num_ids, e->entry_count);
+  // The plan's copies are of entries at offset 0 (a block's entry is its id).
+  w->a_base[0] = e->plan_bentries && e->entry_offset == 0 ? e->bentries : nullptr;
   return WP_OK;
 }
 
@@ -1692,7 +1704,8 @@ int wp_add_lora_static(void* y, const void* x, const void* idx, int32_t idx_is_i
   m.consumed_words = (kSOffPart - kSOffCons) / 4;
   WP_HIP(launch_plan(idx, idx_is_int64 ? 1 : 0, static_cast<int>(T), v.header, reinterpret_cast<Segment*>(base + kSOffSeg),
                      reinterpret_cast<Block*>(base + kSOffBlk), reinterpret_cast<int32_t*>(base + kSOffPerm),
-                     reinterpret_cast<int32_t*>(base + kSOffBperm), kStaticSegCap, kStaticBlockCap, bt, &m, stream));
+                     reinterpret_cast<int32_t*>(base + kSOffBperm), nullptr, kStaticSegCap, kStaticBlockCap, bt, &m,
+                     stream));
   a.tiles = 1;
   a.ptok = kStaticTokens;
   a.part = reinterpret_cast<float*>(base + kSOffPart);

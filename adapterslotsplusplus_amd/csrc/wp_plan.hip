@@ -134,6 +134,7 @@ __device__ void maintain(uint32_t* header, const Maint& m, int* s_flag) {
         uint64_t* dst = reinterpret_cast<uint64_t*>(m.table + id);
 #pragma unroll
         for (int i = 0; i < 4; ++i) dst[i] = w[i];
+        __hip_atomic_fetch_add(&header[kHdrTableVer], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
   }
@@ -180,6 +181,8 @@ __global__ __launch_bounds__(64) void entry_writes_kernel(EntryWrites w) {
   for (int i = 0; i < w.n_retire; ++i)
     __hip_atomic_fetch_max(w.retire[i], w.retire_gen[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   for (int i = 0; i < w.n; ++i) *w.dst[i] = w.val[i];
+  if (w.header != nullptr && w.n > 0)
+    __hip_atomic_fetch_add(&w.header[kHdrTableVer], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Workgroup (job, part) copies its share of the job's A and B in 16-byte
@@ -235,8 +238,8 @@ template <int NT, int E>
 __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, int idx_is_int64, int T,
                                                   uint32_t* __restrict__ header, Segment* __restrict__ segments,
                                                   Block* __restrict__ blocks, int32_t* __restrict__ perm,
-                                                  int32_t* __restrict__ bperm, int seg_cap, int block_cap, int bt,
-                                                  Maint m) {
+                                                  int32_t* __restrict__ bperm, Entry* __restrict__ bentries,
+                                                  int seg_cap, int block_cap, int bt, Maint m) {
   constexpr int CAP = NT * E;
   // s_big: the ids (int64) first, then the sort keys, then per-run offsets.
   __shared__ unsigned long long s_big[CAP];
@@ -264,6 +267,10 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
 
   // 0. Publications into the adapter table; the partial buffer's repair.
   maintain(header, m, s_scan);
+  // The table version the block entry copies below are taken at (every
+  // install above has raised it before maintain's closing barrier).
+  const uint32_t table_ver =
+      tid == 0 && bentries != nullptr ? __hip_atomic_load(&header[kHdrTableVer], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
 
   // ids -> LDS.
 #pragma unroll
@@ -498,6 +505,18 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
     b.count = n - j * bt < bt ? n - j * bt : bt;
     b.entry = s_a[g];
     blocks[q] = b;
+    if (bentries != nullptr) {
+      // The block's adapter-table entry (agent-scope loads: the maintenance
+      // above may have installed it from another wave), or an empty one.
+      uint64_t w[4] = {0, 0, 0, 0};
+      if (m.table != nullptr && b.entry >= 0 && b.entry < m.table_cap) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = agent_load64(reinterpret_cast<const uint64_t*>(m.table + b.entry) + i);
+      }
+      uint64_t* dst = reinterpret_cast<uint64_t*>(bentries + q);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dst[i] = w[i];
+    }
   }
   plan_stamp(m, 6);
   // Block-padded token lists, from the LDS copy of perm.
@@ -517,6 +536,7 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
     header[kHdrNumValid] = static_cast<uint32_t>(n_tok);
     header[kHdrT] = static_cast<uint32_t>(T);
     header[kHdrBlockTokens] = static_cast<uint32_t>(bt);
+    if (bentries != nullptr) header[kHdrPlanVer] = table_ver;
   }
   plan_stamp(m, 7);
 }
@@ -525,8 +545,8 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
 
 // Host launcher: the smallest capacity variant that holds T.
 hipError_t launch_plan(const void* idx, int idx_is_int64, int T, uint32_t* header, Segment* segments, Block* blocks,
-                       int32_t* perm, int32_t* bperm, int seg_cap, int block_cap, int bt, const Maint* m,
-                       hipStream_t stream) {
+                       int32_t* perm, int32_t* bperm, Entry* bentries, int seg_cap, int block_cap, int bt,
+                       const Maint* m, hipStream_t stream) {
   if (T < 0 || bt < 1 || bt > kBlockTokens) return hipErrorInvalidValue;
   Maint mm{};
   if (m != nullptr) mm = *m;
@@ -534,13 +554,13 @@ hipError_t launch_plan(const void* idx, int idx_is_int64, int T, uint32_t* heade
   if (mm.n_pubs < 0 || mm.n_pubs > 256) return hipErrorInvalidValue;
   if (T <= 256) {
     plan_kernel<256, 1><<<1, 256, 0, stream>>>(idx, idx_is_int64, T, header, segments, blocks, perm, bperm,
-                                               seg_cap, block_cap, bt, mm);
+                                               bentries, seg_cap, block_cap, bt, mm);
   } else if (T <= 2048) {
     plan_kernel<1024, 2><<<1, 1024, 0, stream>>>(idx, idx_is_int64, T, header, segments, blocks, perm, bperm,
-                                                 seg_cap, block_cap, bt, mm);
+                                                 bentries, seg_cap, block_cap, bt, mm);
   } else if (T <= kPlanMaxTokens) {
     plan_kernel<1024, 8><<<1, 1024, 0, stream>>>(idx, idx_is_int64, T, header, segments, blocks, perm, bperm,
-                                                 seg_cap, block_cap, bt, mm);
+                                                 bentries, seg_cap, block_cap, bt, mm);
   } else {
     return hipErrorInvalidValue;
   }

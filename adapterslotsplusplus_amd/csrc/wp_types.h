@@ -82,6 +82,12 @@ enum HeaderWord : int {
   // the next plan build (or wp_read_device_errors) refills the buffer with
   // kPartialEmpty, clears the counters and resets the word.
   kHdrPoison = 7,
+  // Raised by every write into the id-indexed adapter table (the entry-write
+  // kernel, a plan build's installed publications).
+  kHdrTableVer = 8,
+  // The table version a plan build copied its blocks' entries at (see
+  // Weights::a_base); the copies hold while the two words are equal.
+  kHdrPlanVer = 9,
   kHdrWords = 16
 };
 
@@ -158,6 +164,13 @@ struct Weights {
   // its own A, stacked mode only: one H per slice, side by side in a row).
   int32_t n_a;
   float scale;       // stacked: the call's scale
+  // Stacked: each A slice's wa_t_all.  Table mode on a device-built plan at
+  // entry offset 0: a_base[0] holds the plan build's copy of each block's
+  // entries[block.entry] (Entry[block slots]), loaded with the block
+  // descriptor instead of after it (one memory latency less before the first
+  // weight load) and used while header[kHdrTableVer] == header[kHdrPlanVer];
+  // null otherwise.  (A field of its own grows the kernel arguments, which
+  // measured ~0.2 us more per launch.)
   const void* a_base[kMaxSlices];
   int64_t a_stride[kMaxSlices];  // elements
   const Entry* entries;

@@ -341,6 +341,63 @@ def test_mixed_rank_store():
     assert engine.device_errors() == 0
 
 
+def test_plan_entry_copies_follow_table_writes():
+    """A build_seg_bounds plan copies each block's adapter-table entry for the
+    mixed-rank store kernels; a table write after the build (an adapter
+    evicted and registered again with other weights, another evicted) must
+    make the calls read the table itself until the next build.  shrink +
+    expand and shrink_expand against the oracle at every stage."""
+    announce("plan entry copies vs table writes")
+    dtype = torch.bfloat16
+    T, d, o = 200, 1024, 1536
+    ranks = [8, 16, 32, 64, 32, 16]
+    engine = WarpPipeEngine()
+    adapters = {}
+
+    def register(i, seed):
+        r = ranks[i]
+        A = randn((r, d), seed, dtype, 0.02)
+        B = randn((o, r), seed + 1, dtype, 0.02)
+        engine.register_adapter(i, A.cuda(), B.cuda(), 8.0 / r, rank=r)
+        adapters[i] = (A, B, 8.0 / r)
+
+    for i in range(len(ranks)):
+        register(i, 500 + 10 * i)
+    idx = np.random.default_rng(11).integers(-1, len(ranks), size=T)
+    X = randn((T, d), 600, dtype)
+    Y0 = randn((T, o), 601, dtype)
+    segs = so.seg_bounds(idx).tolist()
+
+    def check(stage, errors_expected=False):
+        H = engine.shrink(X.cuda(), d, 0, T)
+        Y = Y0.cuda()
+        engine.expand(H, Y, o, 0)
+        Y1 = Y0.cuda()
+        engine.shrink_expand(X.cuda(), Y1, o, 0)
+        torch.cuda.synchronize()
+        live = [sg for sg in segs if int(sg[0]) in adapters]  # an evicted id's tokens are left alone
+        H_ref = bgmv.shrink(X, live, adapters, 64, T)
+        Y_ref = bgmv.expand(H_ref, Y0, live, adapters)
+        assert_close(H, H_ref, f"{stage}: H")
+        assert_close(Y, Y_ref, f"{stage}: Y")
+        assert_close(Y1, Y_ref, f"{stage}: Y, shrink_expand")
+        assert (engine.device_errors() != 0) == errors_expected, stage
+
+    assert engine.build_seg_bounds(torch.from_numpy(idx).cuda())
+    check("as built")
+    # New weights under id 3, after the build.
+    engine.evict_adapter(3)
+    register(3, 700)
+    check("id 3 replaced after the build")
+    # Id 1 gone: its tokens are skipped (and flagged), the others applied.
+    engine.evict_adapter(1)
+    del adapters[1]
+    check("id 1 evicted after the build", errors_expected=True)
+    # The next build copies the current table.
+    assert engine.build_seg_bounds(torch.from_numpy(idx).cuda())
+    check("rebuilt", errors_expected=True)
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_packed_slices_and_offsets(dtype):
     """One shared H expanded into q/k/v slices of a wider y, and a single
