@@ -146,12 +146,12 @@ inline void shrink_split(int d, int rank, int rows, int n_a, int hs, int64_t slo
 
 // Split of a decode-sized shrink() launch: 32-row rank groups x d-ranges of
 // about 512 columns (each wave's share one batch of loads), or 1024 columns
-// past ten ranges (fewer workgroups than residency rounds; measured on
-// MI355X at d = 5120 and 13824), at most kMaxChunks; one reducer workgroup
-// per block.
+// past eight ranges (fewer workgroups than residency rounds; measured on
+// MI355X at d = 13824, and at d = 5120: cfg3 gate/up 42.8 -> 42.2 us per
+// call), at most kMaxChunks; one reducer workgroup per block.
 inline void shrink_small_split(int d, int rank, ApplyArgs* a) {
   int64_t n = std::max<int64_t>(ceil_div(d, 512), 1);
-  if (n > 10) n = std::min<int64_t>(ceil_div(d, 1024), kMaxChunks);
+  if (n > 8) n = std::min<int64_t>(ceil_div(d, 1024), kMaxChunks);
   a->dc = static_cast<int>(ceil_div(ceil_div(d, n), 128) * 128);
   a->n_chunks = static_cast<int>(ceil_div(d, a->dc));
   a->srows = kShrinkRowsFused;
