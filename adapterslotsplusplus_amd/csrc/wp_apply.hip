@@ -890,6 +890,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(waves_
 void apply_kernel(const uint32_t* header, const Block* __restrict__ blocks,
                   const int32_t* __restrict__ bperm, int32_t per_shrink, int32_t n_shrink, int32_t per_block,
                   ApplyArgs a) {
+  // Arguments: three pointers and three ints (40 bytes with the padding),
+  // then ApplyArgs.  Not in the mixed-rank kernels: there it measured slower
+  // (cfg3 122.6 -> 127.8 us per layer).
+  if constexpr (RANK != 0) touch_kernel_args<40 + static_cast<int>(sizeof(ApplyArgs))>();
   using SM = SharedMem<T, RANK, ROLE == kFused ? 1 : (ROLE == kExpandOnly ? 0 : kShrinkRowsFused / 16)>;
   __shared__ SM smem;
   __shared__ int s_flag;

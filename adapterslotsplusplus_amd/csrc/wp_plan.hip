@@ -240,6 +240,8 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
                                                   Block* __restrict__ blocks, int32_t* __restrict__ perm,
                                                   int32_t* __restrict__ bperm, Entry* __restrict__ bentries,
                                                   int seg_cap, int block_cap, int bt, Maint m) {
+  // Arguments before m: 80 bytes (eight pointers, two ints, three ints, padding).
+  touch_kernel_args<80 + static_cast<int>(sizeof(Maint))>();
   constexpr int CAP = NT * E;
   // s_big: the ids (int64) first, then the sort keys, then per-run offsets.
   __shared__ unsigned long long s_big[CAP];
