@@ -22,6 +22,17 @@ __device__ __forceinline__ void touch_kernel_args() {
   for (int i = 0; i < BYTES / 4; i += 16) t ^= ka[i];
   asm volatile("" ::"s"(t));
 }
+// The same in two steps: the loads where touch_kernel_args_issue is called,
+// the wait where its result is passed to touch_kernel_args_wait.
+template <int BYTES>
+__device__ __forceinline__ uint32_t touch_kernel_args_issue() {
+  const uint32_t* ka = (const uint32_t*)__builtin_amdgcn_kernarg_segment_ptr();
+  uint32_t t = 0;
+#pragma unroll
+  for (int i = 0; i < BYTES / 4; i += 16) t ^= ka[i];
+  return t;
+}
+__device__ __forceinline__ void touch_kernel_args_wait(uint32_t t) { asm volatile("" ::"s"(t)); }
 
 // Kernel arguments of one shrink or expand launch (passed by value).
 struct ApplyArgs {
