@@ -895,11 +895,12 @@ void apply_kernel(const uint32_t* header, const Block* __restrict__ blocks,
   // waited for with the plan loads below (cfg2 step 1177 -> 1166 us, cfg3
   // 122.3 -> 120.6 us per layer, against waiting here, which made the
   // mixed-rank ones slower); the fixed-rank one-A-per-slice kernels wait here
-  // (cfg5's 44-launch step 430 vs 437 us).
+  // (cfg5's 44-launch step 430 vs 437 us); the mixed-rank ones wait with the
+  // plan loads (cfg3's gate and up in one launch 123.9 -> 122.6 us per layer).
   constexpr int kArgBytes = 40 + static_cast<int>(sizeof(ApplyArgs));
   uint32_t ka_touch = 0;
   if constexpr (RANK != 0 && PA) touch_kernel_args<kArgBytes>();
-  if constexpr (!PA) ka_touch = touch_kernel_args_issue<kArgBytes>();
+  if constexpr (!PA || RANK == 0) ka_touch = touch_kernel_args_issue<kArgBytes>();
   using SM = SharedMem<T, RANK, ROLE == kFused ? 1 : (ROLE == kExpandOnly ? 0 : kShrinkRowsFused / 16)>;
   __shared__ SM smem;
   __shared__ int s_flag;
@@ -952,7 +953,7 @@ void apply_kernel(const uint32_t* header, const Block* __restrict__ blocks,
   // ids the call cannot resolve produce one) is reported, not silently cut.
   if (b == a.n_slots - 1 && part == 0 && threadIdx.x == 0 && n_blocks > a.n_slots)
     flag_error(a.plan.header, kErrCapacity);
-  if constexpr (!PA) touch_kernel_args_wait(ka_touch);
+  if constexpr (!PA || RANK == 0) touch_kernel_args_wait(ka_touch);
   if ((b >= n_blocks) | (blk.count <= 0) | (tok0 < -1) | (poison != 0u)) return;
   const int32_t t0 = row < blk.count ? tok0 : -1;
   trace_stamp(a, 1);
