@@ -842,6 +842,18 @@ __device__ __forceinline__ void reduce_to_h(const ApplyArgs& a, int b, const Blo
 
 // ---------------------------------------------------------------- kernels ----
 
+// apply_kernel's explicit arguments, as laid out in its kernel-argument
+// segment: touch_kernel_args reads below this size only.
+struct ApplyKernelArgs {
+  const uint32_t* header;
+  const Block* blocks;
+  const int32_t* bperm;
+  int32_t per_shrink, n_shrink, per_block;
+  ApplyArgs a;
+};
+static_assert(offsetof(ApplyKernelArgs, a) == 40 && sizeof(ApplyKernelArgs) == 40 + sizeof(ApplyArgs),
+              "apply_kernel's argument size as passed to touch_kernel_args");
+
 // Occupancy target (waves per SIMD), from the registers each variant needs
 // without spilling: the fused kernel holds B and Y across the partials'
 // collection, the multi-slice one also two 16-row shrink tiles; expand()
@@ -890,14 +902,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(waves_
 void apply_kernel(const uint32_t* header, const Block* __restrict__ blocks,
                   const int32_t* __restrict__ bperm, int32_t per_shrink, int32_t n_shrink, int32_t per_block,
                   ApplyArgs a) {
-  // Arguments: three pointers and three ints (40 bytes with the padding),
-  // then ApplyArgs.  Their lines are loaded here and, in the shared-A kernels,
+  // Arguments: ApplyKernelArgs.  Their lines are loaded here and, in the shared-A kernels,
   // waited for with the plan loads below (cfg2 step 1177 -> 1166 us, cfg3
   // 122.3 -> 120.6 us per layer, against waiting here, which made the
   // mixed-rank ones slower); the fixed-rank one-A-per-slice kernels wait here
   // (cfg5's 44-launch step 430 vs 437 us); the mixed-rank ones wait with the
   // plan loads (cfg3's gate and up in one launch 123.9 -> 122.6 us per layer).
-  constexpr int kArgBytes = 40 + static_cast<int>(sizeof(ApplyArgs));
+  constexpr int kArgBytes = static_cast<int>(sizeof(ApplyKernelArgs));
   uint32_t ka_touch = 0;
   if constexpr (RANK != 0 && PA) touch_kernel_args<kArgBytes>();
   if constexpr (!PA || RANK == 0) ka_touch = touch_kernel_args_issue<kArgBytes>();

@@ -234,14 +234,30 @@ __global__ __launch_bounds__(256) void stage_copy_kernel(StageJobs jobs) {
 constexpr int kRankMax = 1024;
 constexpr int kRankWork = 4096;
 
+// plan_kernel's explicit arguments, as laid out in its kernel-argument
+// segment: touch_kernel_args reads below this size only.
+struct PlanKernelArgs {
+  const void* idx;
+  int idx_is_int64, T;
+  uint32_t* header;
+  Segment* segments;
+  Block* blocks;
+  int32_t* perm;
+  int32_t* bperm;
+  Entry* bentries;
+  int seg_cap, block_cap, bt;
+  Maint m;
+};
+static_assert(offsetof(PlanKernelArgs, m) == 80 && sizeof(PlanKernelArgs) == 80 + sizeof(Maint),
+              "plan_kernel's argument size as passed to touch_kernel_args");
+
 template <int NT, int E>
 __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, int idx_is_int64, int T,
                                                   uint32_t* __restrict__ header, Segment* __restrict__ segments,
                                                   Block* __restrict__ blocks, int32_t* __restrict__ perm,
                                                   int32_t* __restrict__ bperm, Entry* __restrict__ bentries,
                                                   int seg_cap, int block_cap, int bt, Maint m) {
-  // Arguments before m: 80 bytes (eight pointers, two ints, three ints, padding).
-  touch_kernel_args<80 + static_cast<int>(sizeof(Maint))>();
+  touch_kernel_args<static_cast<int>(sizeof(PlanKernelArgs))>();
   constexpr int CAP = NT * E;
   // s_big: the ids (int64) first, then the sort keys, then per-run offsets.
   __shared__ unsigned long long s_big[CAP];
