@@ -10,7 +10,7 @@ import torch
 from adapterslotsplusplus_amd import WarpPipeEngine
 from oracle import bgmv
 from oracle import segments as so
-from tests.helpers import announce, assert_close, randn, seeds
+from tests.helpers import announce, assert_close, h_tie_flips, randn, seeds
 
 pytestmark = pytest.mark.gpu
 
@@ -622,7 +622,16 @@ def test_add_lora_random_shapes(seed):
         assert engine.add_lora_slices(y, x.cuda(), wa.cuda(), [w.cuda() for w in wbs], scale, offs)
     torch.cuda.synchronize()
     segs = so.seg_bounds(idx).tolist()
-    assert_close(y, bgmv.add_lora(y0, x, wa, wbs, scale, segs, offs), f"seed {seed}")
+    # H is rounded to the I/O type before the expand; where an element's exact
+    # value ties with a rounding midpoint within fp32 summation error, either
+    # neighbour is a correct H, and the output may move by that step times |B|.
+    slack = torch.zeros(y0.shape, dtype=torch.float32)
+    for lid in np.unique(idx[(idx >= 0) & (idx < L)]):
+        rows = torch.from_numpy(np.nonzero(idx == lid)[0])
+        flips = h_tie_flips(x[rows], wa[lid, 0], scale, dtype)
+        for wb, off in zip(wbs, offs):
+            slack[rows, off:off + wb.shape[2]] += (flips @ wb[lid, 0].double().abs().T).float()
+    assert_close(y, bgmv.add_lora(y0, x, wa, wbs, scale, segs, offs), f"seed {seed}", slack=slack)
     assert engine.device_errors() == 0
 
 
@@ -673,9 +682,17 @@ def test_store_random_shapes(seed):
     torch.cuda.synchronize()
     H_ref = bgmv.shrink(X, segs, adapters, rank if rank else 64, T)
     Y_ref = bgmv.expand(H_ref, Y0, segs, adapters)
+    # Rounding ties of H (see test_add_lora_random_shapes): per segment, the
+    # steps its H elements may take either way, times |B|.
+    slack = torch.zeros(Y0.shape, dtype=torch.float32)
+    for aid, start, count in ((g[0], g[1], g[2]) for g in segs):
+        if aid in adapters:
+            A, B, alpha = adapters[aid]
+            flips = h_tie_flips(X[start:start + count], A, alpha, dtype)
+            slack[start:start + count] += (flips @ B.double().abs().T).float()
     assert_close(H, H_ref, f"seed {seed} H")
-    assert_close(Y, Y_ref, f"seed {seed} Y")
-    assert_close(Y1, Y_ref, f"seed {seed} Y, shrink_expand")
+    assert_close(Y, Y_ref, f"seed {seed} Y", slack=slack)
+    assert_close(Y1, Y_ref, f"seed {seed} Y, shrink_expand", slack=slack)
     assert engine.device_errors() == 0
 
 
