@@ -42,6 +42,8 @@ EXPORTED = (
     "wp_release_prefetch", "wp_add_lora_static", "wp_wait_prefetch", "wp_set_spin_limit",
     "wp_add_lora_nslice", "wp_prefetch_adapters", "wp_release_prefetches", "wp_wait_prefetches", "wp_set_trace",
     "wp_shrink_expand_slices", "wp_linear_lora", "wp_read_probe",
+    "wp_set_max_adapters", "wp_read_static_errors", "wp_poll_device_errors", "wp_lora_shrink", "wp_lora_expand",
+    "wp_add_bias", "wp_handoff_probe", "wp_barrier_probe",
 )
 
 
@@ -109,6 +111,15 @@ def load():
         "wp_read_probe": ([p, p, i64, p, p], ctypes.c_int),
         "wp_add_lora_static": ([p, p, p, i32, i64, p, i64, i32, i32, p, p, p, p, f32, i32, i32, i64, i32, p],
                                ctypes.c_int),
+        "wp_set_max_adapters": ([p, i64], ctypes.c_int),
+        "wp_read_static_errors": ([i32, p, p], ctypes.c_int),
+        "wp_poll_device_errors": ([p, P(ctypes.c_uint32), p], ctypes.c_int),
+        "wp_lora_shrink": ([p, p, i64, i64, p, i32, p, p, i32, f32, i32, i32, i64, i32, p], ctypes.c_int),
+        "wp_lora_expand": ([p, p, i64, p, i32, i64, i64, i32, p, p, p, p, p, p, i32, i32, i64, i32, i32, p],
+                           ctypes.c_int),
+        "wp_add_bias": ([p, p, i64, i32, p, p, p, p, i32, i64, i32, p], ctypes.c_int),
+        "wp_handoff_probe": ([p, i64, p, i64, p, i64, p, p, i32, i32, i32, p], ctypes.c_int),
+        "wp_barrier_probe": ([p, i32, i32, i32, p, p], ctypes.c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)

@@ -18,7 +18,7 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ_DIR = os.path.join(CSRC, "_build")
 LIB_NAME = "libwarppipe_mi355x.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
-SOURCES = ["wp_plan.hip", "wp_apply.hip", "wp_engine.hip"]
+SOURCES = ["wp_plan.hip", "wp_apply.hip", "wp_aux.hip", "wp_engine.hip"]
 ARCH = os.environ.get("WP_OFFLOAD_ARCH", "gfx950")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -68,6 +68,12 @@ struct ApplyArgs {
   int64_t trace_words; // capacity of `trace` (a launch whose grid does not fit is not traced)
   PlanView plan;
   Weights w;
+  // shrink() only: 1 = H is fp32 and the call adds alpha * sum to it,
+  // unrounded (vLLM's lora_shrink buffer); 0 = H = rn(alpha * sum) in the
+  // I/O type.  At the end of the arguments: fields placed before the hot
+  // kernels' argument reads measured up to 0.3 us more per launch.
+  int32_t h_f32;
+  int32_t pad_end;
 };
 
 // Words per workgroup of a traced build's timestamp buffer: stamps 0..6 and
@@ -190,6 +196,65 @@ hipError_t launch_linear(int dtype_bf16, const ApplyArgs& a, const LinearArgs& l
 // workgroup that does nothing.  A measurement of the device's read rate and
 // launch cost, not part of any call.
 hipError_t launch_read_probe(const void* p, size_t bytes, void* sink, int workgroups, hipStream_t stream);
+
+// *out = *word and *word = 0, as one device-scope atomic exchange (one
+// thread, in stream order).
+hipError_t launch_take_word(uint32_t* word, uint32_t* out, hipStream_t stream);
+
+// The per-token work of vLLM V1's LoRA op surface around the grouped kernels
+// (wp_aux.hip prep_kernel), one workgroup per block slot of the plan:
+//   * h_src != null: the rank columns of slice s of token t's H,
+//     h_src[s * h_slice_stride + t * h_row_stride + k] (fp32 if h_f32, else
+//     the I/O type), rounded into h_dst[t * ldh_dst + s * rank + k];
+//   * zero_y: y[t, y_off[s] .. + o_size[s]) = 0 for every slice;
+//   * otherwise, for each slice with bias[s]: y = rn(y + bias[s][id]) over
+//     the window (bias rows bias_stride[s] elements apart; ids >= num_ids
+//     flagged kErrIdRange).
+struct PrepArgs {
+  PlanView plan;
+  int32_t n_slots;
+  int32_t n_slices;
+  int32_t num_ids;
+  int32_t rank;
+  const void* h_src;
+  int64_t h_slice_stride;
+  int64_t h_row_stride;
+  void* h_dst;
+  int32_t ldh_dst;
+  int32_t h_f32;
+  void* y;
+  int64_t ldy;
+  int32_t zero_y;
+  int32_t pad;
+  int32_t o_size[kMaxSlices];
+  int32_t y_off[kMaxSlices];
+  const void* bias[kMaxSlices];
+  int64_t bias_stride[kMaxSlices];
+};
+hipError_t launch_prep(int dtype_bf16, const PrepArgs& p, hipStream_t stream);
+
+// Barrier probe: `workgroups` workgroups of `threads` (256 or 1024) run
+// `rounds` rounds of LDS writes, lds_barrier(), and reads of every slot;
+// slots that did not hold the round's value are added to *mismatches.
+hipError_t launch_barrier_probe(const uint32_t* salts, int rounds, int threads, int workgroups, uint32_t* mismatches,
+                                hipStream_t stream);
+
+// Handoff probe (a measurement, not part of any call): see wp_aux.hip.
+struct HandoffProbe {
+  const void* a;     // streamed before the count (a call's A and X bytes)
+  uint64_t a16;      // 16-byte words
+  const void* b;     // streamed around the wait (B, and Y read)
+  uint64_t b16;
+  void* y;           // written last (Y)
+  uint64_t y16;
+  uint32_t* counters;  // 2 x kCounterStride words per group, zero between launches
+  uint32_t* err;       // bit 0: a wait gave up
+  int32_t group;       // workgroups that wait for each other
+  int32_t mode;        // 0 no wait, 1 first b batch before the wait, 2 all of b after it
+  uint32_t spin_limit;
+  int32_t pad;
+};
+hipError_t launch_handoff_probe(const HandoffProbe& p, int workgroups, hipStream_t stream);
 
 // Output columns one expand workgroup produces.
 int expand_cols_per_workgroup();

@@ -829,11 +829,19 @@ __device__ __forceinline__ void reduce_to_h(const ApplyArgs& a, int b, const Blo
   if (blk.count * wrote * a.n_chunks > 2048) wait_partials<false>(a, blk, wrote, s_flag);
   T* H = static_cast<T*>(a.h);
   const int32_t* toks = a.plan.bperm + static_cast<int64_t>(b) * kBlockTokens;
+  const bool f32 = a.h_f32 != 0;
   collect_partials<8>(a, blk, wrote / 2, res.alpha, [&](int j, int r0, f32x2 v) {
+    const int64_t at = static_cast<int64_t>(toks[j]) * a.ldh + r0;
+    if (f32) {
+      // fp32 H (vLLM's lora_shrink buffer): added to, not rounded.
+      f32x2* hp = reinterpret_cast<f32x2*>(static_cast<float*>(a.h) + at);
+      *hp = *hp + v;
+      return;
+    }
     typename VecOf<T>::v2 o;
     o[0] = static_cast<T>(v[0]);
     o[1] = static_cast<T>(v[1]);
-    *reinterpret_cast<typename VecOf<T>::v2*>(H + static_cast<int64_t>(toks[j]) * a.ldh + r0) = o;
+    *reinterpret_cast<typename VecOf<T>::v2*>(H + at) = o;
   });
   trace_stamp(a, 4);
   __syncthreads();
@@ -1167,11 +1175,21 @@ void shrink_kernel(ApplyArgs a) {
   // acc[m]: ranks m*16 + 4*(lane/16) + [0, 4) of token slot tl.
   const int rq = (lane >> 4) * 4;
   T* H = static_cast<T*>(a.h);
+  // fp32 H (vLLM's lora_shrink buffer): alpha * sum added to it, unrounded.
+  const bool f32 = a.h_f32 != 0;
+  auto put_h = [&](int64_t at, f32x4 v) {
+    if (f32) {
+      f32x4* hp = reinterpret_cast<f32x4*>(static_cast<float*>(a.h) + at);
+      *hp = *hp + v;
+    } else {
+      store4(H + at, v);
+    }
+  };
   if (n_kc == 1) {
     if (tok >= 0) {
 #pragma unroll
       for (int m = 0; m < MT; ++m)
-        if (m * 16 + rq < rank) store4(H + static_cast<int64_t>(tok) * a.ldh + m * 16 + rq, acc[m] * res.alpha);
+        if (m * 16 + rq < rank) put_h(static_cast<int64_t>(tok) * a.ldh + m * 16 + rq, acc[m] * res.alpha);
     }
     return;
   }
@@ -1227,7 +1245,7 @@ void shrink_kernel(ApplyArgs a) {
     if (u < units) {
       const int j = u / r4;
       const int32_t tj = a.plan.bperm[static_cast<int64_t>(b) * kBlockTokens + j];
-      store4(H + static_cast<int64_t>(tj) * a.ldh + (u - j * r4) * 4, sum[i] * res.alpha);
+      put_h(static_cast<int64_t>(tj) * a.ldh + (u - j * r4) * 4, sum[i] * res.alpha);
     }
   }
   if (tid == 0) atomic_store_u(counter, 0u);

@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include "wp_apply.h"
+#include "wp_sync.h"
 
 namespace wp {
 namespace {
@@ -114,10 +115,6 @@ __device__ __forceinline__ void atomic_store_u(uint32_t* p, unsigned v) {
 // Waits until this wave's outstanding global loads, stores and atomics are
 // acknowledged, which for sc1 stores means they are device-visible.
 __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-// Workgroup barrier for LDS data only: waits for this wave's LDS accesses
-// but not for its global loads in flight, which __syncthreads (a
-// workgroup-scope fence + s_barrier) would drain with s_waitcnt vmcnt(0).
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 __device__ __forceinline__ void flag_error(uint32_t* header, uint32_t bits) { atomicOr(&header[kHdrErrors], bits); }
 

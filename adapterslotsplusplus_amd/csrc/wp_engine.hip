@@ -234,6 +234,14 @@ struct wp_engine {
   int n_cu = 256;  // compute units of the device
   int32_t entry_offset = 0;  // table-mode calls on device-built plans read dtable + entry_offset
   int32_t entry_count = 0;   // ... and at most this many entries (0: to the table's end)
+  int64_t max_adapters = 0;  // declared most registered adapters (wp_set_max_adapters), 0: none declared
+  // wp_poll_device_errors: the error word is moved (and cleared) by a kernel
+  // into a pinned, device-mapped host word; `err_ready` is recorded behind
+  // it, and the host reads the word once the event has completed.
+  uint32_t* err_host = nullptr;   // host address
+  uint32_t* err_hdev = nullptr;   // its device address
+  hipEvent_t err_ready = nullptr;
+  bool err_pending = false;
   uint32_t spin_limit = kDefaultSpinLimit;
   uint64_t* trace = nullptr;  // traced builds: per-workgroup timestamps of fused launches
   int64_t trace_words = 0;
@@ -531,13 +539,35 @@ int block_bound(const wp_engine* e, int64_t groups) {
   return static_cast<int>(std::min<int64_t>(T, T / e->plan_bt + g));
 }
 
-// Distinct ids an adapter-store call on a device-built plan can resolve: the
-// registered adapters, and no more than the ids of the selected layer window
-// (wp_set_entry_offset's count), so a multi-layer store is not bounded by
-// every layer's adapters.
-int64_t resolvable_ids(const wp_engine* e) {
-  const int64_t n = static_cast<int64_t>(e->adapters.size());
-  return e->entry_count > 0 ? std::min<int64_t>(n, e->entry_count) : n;
+// Distinct ids an adapter-store call on a device-built plan can resolve,
+// given `registered` adapters and a table window of `window` ids (the
+// selected layer's: a multi-layer store is not bounded by every layer's
+// adapters).  An eager call counts the adapters registered now: a routing
+// that names only registered ids stays within it.  A call being captured
+// into a graph is replayed after later registrations, so it counts every id
+// of the window (its grid then holds up to T block slots, most of them empty
+// at decode sizes), unless the caller declared the most adapters it will
+// register (wp_set_max_adapters), which registration then enforces.
+int64_t call_ids(const wp_engine* e, hipStream_t stream, int64_t registered, int64_t window) {
+  if (e->max_adapters > 0) return std::min<int64_t>(window, e->max_adapters);
+  if (stream_capturing(stream)) return window;
+  return std::min<int64_t>(window, registered);
+}
+
+int64_t resolvable_ids(const wp_engine* e, hipStream_t stream) {
+  const int64_t window =
+      e->entry_count > 0 ? e->entry_count : std::max<int64_t>(0, static_cast<int64_t>(e->table_cap) - e->entry_offset);
+  return call_ids(e, stream, static_cast<int64_t>(e->adapters.size()), window);
+}
+
+// Registration past the declared maximum (wp_set_max_adapters) is refused:
+// grids sized by it would drop the extra adapters' blocks.
+int check_max_adapters(const wp_engine* e, int32_t adapter_id) {
+  if (e->max_adapters > 0 && e->adapters.count(adapter_id) == 0 &&
+      static_cast<int64_t>(e->adapters.size()) >= e->max_adapters)
+    return fail(WP_ERR_CAPACITY, "register_adapter: %lld adapters are registered, the declared maximum "
+                                 "(set_max_adapters)", (long long)e->max_adapters);
+  return WP_OK;
 }
 
 
@@ -694,6 +724,17 @@ int wp_create(const wp_config* cfg_in, wp_engine** out) {
     if (hipEventCreateWithFlags(&s.ready, hipEventDisableTiming) != hipSuccess)
       return bail(fail(WP_ERR_HIP, "wp_create: slot event creation failed"));
   }
+  void* eh = nullptr;
+  void* ed = nullptr;
+  if (hipHostMalloc(&eh, 256, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess ||
+      hipHostGetDevicePointer(&ed, eh, 0) != hipSuccess ||
+      hipEventCreateWithFlags(&e->err_ready, hipEventDisableTiming) != hipSuccess) {
+    if (eh) (void)hipHostFree(eh);
+    return bail(fail(WP_ERR_HIP, "wp_create: error word setup failed"));
+  }
+  e->err_host = static_cast<uint32_t*>(eh);
+  e->err_hdev = static_cast<uint32_t*>(ed);
+  *e->err_host = 0;
   *out = e;
   return WP_OK;
 }
@@ -723,6 +764,8 @@ int wp_destroy(wp_engine* e) {
     if (e->pinned[i]) (void)hipHostFree(e->pinned[i]);
     if (e->upload_done[i]) (void)hipEventDestroy(e->upload_done[i]);
   }
+  if (e->err_host) (void)hipHostFree(e->err_host);
+  if (e->err_ready) (void)hipEventDestroy(e->err_ready);
   if (e->pstream) (void)hipStreamDestroy(e->pstream);
   if (e->pool) (void)hipMemPoolDestroy(e->pool);
   delete e;
@@ -745,8 +788,9 @@ int wp_register_adapter(wp_engine* e, int32_t adapter_id, const void* A, const v
   DeviceGuard g(e->device);
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   if (stream_capturing(stream)) return fail(WP_ERR_STATE, "register_adapter cannot run during graph capture");
-  int rc = evict_impl(e, adapter_id, stream);
+  int rc = check_max_adapters(e, adapter_id);
   if (rc != WP_OK) return rc;
+  if ((rc = evict_impl(e, adapter_id, stream)) != WP_OK) return rc;
   Adapter ad;
   ad.rank = rank;
   ad.d = d_model;
@@ -800,8 +844,9 @@ int wp_register_adapter_ref(wp_engine* e, int32_t adapter_id, const void* A, con
   }
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   if (stream_capturing(stream)) return fail(WP_ERR_STATE, "register_adapter cannot run during graph capture");
-  int rc = evict_impl(e, adapter_id, stream);
+  int rc = check_max_adapters(e, adapter_id);
   if (rc != WP_OK) return rc;
+  if ((rc = evict_impl(e, adapter_id, stream)) != WP_OK) return rc;
   Adapter ad;
   ad.rank = rank;
   ad.d = d_model;
@@ -826,6 +871,15 @@ int wp_evict_adapter(wp_engine* e, int32_t adapter_id, void* stream) {
 }
 
 int wp_has_adapter(wp_engine* e, int32_t adapter_id) { return (e && e->adapters.count(adapter_id)) ? 1 : 0; }
+
+int wp_set_max_adapters(wp_engine* e, int64_t n) {
+  if (!e) return fail(WP_ERR_INVALID, "set_max_adapters: engine is NULL");
+  if (n < 0) return fail(WP_ERR_INVALID, "set_max_adapters: negative count");
+  if (n > 0 && static_cast<int64_t>(e->adapters.size()) > n)
+    return fail(WP_ERR_STATE, "set_max_adapters: %zu adapters are registered already", e->adapters.size());
+  e->max_adapters = n;
+  return WP_OK;
+}
 
 int wp_set_entry_offset(wp_engine* e, int32_t offset, int32_t count) {
   if (!e) return fail(WP_ERR_INVALID, "set_entry_offset: engine is NULL");
@@ -1059,13 +1113,45 @@ int wp_read_device_errors(wp_engine* e, uint32_t* flags, void* stream_) {
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   if (stream_capturing(stream)) return fail(WP_ERR_STATE, "read_device_errors cannot run during graph capture");
   uint32_t v = 0;
-  WP_HIP(hipMemcpyAsync(&v, e->header + kHdrErrors, sizeof(v), hipMemcpyDeviceToHost, stream));
+  // Bits a poll (wp_poll_device_errors) has already moved out of the word.
+  if (e->err_pending) {
+    WP_HIP(hipEventSynchronize(e->err_ready));
+    v |= __atomic_load_n(e->err_host, __ATOMIC_ACQUIRE);
+    e->err_pending = false;
+  }
+  uint32_t w = 0;
+  WP_HIP(hipMemcpyAsync(&w, e->header + kHdrErrors, sizeof(w), hipMemcpyDeviceToHost, stream));
   WP_HIP(hipStreamSynchronize(stream));
   WP_HIP(launch_fill_u32(e->header + kHdrErrors, 0u, 1, stream));
+  v |= w;
   // After a give-up the buffer is repaired here too, not only at the next plan build.
   if (v & kErrSpin) WP_HIP(launch_maintain(e->header, maint_view(e), stream));
   WP_HIP(hipStreamSynchronize(stream));
   *flags = v;
+  return WP_OK;
+}
+
+int wp_poll_device_errors(wp_engine* e, uint32_t* flags, void* stream_) {
+  if (!e || !flags) return fail(WP_ERR_INVALID, "poll_device_errors: null argument");
+  *flags = 0;
+  DeviceGuard g(e->device);
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  if (stream_capturing(stream)) return WP_OK;
+  if (e->err_pending) {
+    const hipError_t q = hipEventQuery(e->err_ready);
+    if (q == hipErrorNotReady) {
+      (void)hipGetLastError();
+      return WP_OK;  // the previous take is still in flight: its bits come with a later poll
+    }
+    WP_HIP(q);
+    *flags = __atomic_load_n(e->err_host, __ATOMIC_ACQUIRE);
+    e->err_pending = false;
+  }
+  // The word as of this point of the stream, moved to the host word and
+  // cleared on the device in one exchange.
+  WP_HIP(launch_take_word(e->header + kHdrErrors, e->err_hdev, stream));
+  WP_HIP(hipEventRecord(e->err_ready, stream));
+  e->err_pending = true;
   return WP_OK;
 }
 
@@ -1239,7 +1325,7 @@ int wp_shrink(wp_engine* e, const void* X, void* H, int32_t d_model, int32_t ran
   a.d_model = d_model;
   if ((rc = table_weights(e, stream, &a.w)) != WP_OK) return rc;
   a.w.n_slices = 1;
-  a.n_slots = block_bound(e, resolvable_ids(e));
+  a.n_slots = block_bound(e, resolvable_ids(e, stream));
   if (e->plan_T <= kSmallPlanTokens) {
     // Decode-sized plans: many small shrink workgroups and a reducer per
     // block (the fused calls' shrink side), not one workgroup per block and
@@ -1302,7 +1388,7 @@ int wp_expand(wp_engine* e, const void* H, void* Y, int32_t out_features, int32_
   a.w.oc_start[0] = 0;
   a.w.oc_start[1] = static_cast<int32_t>(ceil_div(out_features, cols));
   a.n_ochunks = a.w.oc_start[1];
-  a.n_slots = block_bound(e, resolvable_ids(e));
+  a.n_slots = block_bound(e, resolvable_ids(e, stream));
   WP_HIP(launch_expand(dtype == WP_DTYPE_BF16, a, stream));
   return WP_OK;
 }
@@ -1501,7 +1587,7 @@ int wp_shrink_expand(wp_engine* e, const void* X, void* Y, int32_t d_model, int3
   a.w.oc_start[0] = 0;
   a.w.oc_start[1] = static_cast<int32_t>(ceil_div(out_features, cols));
   a.n_ochunks = a.w.oc_start[1];
-  a.n_slots = block_bound(e, resolvable_ids(e));
+  a.n_slots = block_bound(e, resolvable_ids(e, stream));
   fused_split(&a, rank, d_model, e->n_cu);
   WP_HIP(launch_fused(dtype == WP_DTYPE_BF16, a, stream));
   return WP_OK;
@@ -1585,11 +1671,241 @@ int wp_shrink_expand_slices(wp_engine* e, const void* X, void* Y, int32_t d_mode
   a.n_ochunks = oc;
   // Blocks: bounded as for one layer's window (an id registered in any
   // slice's layer forms a block).
-  int64_t ids = static_cast<int64_t>(e->adapters.size());
-  if (ids_per_layer > 0) ids = std::min<int64_t>(ids, ids_per_layer);
-  a.n_slots = block_bound(e, ids);
+  const int64_t window = ids_per_layer > 0 ? ids_per_layer : static_cast<int64_t>(e->table_cap);
+  a.n_slots = block_bound(e, call_ids(e, stream, static_cast<int64_t>(e->adapters.size()), window));
   fused_split(&a, rank, d_model, e->n_cu);
   WP_HIP(launch_fused(dtype == WP_DTYPE_BF16, a, stream));
+  return WP_OK;
+}
+
+}  // extern "C"
+
+// ============================================================================
+// vLLM V1's LoRA ops (PunicaWrapperGPU.add_shrink / add_expand /
+// add_lora_linear's bias) on the current plan and stacked weights.
+// ============================================================================
+
+namespace {
+
+// Launch fields of a stacked-weight call that every V1 op shares.
+ApplyArgs stacked_base(const wp_engine* e, int32_t rank, int32_t num_loras, float scale) {
+  ApplyArgs a = base_args(e, rank);
+  a.w.mode = kStacked;
+  a.w.num_ids = num_loras;
+  a.w.scale = scale;
+  a.w.n_slices = 1;
+  a.n_slots = block_bound(e, num_loras);
+  return a;
+}
+
+int check_plan_for(const wp_engine* e, const char* who, int64_t T) {
+  if (e->plan_kind == 0) return fail(WP_ERR_STATE, "%s: no segment table (call build_seg_bounds first)", who);
+  if (e->plan_T > T)
+    return fail(WP_ERR_INVALID, "%s: segments reach token %lld but the call has %lld rows", who, (long long)e->plan_T,
+                (long long)T);
+  return WP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int wp_lora_shrink(wp_engine* e, float* out, int64_t out_slice_stride, int64_t out_row_stride, const void* x,
+                   int32_t n_slices, const void* const* wa, const int64_t* wa_stride0, int32_t num_loras, float scale,
+                   int32_t rank, int32_t d_model, int64_t T, int32_t dtype, void* stream_) {
+  const char* who = "lora_shrink";
+  if (!e) return fail(WP_ERR_INVALID, "%s: engine is NULL", who);
+  if (!rank_ok(rank)) return WP_NOT_HANDLED;
+  int rc = check_io(who, dtype, x, "x");
+  if (rc != WP_OK) return rc;
+  if (!out || !aligned(out, 16)) return fail(WP_ERR_INVALID, "%s: the fp32 output must be 16-byte aligned", who);
+  if (out_row_stride < rank || out_row_stride % 4 != 0 || out_slice_stride < 0 || out_slice_stride % 4 != 0)
+    return fail(WP_ERR_INVALID, "%s: output rows of >= rank fp32 and strides that are multiples of 4", who);
+  if (n_slices < 1 || n_slices > kMaxSlices || !wa || !wa_stride0)
+    return fail(WP_ERR_INVALID, "%s: 1..%d slices, each with its lora_a", who, kMaxSlices);
+  for (int s = 0; s < n_slices; ++s) {
+    if ((rc = check_io(who, dtype, wa[s], "lora_a")) != WP_OK) return rc;
+    if (!wa[s] || wa_stride0[s] % 8 != 0) return fail(WP_ERR_INVALID, "%s: lora_a stride must be a multiple of 8", who);
+  }
+  if (d_model <= 0 || d_model % 8 != 0) return fail(WP_ERR_INVALID, "%s: d_model must be a positive multiple of 8", who);
+  if (num_loras <= 0) return fail(WP_ERR_INVALID, "%s: num_loras must be positive", who);
+  if ((rc = check_plan_for(e, who, T)) != WP_OK) return rc;
+  DeviceGuard g(e->device);
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  for (int s = 0; s < n_slices; ++s) {
+    ApplyArgs a = stacked_base(e, rank, num_loras, scale);
+    a.x = x;
+    a.ldx = d_model;
+    a.d_model = d_model;
+    a.w.a_base[0] = wa[s];
+    a.w.a_stride[0] = wa_stride0[s];
+    a.h = out + s * out_slice_stride;
+    a.ldh = out_row_stride;
+    a.h_f32 = 1;
+    if (e->plan_bt <= 16) {
+      shrink_small_split(d_model, rank, &a);
+      a.red_first = 2 * static_cast<int64_t>(a.n_slots) <= static_cast<int64_t>(e->n_cu) * shrink_small_waves_per_simd() ? 1 : 0;
+      WP_HIP(launch_shrink_small(dtype == WP_DTYPE_BF16, a, stream));
+    } else {
+      shrink_range_split(d_model, &a);
+      a.part = e->spart;
+      a.ptok = e->tok_cap;
+      WP_HIP(launch_shrink(dtype == WP_DTYPE_BF16, a, stream));
+    }
+  }
+  return WP_OK;
+}
+
+int wp_add_bias(wp_engine* e, void* y, int64_t y_row_stride, int32_t n_slices, const void* const* bias,
+                const int64_t* bias_stride0, const int32_t* out_features, const int32_t* y_col_offsets,
+                int32_t num_loras, int64_t T, int32_t dtype, void* stream_) {
+  const char* who = "add_bias";
+  if (!e) return fail(WP_ERR_INVALID, "%s: engine is NULL", who);
+  int rc = check_io(who, dtype, nullptr, "");
+  if (rc != WP_OK) return rc;
+  if (!y || !aligned(y, 8) || y_row_stride % 4 != 0) return fail(WP_ERR_INVALID, "%s: y must be 8-byte aligned with a row stride that is a multiple of 4", who);
+  if (n_slices < 1 || n_slices > kMaxSlices || !bias || !bias_stride0 || !out_features || !y_col_offsets)
+    return fail(WP_ERR_INVALID, "%s: 1..%d slices with their biases, strides, widths and offsets", who, kMaxSlices);
+  if (num_loras <= 0) return fail(WP_ERR_INVALID, "%s: num_loras must be positive", who);
+  PrepArgs p{};
+  bool any = false;
+  for (int s = 0; s < n_slices; ++s) {
+    if (out_features[s] <= 0 || out_features[s] % 4 != 0 || y_col_offsets[s] < 0 || y_col_offsets[s] % 4 != 0 ||
+        y_col_offsets[s] + out_features[s] > y_row_stride)
+      return fail(WP_ERR_INVALID, "%s: slice %d window [%d, %d) does not fit y (row stride %lld, 4-aligned)", who, s,
+                  y_col_offsets[s], y_col_offsets[s] + out_features[s], (long long)y_row_stride);
+    if (bias[s] != nullptr && (!aligned(bias[s], 8) || bias_stride0[s] % 4 != 0 || bias_stride0[s] < out_features[s]))
+      return fail(WP_ERR_INVALID, "%s: slice %d bias rows must be 8-byte aligned, >= the slice width and 4-aligned apart",
+                  who, s);
+    p.o_size[s] = out_features[s];
+    p.y_off[s] = y_col_offsets[s];
+    p.bias[s] = bias[s];
+    p.bias_stride[s] = bias_stride0[s];
+    any = any || bias[s] != nullptr;
+  }
+  if ((rc = check_plan_for(e, who, T)) != WP_OK) return rc;
+  if (!any) return WP_OK;
+  DeviceGuard g(e->device);
+  p.plan = plan_view(e);
+  p.n_slots = block_bound(e, num_loras);
+  p.n_slices = n_slices;
+  p.num_ids = num_loras;
+  p.y = y;
+  p.ldy = y_row_stride;
+  WP_HIP(launch_prep(dtype == WP_DTYPE_BF16, p, static_cast<hipStream_t>(stream_)));
+  return WP_OK;
+}
+
+int wp_lora_expand(wp_engine* e, void* y, int64_t y_row_stride, const void* h, int32_t h_is_f32, int64_t h_slice_stride,
+                   int64_t h_row_stride, int32_t n_slices, const void* const* wb, const int64_t* wb_stride0,
+                   const int32_t* out_features, const int32_t* y_col_offsets, const void* const* bias,
+                   const int64_t* bias_stride0, int32_t num_loras, int32_t rank, int64_t T, int32_t add_inputs,
+                   int32_t dtype, void* stream_) {
+  const char* who = "lora_expand";
+  if (!e) return fail(WP_ERR_INVALID, "%s: engine is NULL", who);
+  if (!rank_ok(rank)) return WP_NOT_HANDLED;
+  int rc = check_io(who, dtype, nullptr, "");
+  if (rc != WP_OK) return rc;
+  if (!h || !aligned(h, h_is_f32 ? 4 : 2)) return fail(WP_ERR_INVALID, "%s: null or misaligned input", who);
+  if (h_row_stride < rank || h_slice_stride < 0) return fail(WP_ERR_INVALID, "%s: input rows must hold rank values", who);
+  if (!y || !aligned(y, 8) || y_row_stride % 4 != 0)
+    return fail(WP_ERR_INVALID, "%s: y must be 8-byte aligned with a row stride that is a multiple of 4", who);
+  if (n_slices < 1 || n_slices > kMaxSlices || !wb || !wb_stride0 || !out_features || !y_col_offsets)
+    return fail(WP_ERR_INVALID, "%s: 1..%d slices with their lora_b, widths and offsets", who, kMaxSlices);
+  if (num_loras <= 0) return fail(WP_ERR_INVALID, "%s: num_loras must be positive", who);
+  if ((rc = check_plan_for(e, who, T)) != WP_OK) return rc;
+  if (e->plan_T > e->tok_cap) return fail(WP_ERR_CAPACITY, "%s: the table reaches past the engine's H rows", who);
+  PrepArgs p{};
+  ApplyArgs a{};
+  {
+    a = stacked_base(e, rank, num_loras, 1.0f);
+    a.h = e->hbuf;
+    a.ldh = static_cast<int64_t>(n_slices) * rank;
+    a.y = y;
+    a.ldy = y_row_stride;
+    a.hs1 = rank;
+    a.hs = n_slices * rank;
+    a.w.n_a = n_slices;  // slice s reads H columns [s * rank, (s + 1) * rank)
+    a.w.n_slices = n_slices;
+    const int cols = expand_cols_per_workgroup();
+    int oc = 0;
+    for (int s = 0; s < n_slices; ++s) {
+      if ((rc = check_io(who, dtype, wb[s], "lora_b")) != WP_OK) return rc;
+      if (!wb[s] || wb_stride0[s] % 8 != 0) return fail(WP_ERR_INVALID, "%s: lora_b stride must be a multiple of 8", who);
+      if (out_features[s] <= 0 || out_features[s] % 4 != 0 || y_col_offsets[s] < 0 || y_col_offsets[s] % 4 != 0 ||
+          y_col_offsets[s] + out_features[s] > y_row_stride)
+        return fail(WP_ERR_INVALID, "%s: slice %d window [%d, %d) does not fit y (row stride %lld, 4-aligned)", who, s,
+                    y_col_offsets[s], y_col_offsets[s] + out_features[s], (long long)y_row_stride);
+      const void* bs = bias ? bias[s] : nullptr;
+      if (bs != nullptr && (!bias_stride0 || !aligned(bs, 8) || bias_stride0[s] % 4 != 0 || bias_stride0[s] < out_features[s]))
+        return fail(WP_ERR_INVALID, "%s: slice %d bias rows must be 8-byte aligned, >= the slice width and 4-aligned apart",
+                    who, s);
+      a.w.b_base[s] = wb[s];
+      a.w.b_stride[s] = wb_stride0[s];
+      a.w.o_size[s] = out_features[s];
+      a.w.y_off[s] = y_col_offsets[s];
+      a.w.oc_start[s] = oc;
+      oc += static_cast<int>(ceil_div(out_features[s], cols));
+      p.o_size[s] = out_features[s];
+      p.y_off[s] = y_col_offsets[s];
+      p.bias[s] = add_inputs ? bs : nullptr;
+      p.bias_stride[s] = bs ? bias_stride0[s] : 0;
+    }
+    a.w.oc_start[n_slices] = oc;
+    a.n_ochunks = oc;
+  }
+  DeviceGuard g(e->device);
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  // The input rounded into the engine's H rows (vLLM's lora_expand casts an
+  // fp32 input to the weights' type before the product), the windows zeroed
+  // when the expand overwrites, the biases added when it adds.
+  p.plan = plan_view(e);
+  p.n_slots = a.n_slots;
+  p.n_slices = n_slices;
+  p.num_ids = num_loras;
+  p.rank = rank;
+  p.h_src = h;
+  p.h_f32 = h_is_f32 ? 1 : 0;
+  p.h_slice_stride = h_slice_stride;
+  p.h_row_stride = h_row_stride;
+  p.h_dst = e->hbuf;
+  p.ldh_dst = n_slices * rank;
+  p.y = y;
+  p.ldy = y_row_stride;
+  p.zero_y = add_inputs ? 0 : 1;
+  WP_HIP(launch_prep(dtype == WP_DTYPE_BF16, p, stream));
+  WP_HIP(launch_expand(dtype == WP_DTYPE_BF16, a, stream));
+  return WP_OK;
+}
+
+int wp_barrier_probe(const uint32_t* salts, int32_t rounds, int32_t threads, int32_t workgroups, uint32_t* mismatches,
+                     void* stream) {
+  if (!salts || !mismatches || rounds < 1 || workgroups < 1 || (threads != 256 && threads != 1024))
+    return fail(WP_ERR_INVALID, "barrier_probe: salts[rounds], a mismatch word, 256 or 1024 threads");
+  WP_HIP(launch_barrier_probe(salts, rounds, threads, workgroups, mismatches, static_cast<hipStream_t>(stream)));
+  return WP_OK;
+}
+
+int wp_handoff_probe(const void* a, int64_t a_bytes, const void* b, int64_t b_bytes, void* y, int64_t y_bytes,
+                     uint32_t* counters, uint32_t* err, int32_t group, int32_t mode, int32_t workgroups, void* stream) {
+  if (a_bytes < 0 || b_bytes < 0 || y_bytes < 0 || a_bytes % 16 || b_bytes % 16 || y_bytes % 16 ||
+      (a_bytes && !aligned(a, 16)) || (b_bytes && !aligned(b, 16)) || (y_bytes && !aligned(y, 16)) || !counters ||
+      !err || group < 1 || mode < 0 || mode > 2 || workgroups < 1)
+    return fail(WP_ERR_INVALID, "handoff_probe: 16-byte aligned buffers of multiples of 16 bytes, counters, an error "
+                                "word, group >= 1, mode 0..2");
+  HandoffProbe p{};
+  p.a = a;
+  p.a16 = static_cast<uint64_t>(a_bytes) / 16;
+  p.b = b;
+  p.b16 = static_cast<uint64_t>(b_bytes) / 16;
+  p.y = y;
+  p.y16 = static_cast<uint64_t>(y_bytes) / 16;
+  p.counters = counters;
+  p.err = err;
+  p.group = group;
+  p.mode = mode;
+  p.spin_limit = kDefaultSpinLimit;
+  WP_HIP(launch_handoff_probe(p, workgroups, static_cast<hipStream_t>(stream)));
   return WP_OK;
 }
 
@@ -1715,6 +2031,21 @@ int wp_add_lora_static(void* y, const void* x, const void* idx, int32_t idx_is_i
   a.n_slots = static_cast<int>(std::min<int64_t>(T, T / bt + std::min<int64_t>(num_loras, T)));
   fused_split(&a, rank, d_model, sd->n_cu);
   WP_HIP(launch_fused(dtype == WP_DTYPE_BF16, a, stream));
+  return WP_OK;
+}
+
+int wp_read_static_errors(int32_t device, uint32_t* out, void* stream_) {
+  if (!out) return fail(WP_ERR_INVALID, "read_static_errors: out is NULL");
+  int ndev = 0;
+  WP_HIP(hipGetDeviceCount(&ndev));
+  if (device < 0 || device >= ndev || device >= kStaticMaxDevices)
+    return fail(WP_ERR_NO_DEVICE, "read_static_errors: device %d out of range", device);
+  DeviceGuard g(device);
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  StaticDevice* sd = nullptr;
+  const int rc = static_scratch(device, stream, &sd);
+  if (rc != WP_OK) return rc;
+  WP_HIP(launch_take_word(reinterpret_cast<uint32_t*>(sd->ptr + kSOffHdr) + kHdrErrors, out, stream));
   return WP_OK;
 }
 

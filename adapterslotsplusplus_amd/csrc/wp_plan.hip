@@ -23,14 +23,11 @@
 #include <hip/hip_runtime.h>
 
 #include "wp_apply.h"
+#include "wp_sync.h"
 
 namespace wp {
 namespace {
 
-// Workgroup barrier for LDS data: waits for this wave's LDS accesses, not
-// for its global stores (a __syncthreads would wait for those to be
-// acknowledged; nothing here reads back what it stored to global memory).
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // Exclusive scan of one int per thread across the workgroup.  `scratch` holds
 // NT/64 ints.  Returns the thread's exclusive prefix; *total gets the sum.
@@ -287,8 +284,11 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
   maintain(header, m, s_scan);
   // The table version the block entry copies below are taken at (every
   // install above has raised it before maintain's closing barrier).
+  // A build without copies records a version that no table write produces
+  // (the complement of the current one), so copies left by an earlier build
+  // can never pass for current ones.
   const uint32_t table_ver =
-      tid == 0 && bentries != nullptr ? __hip_atomic_load(&header[kHdrTableVer], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+      tid == 0 ? __hip_atomic_load(&header[kHdrTableVer], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
 
   // ids -> LDS.
 #pragma unroll
@@ -554,7 +554,7 @@ __global__ __launch_bounds__(NT) void plan_kernel(const void* __restrict__ idx, 
     header[kHdrNumValid] = static_cast<uint32_t>(n_tok);
     header[kHdrT] = static_cast<uint32_t>(T);
     header[kHdrBlockTokens] = static_cast<uint32_t>(bt);
-    if (bentries != nullptr) header[kHdrPlanVer] = table_ver;
+    header[kHdrPlanVer] = bentries != nullptr ? table_ver : ~table_ver;
   }
   plan_stamp(m, 7);
 }

@@ -86,7 +86,9 @@ enum HeaderWord : int {
   // kernel, a plan build's installed publications).
   kHdrTableVer = 8,
   // The table version a plan build copied its blocks' entries at (see
-  // Weights::a_base); the copies hold while the two words are equal.
+  // Weights::a_base); the copies hold while the two words are equal.  A
+  // build without copies stores the complement of the current version, so
+  // copies an earlier build left behind never count as current.
   kHdrPlanVer = 9,
   kHdrWords = 16
 };

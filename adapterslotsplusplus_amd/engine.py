@@ -255,6 +255,27 @@ class WarpPipeEngine:
         _lib.check(self._lib.wp_read_device_errors(self._handle, ctypes.byref(v), self._stream()), "device_errors")
         return int(v.value)
 
+    def poll_device_errors(self) -> int:
+        """The device error word without a host wait (not in the reference):
+        returns the bits an earlier poll moved out of the word if that move
+        has completed (else 0: they come with a later poll or with
+        device_errors()), then enqueues the next move on torch's current
+        stream.  For serving loops, once per step outside graph capture; a
+        no-op returning 0 while the stream is capturing."""
+        v = ctypes.c_uint32(0)
+        _lib.check(self._lib.wp_poll_device_errors(self._handle, ctypes.byref(v), self._stream()),
+                   "poll_device_errors")
+        return int(v.value)
+
+    def set_max_adapters(self, n: Optional[int]) -> None:
+        """Declares the most adapters that will be registered at once (not in
+        the reference; None or 0 withdraws the declaration).  Adapter-store
+        calls (shrink / expand / shrink_expand / shrink_expand_slices on a
+        build_seg_bounds table) captured into a graph then size their grids by
+        n instead of by every id of the table, and registering an (n+1)-th
+        adapter raises."""
+        _lib.check(self._lib.wp_set_max_adapters(self._handle, int(n or 0)), "set_max_adapters")
+
     # --------------------------------------------------------------- apply --
     def shrink(self, X, d_model, rank, total_tokens, out=None, layer=None):
         """H = rn(alpha * X . A^T) per segment; returns a new zero-initialised
@@ -493,6 +514,151 @@ class WarpPipeEngine:
             acc += int(o)
         return self.add_lora_slices(y, x, list(lora_a_stacked), list(lora_b_stacked), scale, offs,
                                     [int(o) for o in output_slices])
+
+    # ------------------------------------------------- vLLM V1 LoRA ops --
+    # The grouped ops behind vLLM V1's PunicaWrapperGPU (add_shrink,
+    # add_expand, add_lora_embedding, add_lora_linear's bias), on the last
+    # build_seg_bounds table; not in the reference, which hooks only the V0
+    # add_lora (lora_warp_pipe/punica_wrapper.py:8-16).  Stacked weights as
+    # vLLM holds them: lora_a [L, 1, r, d], lora_b [L, 1, o, r], bias
+    # [L, 1, o] (or [L, o]).  Each returns False when the shapes have no
+    # kernel (the caller falls back) and raises on invalid arguments.
+
+    def _rank_ok(self, rank: int) -> bool:
+        ok = self._ranks.get(rank)
+        if ok is None:
+            ok = self._ranks[rank] = bool(self._ext.rank_supported(rank))
+        return ok
+
+    def _stacked(self, ts: Sequence[torch.Tensor], dtype, what: str):
+        for t in ts:
+            self._on_device(t, what)
+            if t.dtype != dtype:
+                raise RuntimeError(f"{what} must have the activations' dtype {dtype}, got {t.dtype}")
+            if t.dim() < 2 or not t[0].is_contiguous():
+                raise RuntimeError(f"{what}: each adapter's matrix must be contiguous")
+        n = len(ts)
+        return ((ctypes.c_void_p * n)(*[t.data_ptr() for t in ts]),
+                (ctypes.c_int64 * n)(*[int(t.stride(0)) for t in ts]))
+
+    def lora_shrink(self, out: torch.Tensor, x: torch.Tensor, lora_a_stacked: Sequence[torch.Tensor],
+                    scale: float) -> bool:
+        """out[s][t, :r] += scale * x[t] . lora_a_stacked[s][id_t]^T in fp32,
+        unrounded (V1's add_shrink / lora_shrink buffer); out is fp32
+        [n_slices, T, >= r] (or a sequence of [T, >= r] views of one such
+        tensor), 16-byte aligned with rows a multiple of 4 floats apart.
+        Tokens without an adapter keep their rows."""
+        was = list(lora_a_stacked)
+        n = len(was)
+        rank = int(was[0].size(-2))
+        if n < 1 or n > 4 or not self._rank_ok(rank) or any(int(w.size(-2)) != rank for w in was):
+            return False
+        self._on_device(x, "x")
+        dt = _dtype_code(x, "x")
+        x2 = x.reshape(-1, x.size(-1))
+        if not x2.is_contiguous():
+            raise RuntimeError("lora_shrink: x must be contiguous")
+        T, d = int(x2.size(0)), int(x2.size(1))
+        L = int(was[0].size(0))
+        if any(int(w.size(0)) != L or int(w.size(-1)) != d for w in was):
+            raise RuntimeError("lora_shrink: every lora_a must be [L, 1, r, d] with x's d")
+        a_ptrs, a_strides = self._stacked(was, x.dtype, "lora_a_stacked")
+        outs = list(out) if isinstance(out, (list, tuple)) else [out[s] for s in range(int(out.size(0)))]
+        if len(outs) != n:
+            raise RuntimeError(f"lora_shrink: {len(outs)} output slices for {n} lora_a tensors")
+        o0 = outs[0]
+        for o in outs:
+            self._on_device(o, "out")
+            if o.dtype != torch.float32 or o.dim() != 2 or o.stride(1) != 1 or int(o.size(0)) < T:
+                raise RuntimeError("lora_shrink: out slices must be fp32 [T, >= rank] with unit column stride")
+            if o.stride(0) != o0.stride(0):
+                raise RuntimeError("lora_shrink: out slices must share one row stride")
+        row = int(o0.stride(0))
+        sstride = (outs[1].data_ptr() - o0.data_ptr()) // 4 if n > 1 else 0
+        if any(outs[s].data_ptr() != o0.data_ptr() + 4 * s * sstride for s in range(n)) or sstride < 0:
+            raise RuntimeError("lora_shrink: out slices must be evenly spaced in one buffer")
+        rc = _lib.check(self._lib.wp_lora_shrink(self._handle, _ptr(o0), sstride, row, _ptr(x2), n, a_ptrs, a_strides, L,
+                                                 float(scale), rank, d, T, dt, self._stream()), "lora_shrink")
+        return rc == _lib.WP_OK
+
+    def _bias_args(self, biases, y, n: int, what: str):
+        bs = list(biases) if biases is not None else [None] * n
+        if len(bs) != n:
+            raise RuntimeError(f"{what}: {len(bs)} biases for {n} slices")
+        ptrs, strides = [], []
+        for b in bs:
+            if b is None:
+                ptrs.append(None)
+                strides.append(0)
+                continue
+            self._on_device(b, "lora_bias_stacked")
+            if b.dtype != y.dtype:
+                raise RuntimeError(f"{what}: lora_bias_stacked must have y's dtype")
+            b2 = b.reshape(b.size(0), -1)
+            if b2.stride(1) != 1 or b2.data_ptr() != b.data_ptr():
+                raise RuntimeError(f"{what}: each adapter's bias row must be contiguous")
+            ptrs.append(b.data_ptr())
+            strides.append(int(b2.stride(0)))
+        return (ctypes.c_void_p * n)(*ptrs), (ctypes.c_int64 * n)(*strides), any(b is not None for b in bs)
+
+    def add_bias(self, y: torch.Tensor, lora_bias_stacked, output_slices: Sequence[int], num_loras: int,
+                 offset_start: int = 0) -> None:
+        """V1's _apply_bias: y[t, window s] = rn(y[t, window s] + bias[s][id_t])
+        for every token with an adapter and every slice whose bias is not
+        None; slice windows are consecutive from offset_start."""
+        self._on_device(y, "y")
+        dt = _dtype_code(y, "y")
+        y2 = y.reshape(-1, y.size(-1))
+        if not y2.is_contiguous() or y2.data_ptr() != y.data_ptr():
+            raise RuntimeError("add_bias: y must be contiguous")
+        n = len(output_slices)
+        offs = [int(offset_start) + sum(int(o) for o in output_slices[:i]) for i in range(n)]
+        b_ptrs, b_strides, _ = self._bias_args(lora_bias_stacked, y, n, "add_bias")
+        o_arr = (ctypes.c_int32 * n)(*[int(o) for o in output_slices])
+        off_arr = (ctypes.c_int32 * n)(*offs)
+        _lib.check(self._lib.wp_add_bias(self._handle, _ptr(y2), int(y2.size(1)), n, b_ptrs, b_strides, o_arr, off_arr,
+                                         int(num_loras), int(y2.size(0)), dt, self._stream()), "add_bias")
+
+    def lora_expand(self, y: torch.Tensor, h: torch.Tensor, lora_b_stacked: Sequence[torch.Tensor],
+                    output_slices: Sequence[int], offset_start: int = 0, add_inputs: bool = True,
+                    lora_bias_stacked=None) -> bool:
+        """V1's lora_expand: for every slice s and token t with an adapter,
+        y[t, off_s + o] = rn((add_inputs ? y'[t, off_s + o] : 0) + rn(h[s][t]) . B_s[id_t][o]^T)
+        with slice windows consecutive from offset_start and y' = rn(y + bias)
+        where lora_bias_stacked[s] is given (add_inputs only).  h: [n, T, r]
+        fp32 (rounded to y's dtype first, as V1 casts it) or y's dtype.  Two
+        launches; tokens without an adapter keep their rows."""
+        wbs = list(lora_b_stacked)
+        n = len(wbs)
+        rank = int(wbs[0].size(-1))
+        if n < 1 or n > 4 or not self._rank_ok(rank) or any(int(w.size(-1)) != rank for w in wbs):
+            return False
+        self._on_device(y, "y")
+        self._on_device(h, "h")
+        dt = _dtype_code(y, "y")
+        y2 = y.reshape(-1, y.size(-1))
+        if not y2.is_contiguous() or y2.data_ptr() != y.data_ptr():
+            raise RuntimeError("lora_expand: y must be contiguous")
+        T = int(y2.size(0))
+        if h.dim() != 3 or int(h.size(0)) != n or h.stride(2) != 1 or int(h.size(1)) < T or int(h.size(2)) < rank:
+            raise RuntimeError(f"lora_expand: h must be [{n}, >= {T}, >= {rank}] with unit column stride")
+        if h.dtype not in (torch.float32, y.dtype):
+            raise RuntimeError("lora_expand: h must be fp32 or y's dtype")
+        L = int(wbs[0].size(0))
+        outs = [int(o) for o in output_slices]
+        if len(outs) != n or any(int(w.size(0)) != L or int(w.size(-2)) != o for w, o in zip(wbs, outs)):
+            raise RuntimeError("lora_expand: lora_b_stacked[s] must be [L, 1, output_slices[s], r]")
+        b_ptrs, b_strides = self._stacked(wbs, y.dtype, "lora_b_stacked")
+        bias_ptrs, bias_strides, _ = self._bias_args(lora_bias_stacked, y, n, "lora_expand")
+        offs = [int(offset_start) + sum(outs[:i]) for i in range(n)]
+        o_arr = (ctypes.c_int32 * n)(*outs)
+        off_arr = (ctypes.c_int32 * n)(*offs)
+        rc = _lib.check(self._lib.wp_lora_expand(self._handle, _ptr(y2), int(y2.size(1)), _ptr(h),
+                                                 1 if h.dtype == torch.float32 else 0, int(h.stride(0)),
+                                                 int(h.stride(1)), n, b_ptrs, b_strides, o_arr, off_arr, bias_ptrs,
+                                                 bias_strides, L, rank, T, 1 if add_inputs else 0, dt, self._stream()),
+                        "lora_expand")
+        return rc == _lib.WP_OK
 
     # ------------------------------------------------------------- staging --
     def prefetch_adapter(self, adapter_id, layer=None) -> int:

@@ -35,6 +35,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .engine import WarpPipeEngine
+from .punica_wrapper import report_device_errors
 
 
 class DraftLoRAContext:
@@ -55,6 +56,19 @@ class DraftLoRAContext:
         self.fused_linear = bool(fused_linear)
         dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
         self.idx = torch.zeros(self.tokens, dtype=torch.int64, device=dev)
+        # OR of every device error bit poll_errors has seen.
+        self.device_errors = 0
+
+    def poll_errors(self) -> int:
+        """Device error bits of earlier steps (tokens the kernels skipped, whose
+        rows lack their LoRA delta), without a host wait: the bits an earlier
+        poll moved to host memory once that move has landed.  ORs them into
+        `device_errors` and reports them (a logged warning, or RuntimeError
+        with AS_WARP_PIPE_STRICT=1).  Call outside graph capture; replay
+        loops call it between replays."""
+        bits = self.engine.poll_device_errors()
+        self.device_errors |= bits
+        return report_device_errors(bits, "DraftLoRAContext")
 
     def set_routing(self, ids: torch.Tensor) -> None:
         """Copies per-token adapter ids into the routing buffer (stream-ordered,
@@ -66,9 +80,13 @@ class DraftLoRAContext:
 
     def begin_step(self) -> None:
         """Builds the step's segment table from `idx` (once per step, before the
-        model's forward; inside a captured step it is one graph node)."""
+        model's forward; inside a captured step it is one graph node).
+        Outside capture it first reports tokens an earlier step's kernels had
+        to skip (poll_errors)."""
         if self.mode == "none":
             return
+        if not torch.cuda.is_current_stream_capturing():
+            self.poll_errors()
         if not self.engine.build_seg_bounds(self.idx):
             raise RuntimeError(f"DraftLoRAContext: {self.tokens} tokens exceed the engine's max_tokens")
 
@@ -223,5 +241,7 @@ class CapturedStep:
     def replay(self, routing: Optional[torch.Tensor] = None) -> torch.Tensor:
         if routing is not None:
             self.ctx.set_routing(routing)
+        if self.ctx.mode != "none":
+            self.ctx.poll_errors()
         self.graph.replay()
         return self.out

@@ -15,7 +15,10 @@ and :219-238 (install_warp_pipe_add_lora).  Same contract:
 
 Added: add_lora_packed_nslice (vLLM's packed q/k/v and gate/up layers, one
 lora_a / lora_b per slice) runs every slice in one launch; the reference
-leaves it to its parent class (punica_wrapper.py:8-16).
+leaves it to its parent class (punica_wrapper.py:8-16).  update_metadata
+also reports tokens an earlier step's kernels had to skip (the engine's
+device error word, polled without a host wait): a logged warning, or
+RuntimeError with AS_WARP_PIPE_STRICT=1.
 
 Differences: the reference can only subclass AdapterSlots' FusedPunicaWrapper
 (an absent dependency here), so the overrides live in a mixin that is combined
@@ -26,6 +29,7 @@ back for that step instead of reusing the previous step's table.
 """
 from __future__ import annotations
 
+import logging
 import os
 from typing import Optional
 
@@ -54,6 +58,34 @@ def warp_pipe_available() -> bool:
     return _WARP_PIPE_IMPORT_OK and os.environ.get("AS_WARP_PIPE", "0") == "1"
 
 
+_log = logging.getLogger(__name__)
+_ERROR_NAMES = ((1, "adapter id outside the stacked weights"), (2, "adapter id not registered"),
+                (4, "adapter shape does not match the call"), (8, "a wait on partial results gave up"),
+                (16, "more adapter blocks than the call's grid"))
+# Every device error bit reported so far in this process (OR of them).
+device_errors_seen = 0
+
+
+def describe_device_errors(bits: int) -> str:
+    return ", ".join(name for bit, name in _ERROR_NAMES if bits & bit) or "none"
+
+
+def report_device_errors(bits: int, where: str) -> int:
+    """Records device error bits that an earlier step's kernels set (tokens
+    they skipped, leaving those rows without their LoRA delta): ORs them into
+    `device_errors_seen`, logs a warning, and raises RuntimeError instead when
+    AS_WARP_PIPE_STRICT=1.  Returns `bits`."""
+    global device_errors_seen
+    if bits:
+        device_errors_seen |= bits
+        msg = (f"WarpPipe: an earlier step skipped tokens (device errors 0x{bits:x}: "
+               f"{describe_device_errors(bits)}); reported at {where}")
+        if os.environ.get("AS_WARP_PIPE_STRICT", "0") == "1":
+            raise RuntimeError(msg)
+        _log.warning(msg)
+    return bits
+
+
 class WarpPipeAddLoraMixin:
     """update_metadata / add_lora overrides; combine with a PunicaWrapper class."""
 
@@ -65,7 +97,11 @@ class WarpPipeAddLoraMixin:
                                 long_lora_context)
         self._wp_step_ok = False
         if not self.is_prefill and warp_pipe_available():  # type: ignore[attr-defined]
-            self._wp_step_ok = bool(_get_engine().build_seg_bounds(self.token_lora_indices))  # type: ignore[attr-defined]
+            engine = _get_engine()
+            # Errors of earlier steps, without a host wait: the bits a
+            # previous poll moved to host memory, once that move has landed.
+            report_device_errors(engine.poll_device_errors(), "update_metadata")
+            self._wp_step_ok = bool(engine.build_seg_bounds(self.token_lora_indices))  # type: ignore[attr-defined]
 
     def add_lora(self, y: torch.Tensor, x: torch.Tensor, wa_t_all: torch.Tensor, wb_t_all: torch.Tensor,
                  scale: float, y_offset: Optional[int] = None, y_slice_size: Optional[int] = None, *,

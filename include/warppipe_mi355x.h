@@ -126,6 +126,18 @@ int wp_has_adapter(wp_engine* e, int32_t adapter_id);
  * offset 0. */
 int wp_set_entry_offset(wp_engine* e, int32_t offset, int32_t count);
 
+/* No reference counterpart (its registry has no capacity, adapter_store.h:12-19):
+ * declares that at most n adapters will be registered at once (0: no
+ * declaration).  Grids of adapter-store calls (shrink, expand, shrink_expand,
+ * shrink_expand_slices on a build_seg_bounds table) hold a block slot per
+ * possible block; an eager call counts the adapters registered when it is
+ * enqueued, but a call captured into a graph is replayed after later
+ * registrations, so without a declaration its grid holds up to T slots
+ * (mostly empty at decode sizes).  With one, both use n, and registering an
+ * (n+1)-th adapter fails with WP_ERR_CAPACITY.  WP_ERR_STATE if more than n
+ * are registered already. */
+int wp_set_max_adapters(wp_engine* e, int64_t n);
+
 /* ---- segment tables ----------------------------------------------------- */
 
 /* Replaces WarpPipeExtension::build_segments (bindings:128-130) /
@@ -153,8 +165,20 @@ int wp_read_segments(wp_engine* e, int32_t* out, int64_t cap, int64_t* num_segme
 int wp_read_plan(wp_engine* e, int32_t* perm, int64_t perm_cap, int32_t* blocks, int64_t block_cap,
                  int64_t* n_valid, int64_t* n_blocks, void* stream);
 
-/* Reads and clears the device error word (bit flags, see wp_types.h). */
+/* Reads and clears the device error word (bit flags, see wp_types.h).
+ * Synchronises `stream`.  Includes bits an earlier wp_poll_device_errors had
+ * moved out of the word and not yet reported. */
 int wp_read_device_errors(wp_engine* e, uint32_t* flags, void* stream);
+
+/* No reference counterpart: the device error word without a host wait on
+ * the compute path, for serving loops (the punica hook's update_metadata,
+ * DraftLoRAContext.begin_step).  *flags gets the bits the previous poll moved
+ * out of the word if that move has completed (0 otherwise: they come with a
+ * later poll or with wp_read_device_errors); then, unless one is still in
+ * flight, one kernel on `stream` moves the word (as of that point of the
+ * stream) into a pinned host word and clears it.  Does nothing while
+ * `stream` is capturing. */
+int wp_poll_device_errors(wp_engine* e, uint32_t* flags, void* stream);
 
 /* ---- apply ---------------------------------------------------------------- */
 
@@ -241,6 +265,19 @@ int wp_add_lora_static(void* y, const void* x, const void* idx, int32_t idx_is_i
                        const int64_t* wb_stride0, const int32_t* out_features, const int32_t* y_col_offsets,
                        float scale, int32_t rank, int32_t d_model, int64_t y_row_stride, int32_t dtype, void* stream);
 
+/* No counterpart in the reference; for the callers of wp_add_lora_static
+ * (those that cannot allocate).  The kernels of wp_add_lora_static skip
+ * tokens they cannot serve and record why in the device error word of the
+ * GPU's static scratch (bit flags as wp_read_device_errors reports them: 1
+ * an id >= num_loras, 8 a wait on partials gave up, 16 more blocks than the
+ * grid holds).  This enqueues, on `stream`, one kernel that copies that word
+ * of device `device` into *out (4 bytes of device-accessible memory the
+ * caller provides) and clears it; it allocates nothing and may be captured
+ * once the device's scratch is set up (its first call on a device, or the
+ * first wp_add_lora_static there, sets it up synchronously, outside capture).
+ * The word is shared like the scratch: calls that overlap on one GPU race. */
+int wp_read_static_errors(int32_t device, uint32_t* out, void* stream);
+
 /* wp_add_lora with one A per output slice: vLLM's add_lora_packed_nslice
  * (packed q/k/v or gate/up layers, each slice with its own lora_a and lora_b;
  * the reference hook leaves this method to the stock path,
@@ -253,6 +290,45 @@ int wp_add_lora_nslice(wp_engine* e, void* y, const void* x, int32_t n_slices, c
                        const int64_t* wa_stride0, const void* const* wb, const int64_t* wb_stride0,
                        const int32_t* out_features, const int32_t* y_col_offsets, int32_t num_loras, float scale,
                        int32_t rank, int32_t d_model, int64_t T, int64_t y_row_stride, int32_t dtype, void* stream);
+
+/* ---- vLLM V1 LoRA ops ------------------------------------------------------ */
+/* No reference counterpart: the reference hooks only vLLM 0.6's add_lora and
+ * scopes the V1 op surface out (lora_warp_pipe/punica_wrapper.py:8-16).  These
+ * are the grouped ops behind V1's PunicaWrapperGPU (add_shrink, add_expand,
+ * add_lora_embedding, add_lora_linear) on the last build_seg_bounds table and
+ * vLLM's stacked weights: lora_a_stacked[s] [L, 1, rank, d], lora_b_stacked[s]
+ * [L, 1, o_s, rank], lora_bias_stacked[s] [L, 1, o_s] (element strides between
+ * adapters given).  add_lora_linear itself is wp_add_bias (if biases) then
+ * wp_add_lora_nslice: no H round trip. */
+
+/* add_shrink: out[s][t][k] += scale * x[t] . wa[s][id_t][k, :] for k < rank,
+ * fp32, unrounded (V1's lora_shrink buffer), for every token t of the table
+ * and slice s; slice s of out starts out_slice_stride floats after slice 0,
+ * rows out_row_stride floats apart (both multiples of 4; out 16-byte
+ * aligned).  WP_NOT_HANDLED for a rank without kernels. */
+int wp_lora_shrink(wp_engine* e, float* out, int64_t out_slice_stride, int64_t out_row_stride, const void* x,
+                   int32_t n_slices, const void* const* wa, const int64_t* wa_stride0, int32_t num_loras, float scale,
+                   int32_t rank, int32_t d_model, int64_t T, int32_t dtype, void* stream);
+
+/* add_expand / add_lora_embedding: for every token t of the table and slice s,
+ *   y[t, off_s + o] = rn((add_inputs ? y'[t, off_s + o] : 0) + rn(h[s][t][:]) . wb[s][id_t][o, :])
+ * with y' = rn(y + bias[s][id_t]) where bias[s] is given (add_inputs only,
+ * as V1 applies the bias before an expand that adds).  h is fp32 (h_is_f32;
+ * rounded to the I/O type first, as V1's lora_expand casts it) or the I/O
+ * type; slice s at h + s * h_slice_stride, rows h_row_stride apart.  Two
+ * launches.  WP_NOT_HANDLED for a rank without kernels. */
+int wp_lora_expand(wp_engine* e, void* y, int64_t y_row_stride, const void* h, int32_t h_is_f32, int64_t h_slice_stride,
+                   int64_t h_row_stride, int32_t n_slices, const void* const* wb, const int64_t* wb_stride0,
+                   const int32_t* out_features, const int32_t* y_col_offsets, const void* const* bias,
+                   const int64_t* bias_stride0, int32_t num_loras, int32_t rank, int64_t T, int32_t add_inputs,
+                   int32_t dtype, void* stream);
+
+/* V1's _apply_bias: y[t, off_s + o] = rn(y[t, off_s + o] + bias[s][id_t][o]) for
+ * every token of the table and every slice whose bias is not NULL (ids >=
+ * num_loras are skipped and flagged, device error 1). */
+int wp_add_bias(wp_engine* e, void* y, int64_t y_row_stride, int32_t n_slices, const void* const* bias,
+                const int64_t* bias_stride0, const int32_t* out_features, const int32_t* y_col_offsets,
+                int32_t num_loras, int64_t T, int32_t dtype, void* stream);
 
 /* ---- staging / prefetch ---------------------------------------------------- */
 
@@ -307,6 +383,29 @@ int wp_set_spin_limit(wp_engine* e, uint32_t polls);
  * it to state the floor of a call: the time one launch takes to read that
  * call's bytes, and the launch cost alone. */
 int wp_read_probe(wp_engine* e, const void* buffer, int64_t bytes, void* sink, void* stream);
+
+/* Measurement, no reference counterpart: what one cross-workgroup dependency
+ * costs a launch that streams a call's bytes.  `workgroups` workgroups of 512
+ * threads each stream their share of `a` (a call's A and X bytes), count
+ * themselves on their group's counter (`group` consecutive workgroups wait
+ * for each other), stream their share of `b` (B, and Y read) -- the first
+ * batch of it before waiting for the group (mode 1), all of it after (mode
+ * 2), or with no wait (mode 0) -- and write their share of `y`.  counters:
+ * 2 x 64 words per group, zero before the first launch (each launch leaves
+ * them zero); *err gets bit 0 if a wait gave up (about 0.1 s; the counters
+ * must then be zeroed again).  All pointers are device memory. */
+int wp_handoff_probe(const void* a, int64_t a_bytes, const void* b, int64_t b_bytes, void* y, int64_t y_bytes,
+                     uint32_t* counters, uint32_t* err, int32_t group, int32_t mode, int32_t workgroups, void* stream);
+
+/* Test of lds_barrier(), the LDS-only workgroup barrier of every kernel here
+ * (the property the reference checks for its barrier wrappers,
+ * tests/unit/test_barrier_sync.cu:21-41): `workgroups` workgroups of `threads`
+ * (256 = 4 wave64 waves, or 1024) run `rounds` rounds in which every thread
+ * writes a value built from salts[round] (a device array) into its LDS slot,
+ * passes the barrier, and checks every slot of the workgroup; mismatches are
+ * added to *mismatches (device memory, zeroed by the caller). */
+int wp_barrier_probe(const uint32_t* salts, int32_t rounds, int32_t threads, int32_t workgroups, uint32_t* mismatches,
+                     void* stream);
 
 /* Diagnostics: in a library built with WP_TRACE (adapterslotsplusplus_amd.build
  * --trace), fused launches whose grid fits record 8 timestamps per workgroup

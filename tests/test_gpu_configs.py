@@ -172,3 +172,68 @@ def test_cfg5_draft_step_graph():
         segs = so.seg_bounds(idx.numpy()).tolist()
         for i in range(0, n_calls, 11):
             assert_close(d_ys[i], bgmv.add_lora(y0s[i], xs[i], was[i], wbs[i], 0.5, segs), f"cfg5 call {i} rep {rep}")
+
+
+@pytest.mark.parametrize("order", ["unsorted", "sorted"])
+def test_cfg3_gate_up_one_launch_full_size(order):
+    """configs[2] at the launch shape the benchmark times for gate+up: a
+    multi-layer store (gate = layer 0, up = layer 1) of the touched adapters
+    of 128 with ranks uniform in {8,16,32,64} (seed 2), T=512 Zipf(1.1)
+    routing (seed 3), d=5120, 2 x 13824 outputs in one shrink_expand_slices
+    launch at mixed ranks; the oracle runs per slice shrink then expand."""
+    from adapterslotsplusplus_amd import WarpPipeConfig
+
+    announce(f"cfg3 gate+up one launch {order}")
+    dt, T, d, o = torch.bfloat16, 512, 5120, 13824
+    g = torch.Generator().manual_seed(2)
+    ranks = [int(v) for v in torch.tensor([8, 16, 32, 64])[torch.randint(0, 4, (128,), generator=g)]]
+    idx = wl.zipf_indices(T, 128, 1.1, seed=3)
+    if order == "sorted":
+        idx = torch.sort(idx).values
+    touched = sorted(set(idx.tolist()))
+    engine = WarpPipeEngine(WarpPipeConfig(layer_stride=128))
+    per_slice = []
+    for lay in range(2):
+        ad = {}
+        for i in touched:
+            r = ranks[i]
+            A = wl.normal((r, d), 0.02, dt, 7000 + 300 * lay + i)
+            B = wl.normal((o, r), 0.02, dt, 8000 + 300 * lay + i)
+            engine.register_adapter(i, A.cuda(), B.cuda(), 16.0 / r, rank=r, layer=lay)
+            ad[i] = (A, B, 16.0 / r)
+        per_slice.append(ad)
+    X = wl.normal((T, d), 1.0, dt, 70)
+    Y0 = wl.normal((T, 2 * o), 1.0, dt, 71)
+    assert engine.build_seg_bounds(idx.cuda())
+    Y = Y0.cuda()
+    engine.shrink_expand_slices(X.cuda(), Y, [0, 1], [o, o], [0, o])
+    torch.cuda.synchronize()
+    segs = so.seg_bounds(idx.numpy()).tolist()
+    ref = Y0.clone()
+    for ad, off in zip(per_slice, [0, o]):
+        H = bgmv.shrink(X, segs, ad, 64, T)
+        ref = bgmv.expand(H, ref, segs, ad, off)
+    assert_close(Y, ref, f"cfg3 gate+up one launch {order}")
+    assert engine.device_errors() == 0
+
+
+@pytest.mark.parametrize("order", ["segments", "shuffled"])
+def test_cfg4_packed_qkv_full_size(order):
+    """configs[3] at the launch shape the benchmark times for q/k/v: T=8192
+    over 16 adapters with lognormal(6, 1) segment lengths (seed 4), r=64,
+    fp16, one add_lora_slices call writing 3 x 4096 columns from one shared
+    A; the tokens in segment order and shuffled (seed 5)."""
+    announce(f"cfg4 packed qkv {order}")
+    dt, T, h, r = torch.float16, 8192, 4096, 64
+    lens = wl.lognormal_segments(T, 16, 6.0, 1.0, seed=4)
+    idx = torch.repeat_interleave(torch.arange(16), torch.tensor(lens))
+    if order == "shuffled":
+        idx = idx[torch.randperm(T, generator=torch.Generator().manual_seed(5))]
+    x = wl.normal((T, h), 1.0, dt, 80)
+    wa = wl.normal((16, 1, r, h), 0.02, dt, 81)
+    wbs = [wl.normal((16, 1, h, r), 0.02, dt, 82 + i) for i in range(3)]
+    y0 = wl.normal((T, 3 * h), 1.0, dt, 85)
+    engine = WarpPipeEngine()
+    assert engine.build_seg_bounds(idx.cuda())
+    add_lora_check(engine, idx, x, y0, wa, wbs, [0, h, 2 * h], 0.25, f"cfg4 packed qkv {order}")
+    assert engine.device_errors() == 0

@@ -100,3 +100,63 @@ def test_static_in_captured_graph_replays():
         torch.cuda.synchronize()
         segs = so.seg_bounds(new_idx.tolist()).tolist()
         assert_close(y, bgmv.add_lora(y0, x, wa, wbs, 2.0, segs, offs), f"replay {rep}")
+
+
+def read_static_errors(out):
+    lib = _lib.load()
+    return lib.wp_read_static_errors(torch.cuda.current_device(), ctypes.c_void_p(out.data_ptr()),
+                                     ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+
+
+def test_static_errors_are_readable_and_cleared():
+    """An id >= num_loras makes the static call skip its tokens (device error
+    1); wp_read_static_errors copies the word into caller memory and clears
+    it, so the next read is 0."""
+    announce("add_lora_static: error word")
+    idx, x, wa, wbs, offs, y0 = case(64, 4, 16, 256, [256], torch.bfloat16, 31)
+    idx[7] = 9
+    word = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+    assert read_static_errors(word) == _lib.WP_OK, _lib.last_error()  # clears what earlier tests left
+    y = y0.cuda()
+    assert static_call(y, x.cuda(), idx.cuda(), wa.cuda(), [w.cuda() for w in wbs], offs, 1.0, 16) == _lib.WP_OK
+    assert read_static_errors(word) == _lib.WP_OK
+    torch.cuda.synchronize()
+    assert int(word.item()) & 1
+    assert read_static_errors(word) == _lib.WP_OK
+    torch.cuda.synchronize()
+    assert int(word.item()) == 0
+    # The rows of valid ids are still applied.
+    keep = [s for s in so.seg_bounds(idx.tolist()).tolist() if s[0] < 4]
+    assert_close(y, bgmv.add_lora(y0, x, wa, wbs, 1.0, keep, offs), "valid rows")
+    assert _lib.load().wp_read_static_errors(0, None, None) == _lib.WP_ERR_INVALID
+
+
+def test_static_at_capacity_allocates_nothing():
+    """T=256 (the static scratch's capacity) against the engine and the
+    oracle; after a first call, further calls of any size leave the device's
+    free memory and torch's allocator untouched."""
+    announce("add_lora_static: T=256 and device memory")
+    engine = WarpPipeEngine()
+    idx, x, wa, wbs, offs, y0 = case(256, 16, 32, 1024, [1024, 512], torch.float16, 41)
+    xd, wad, wbd, idxd = x.cuda(), wa.cuda(), [w.cuda() for w in wbs], idx.cuda()
+    y = y0.cuda()
+    assert static_call(y, xd, idxd, wad, wbd, offs, 0.75, 32) == _lib.WP_OK
+    torch.cuda.synchronize()
+    ref = bgmv.add_lora(y0, x, wa, wbs, 0.75, so.seg_bounds(idx.tolist()).tolist(), offs)
+    assert_close(y, ref, "T=256")
+    ye = y0.cuda()
+    assert engine.build_seg_bounds(idxd)
+    assert engine.add_lora_slices(ye, xd, wad, wbd, 0.75, offs)
+    torch.cuda.synchronize()
+    assert torch.equal(y.cpu(), ye.cpu())
+    sizes = (256, 17, 128)
+    ys = [y0[:T].cuda() for T in sizes]
+    torch.cuda.synchronize()
+    free0, _ = torch.cuda.mem_get_info()
+    alloc0 = torch.cuda.memory_allocated()
+    for T, y2 in zip(sizes, ys):
+        assert static_call(y2, xd[:T], idxd[:T], wad, wbd, offs, 0.75, 32) == _lib.WP_OK
+    torch.cuda.synchronize()
+    free1, _ = torch.cuda.mem_get_info()
+    assert free1 == free0, f"device free memory moved by {free0 - free1} bytes"
+    assert torch.cuda.memory_allocated() == alloc0
