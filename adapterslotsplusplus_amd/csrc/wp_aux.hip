@@ -11,8 +11,8 @@
 //   * barrier_probe_kernel: checks that lds_barrier() makes every wave's LDS
 //     writes visible to every other wave of the workgroup (the property the
 //     reference tests for its barrier wrappers, tests/unit/test_barrier_sync.cu:21-41);
-//   * handoff_probe_kernel: a measurement of what one cross-workgroup
-//     dependency costs a launch that streams a call's bytes.
+//   * handoff_probe_kernel / handoff_split_kernel: measurements of what one
+//     cross-workgroup dependency costs a launch that streams a call's bytes.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -213,6 +213,72 @@ __global__ __launch_bounds__(kHandoffThreads) void handoff_probe_kernel(HandoffP
   for (size_t i = ybeg + threadIdx.x; i < yend; i += kHandoffThreads) __builtin_nontemporal_store(acc, y + i);
 }
 
+// Split-role handoff probe (mode 3): workgroups [0, group) stream the `a`
+// share alone and count themselves on one counter; workgroups [group, grid)
+// stream the whole `b` share first, then wait for every `a` workgroup's count
+// and write the `y` share.  96 KB of LDS per workgroup keeps one workgroup on
+// each compute unit, so a role is a compute unit's role: the `a` side's count
+// never queues behind `b` loads in its compute unit's memory pipeline.  The
+// last `b` workgroup past the wait resets the counters.
+__device__ __forceinline__ u32x4 stream_part(const u32x4* __restrict__ p, size_t n16, int part, int parts, u32x4 acc) {
+  const size_t per = (n16 + parts - 1) / parts;
+  const size_t beg = static_cast<size_t>(part) * per;
+  const size_t end = beg + per < n16 ? beg + per : n16;
+  for (size_t i = beg + threadIdx.x; i < end; i += static_cast<size_t>(kHandoffThreads) * kHandoffDepth) {
+    u32x4 v[kHandoffDepth];
+#pragma unroll
+    for (int u = 0; u < kHandoffDepth; ++u) {
+      const size_t j = i + static_cast<size_t>(u) * kHandoffThreads;
+      v[u] = j < end ? __builtin_nontemporal_load(p + j) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < kHandoffDepth; ++u) acc ^= v[u];
+  }
+  return acc;
+}
+
+__global__ __launch_bounds__(kHandoffThreads) void handoff_split_kernel(HandoffProbe p) {
+  __shared__ uint32_t s_pad[24 * 1024];
+  __shared__ int s_ok;
+  const int n_a = p.group;
+  const int n_b = static_cast<int>(gridDim.x) - n_a;
+  const int wg = static_cast<int>(blockIdx.x);
+  uint32_t* cnt = p.counters;
+  uint32_t* done = p.counters + kCounterStride;
+  u32x4 acc{0u, 0u, 0u, 0u};
+  if (wg < n_a) {
+    acc = stream_part(static_cast<const u32x4*>(p.a), p.a16, wg, n_a, acc);
+    s_pad[threadIdx.x] = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+    __syncthreads();
+    if (threadIdx.x == 0) atomic_add_u(cnt, 1u);
+    return;
+  }
+  acc = stream_part(static_cast<const u32x4*>(p.b), p.b16, wg - n_a, n_b, acc);
+  if (threadIdx.x == 0) {
+    int ok = 1;
+    for (uint32_t spins = 0; atomic_load_u(cnt) < static_cast<uint32_t>(n_a); ++spins) {
+      if (spins >= p.spin_limit) {
+        ok = 0;
+        atomicOr(p.err, 1u);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+    s_ok = ok;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0 && s_ok != 0 && atomic_add_u(done, 1u) == static_cast<uint32_t>(n_b - 1)) {
+    atomic_store_u(cnt, 0u);
+    atomic_store_u(done, 0u);
+  }
+  u32x4* y = static_cast<u32x4*>(p.y);
+  const size_t yper = (p.y16 + n_b - 1) / n_b;
+  const size_t ybeg = static_cast<size_t>(wg - n_a) * yper;
+  const size_t yend = ybeg + yper < p.y16 ? ybeg + yper : p.y16;
+  acc[0] ^= s_pad[threadIdx.x];
+  for (size_t i = ybeg + threadIdx.x; i < yend; i += kHandoffThreads) __builtin_nontemporal_store(acc, y + i);
+}
+
 }  // namespace
 
 hipError_t launch_take_word(uint32_t* word, uint32_t* out, hipStream_t stream) {
@@ -247,10 +313,14 @@ hipError_t launch_barrier_probe(const uint32_t* salts, int rounds, int threads, 
 }
 
 hipError_t launch_handoff_probe(const HandoffProbe& p, int workgroups, hipStream_t stream) {
-  if (workgroups < 1 || p.group < 1 || p.mode < 0 || p.mode > 2 || p.counters == nullptr || p.err == nullptr ||
-      (p.a16 > 0 && p.a == nullptr) || (p.b16 > 0 && p.b == nullptr) || (p.y16 > 0 && p.y == nullptr))
+  if (workgroups < 1 || p.group < 1 || p.mode < 0 || p.mode > 3 || p.counters == nullptr || p.err == nullptr ||
+      (p.a16 > 0 && p.a == nullptr) || (p.b16 > 0 && p.b == nullptr) || (p.y16 > 0 && p.y == nullptr) ||
+      (p.mode == 3 && p.group >= workgroups))
     return hipErrorInvalidValue;
-  handoff_probe_kernel<<<workgroups, kHandoffThreads, 0, stream>>>(p);
+  if (p.mode == 3)
+    handoff_split_kernel<<<workgroups, kHandoffThreads, 0, stream>>>(p);
+  else
+    handoff_probe_kernel<<<workgroups, kHandoffThreads, 0, stream>>>(p);
   return hipGetLastError();
 }
 

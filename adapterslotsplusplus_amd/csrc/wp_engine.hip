@@ -1890,9 +1890,9 @@ int wp_handoff_probe(const void* a, int64_t a_bytes, const void* b, int64_t b_by
                      uint32_t* counters, uint32_t* err, int32_t group, int32_t mode, int32_t workgroups, void* stream) {
   if (a_bytes < 0 || b_bytes < 0 || y_bytes < 0 || a_bytes % 16 || b_bytes % 16 || y_bytes % 16 ||
       (a_bytes && !aligned(a, 16)) || (b_bytes && !aligned(b, 16)) || (y_bytes && !aligned(y, 16)) || !counters ||
-      !err || group < 1 || mode < 0 || mode > 2 || workgroups < 1)
+      !err || group < 1 || mode < 0 || mode > 3 || workgroups < 1 || (mode == 3 && group >= workgroups))
     return fail(WP_ERR_INVALID, "handoff_probe: 16-byte aligned buffers of multiples of 16 bytes, counters, an error "
-                                "word, group >= 1, mode 0..2");
+                                "word, group >= 1, mode 0..3 (mode 3: group < workgroups)");
   HandoffProbe p{};
   p.a = a;
   p.a16 = static_cast<uint64_t>(a_bytes) / 16;

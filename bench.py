@@ -210,6 +210,55 @@ def measure_floor(engine, dev, n_calls, sizes, reps):
     return out
 
 
+def measure_handoff(dev, n_calls, volumes, reps):
+    """Per-launch time of the library's handoff probe (wp_handoff_probe) at a
+    call's volumes: `a` = the call's A and X bytes (the shrink side), `b` = B
+    and the Y read (the expand side), `y` = the Y write, over n_calls distinct
+    buffers in one graph.  Forms: no dependency (mode 0), one chip-wide
+    dependency between the two halves on every compute unit (mode 1, the
+    expand side's first batch issued before the wait), and the halves on
+    separate compute units (mode 3: `group` compute units stream `a` and
+    count, the rest stream all of `b` before waiting, then write `y`).  What
+    one handoff costs a launch with no MFMA, no partial data and perfect
+    balance."""
+    import ctypes
+
+    import torch
+
+    from adapterslotsplusplus_amd import _lib
+
+    lib = _lib.load()
+    wgs = torch.cuda.get_device_properties(dev).multi_processor_count
+    out = {}
+    for name, (a_bytes, b_bytes, y_bytes) in volumes.items():
+        a16, b16, y16 = (v // 16 * 16 for v in (a_bytes, b_bytes, y_bytes))
+        stride = (a16 + b16 + y16 + 255) // 256 * 256
+        buf = torch.empty(n_calls * stride, dtype=torch.uint8, device=dev).fill_(1)
+        counters = torch.zeros(wgs * 2 * 64, dtype=torch.int32, device=dev)
+        err = torch.zeros(1, dtype=torch.int32, device=dev)
+        base = buf.data_ptr()
+
+        def probe(i, group, mode):
+            o = base + i * stride
+            return lambda: _lib.check(lib.wp_handoff_probe(
+                ctypes.c_void_p(o), a16, ctypes.c_void_p(o + a16), b16, ctypes.c_void_p(o + a16 + b16), y16,
+                ctypes.c_void_p(counters.data_ptr()), ctypes.c_void_p(err.data_ptr()), group, mode, wgs,
+                ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "handoff_probe")
+
+        res = {"no_wait_us": launch_duration_us([probe(i, 1, 0) for i in range(n_calls)], reps),
+               "one_chip_wide_wait_us": launch_duration_us([probe(i, wgs, 1) for i in range(n_calls)], reps)}
+        for S in (wgs // 4, 3 * wgs // 8, wgs // 2):
+            res[f"split_{S}_of_{wgs}_cus_us"] = launch_duration_us([probe(i, S, 3) for i in range(n_calls)], reps)
+        torch.cuda.synchronize()
+        if int(err.item()) != 0:
+            raise RuntimeError("handoff probe: a wait gave up")
+        out[name] = {k: round(v, 3) for k, v in res.items()}
+        out[name]["bytes"] = {"a": a16, "b": b16, "y": y16}
+        del buf, counters, err
+        torch.cuda.empty_cache()
+    return out
+
+
 def calibration_copy(dev):
     """One device copy of COPY_BYTES (read and written once): the reference
     point that scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes.
@@ -947,6 +996,12 @@ def main():
     log("floor: read probe")
     fl = measure_floor(engine, dev, n_layers, [bytes_qkv, bytes_o], reps)
     floor_step_us = n_layers * (fl[bytes_qkv] + fl[bytes_o])
+    log("floor: handoff probe")
+    x_bytes = 2 * T * h
+    a_side = 2 * touched * r * h + x_bytes
+    ho = measure_handoff(dev, n_layers, {
+        "qkv": (a_side, 2 * touched * r * 3 * h + 2 * T * 3 * h, 2 * T * 3 * h),
+        "o_proj": (a_side, 2 * touched * r * h + 2 * T * h, 2 * T * h)}, reps)
 
     copy_gbs = calibration_copy(dev)
 
@@ -1002,6 +1057,7 @@ def main():
             "qkv_frac_of_floor": round(fl[bytes_qkv] / qkv_us, 4),
             "read_GB_s_qkv_bytes": round(bytes_qkv / (fl[bytes_qkv] * 1e-6) / 1e9, 1),
             "copy_GB_s_256MiB": round(copy_gbs, 1),
+            "handoff_probe": ho,
         },
     }
     if not args.no_secondary:

@@ -390,7 +390,10 @@ int wp_read_probe(wp_engine* e, const void* buffer, int64_t bytes, void* sink, v
  * themselves on their group's counter (`group` consecutive workgroups wait
  * for each other), stream their share of `b` (B, and Y read) -- the first
  * batch of it before waiting for the group (mode 1), all of it after (mode
- * 2), or with no wait (mode 0) -- and write their share of `y`.  counters:
+ * 2), or with no wait (mode 0) -- and write their share of `y`.  Mode 3
+ * splits the roles over compute units instead (one workgroup per compute
+ * unit): workgroups [0, group) stream `a` and count themselves, the others
+ * stream all of `b`, wait for every count and write `y`.  counters:
  * 2 x 64 words per group, zero before the first launch (each launch leaves
  * them zero); *err gets bit 0 if a wait gave up (about 0.1 s; the counters
  * must then be zeroed again).  All pointers are device memory. */

@@ -50,16 +50,16 @@ def test_barrier_probe_rejects_bad_arguments():
                                     ctypes.c_void_p(bad.data_ptr()), _stream()) == _lib.WP_ERR_INVALID
 
 
-@pytest.mark.parametrize("mode", [0, 1, 2])
-def test_handoff_probe_runs_clean(mode):
+@pytest.mark.parametrize("mode,group", [(0, 8), (1, 8), (2, 8), (3, 64)])
+def test_handoff_probe_runs_clean(mode, group):
     """Every wait ends (no give-up), the group counters are left at zero for
     the next launch, and y is written."""
-    announce(f"handoff probe mode {mode}")
+    announce(f"handoff probe mode {mode} group {group}")
     lib = _lib.load()
     a = torch.randint(0, 255, (4 << 20,), dtype=torch.uint8, device="cuda")
     b = torch.randint(0, 255, (8 << 20,), dtype=torch.uint8, device="cuda")
     y = torch.zeros(2 << 20, dtype=torch.uint8, device="cuda")
-    workgroups, group = 256, 8
+    workgroups = 256
     counters = torch.zeros(workgroups // group * 2 * 64, dtype=torch.int32, device="cuda")
     err = torch.zeros(1, dtype=torch.int32, device="cuda")
     for _ in range(3):
