@@ -22,6 +22,12 @@ achieved = the call's algorithmic bytes / that duration.  traffic (HBM bytes per
 FETCH_SIZE / WRITE_SIZE runs summarised in profiles/apply_qkv_cfg2_pmc.json,
 scaled by the same counters' reading for the plain copy this script launches
 once (COPY_BYTES read + written); null when that summary is absent.
+traffic_measured_on names the commit whose kernels those counters were read
+on (the summary's `measured_on`).
+
+cpu_baseline: the oracle's per-segment torch fp32 path on this host's cores,
+on one cfg2 o_proj call (the metric's unit), with BASELINE.json configs[0]
+(cfg1, the reference's CPU-runnable case) beside it under `cfg1`.
 
 Prints one JSON line.  `--gpus N` with N > 1 exits: this build runs on one GPU.
 
@@ -52,6 +58,9 @@ if ROOT not in sys.path:
 PEAK_HBM_GBS = 8000.0
 COPY_BYTES = 256 << 20  # calibration copy: bytes read (and written) once
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "apply_qkv_cfg2_pmc.json")
+# Bytes one replay of the flatness and cfg1 graphs reads at least: twice the
+# 256 MB last-level cache, so those rows are not served from it.
+FLAT_WORKING_SET = 512 << 20
 METRIC = "shrink+expand achieved HBM GB/s (% of peak); us per 80-call decode step"
 
 
@@ -138,14 +147,14 @@ def launch_duration_us(calls, reps):
 
 
 def pmc_traffic():
-    """HBM bytes per launch of the qkv apply kernel from the committed PMC
-    summary, or None."""
+    """(HBM bytes per launch of the qkv apply kernel, the build they were
+    counted on) from the committed PMC summary, or (None, None)."""
     try:
         with open(PMC_SUMMARY) as f:
             p = json.load(f)
-        return int(p["hbm_bytes_per_launch"])
+        return int(p["hbm_bytes_per_launch"]), p.get("measured_on")
     except (OSError, ValueError, KeyError):
-        return None
+        return None, None
 
 
 def graph_us(fn, reps, warmup=3):
@@ -289,16 +298,17 @@ def emit(out):
 
 def measure_flatness(reps, sort=False):
     """cfg2 shapes with N resident adapters, N = 1..128 (Zipf(1.1), seed 1;
-    sort: the same tokens sorted by adapter): 8 layers x {qkv, o_proj} with
-    distinct weights per layer, one graph per N.  Returns the rows and
-    max/min of the latency."""
+    sort: the same tokens sorted by adapter): layers x {qkv, o_proj} with
+    distinct weights per layer, one graph per N, with as many layers as make
+    one replay read FLAT_WORKING_SET bytes.  Returns the rows and max/min of
+    the latency per (qkv, o_proj) pair."""
     import torch
 
     from adapterslotsplusplus_amd import WarpPipeEngine
     from adapterslotsplusplus_amd import workloads as wl
 
     dev = torch.device("cuda", 0)
-    T, r, h, dt, n_layers = 256, 32, 4096, torch.bfloat16, 8
+    T, r, h, dt = 256, 32, 4096, torch.bfloat16
     gen = torch.Generator(device=dev)
     gen.manual_seed(99)
 
@@ -313,6 +323,11 @@ def measure_flatness(reps, sort=False):
         if sort:
             idx = torch.sort(idx).values
         touched = len(set(idx.tolist()))
+        # Enough layers that one replay reads at least FLAT_WORKING_SET bytes
+        # (X, both Y and the touched adapters' weights of every layer), past
+        # the 256 MB last-level cache, and at least 8.
+        per_layer = 2 * T * h * 5 + touched * 2 * r * h * 6
+        n_layers = max(8, -(-FLAT_WORKING_SET // per_layer))
         layers = [dict(wa_q=rn((N, 1, r, h), .02), wb_q=[rn((N, 1, h, r), .02) for _ in range(3)],
                        wa_o=rn((N, 1, r, h), .02), wb_o=rn((N, 1, h, r), .02), x=rn((T, h), 1.),
                        y_q=rn((T, 3 * h), 1.), y_o=rn((T, h), 1.)) for _ in range(n_layers)]
@@ -325,44 +340,48 @@ def measure_flatness(reps, sort=False):
 
         us, _ = graph_us(step, reps)
         nbytes = n_layers * (wl.algorithmic_bytes(T, h, 3 * h, [r] * touched) + wl.algorithmic_bytes(T, h, h, [r] * touched))
-        rows.append({"resident": N, "touched": touched, "us_per_16_calls": round(us, 2),
-                     "us_per_80_call_step": round(us * 5, 1), "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1)})
+        pair = us / n_layers
+        rows.append({"resident": N, "touched": touched, "layers": n_layers,
+                     "working_set_MiB": round(n_layers * per_layer / 2 ** 20, 1), "us_per_graph": round(us, 2),
+                     "us_per_qkv_o_pair": round(pair, 3), "us_per_80_call_step": round(pair * 40, 1),
+                     "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1)})
         log(f"flatness{' (sorted)' if sort else ''} N={N}: {rows[-1]}")
         del layers
         torch.cuda.empty_cache()
     assert engine.device_errors() == 0
-    lat = [x["us_per_16_calls"] for x in rows]
+    lat = [x["us_per_qkv_o_pair"] for x in rows]
     return {"rows": rows, "max_over_min_latency": round(max(lat) / min(lat), 3), "target_max_over_min": 1.15}
 
 
 def run_flatness(args):
     res = measure_flatness(max(5, args.steps))
     res_s = measure_flatness(max(5, args.steps), sort=True)
-    emit({"workload": "cfg2 flatness: resident adapters 1..128, 8 layers x (qkv, o_proj) + build_seg_bounds per graph",
+    emit({"workload": "cfg2 flatness: resident adapters 1..128, layers x (qkv, o_proj) + build_seg_bounds per graph, "
+                      "at least 8 layers and 512 MiB read per replay",
           **res, "sorted_routing": res_s})
 
 
 def measure_cfg1_gpu(reps, sort=False):
     """BASELINE configs[0] on the GPU: h=4096, r=16, 4 adapters, 64 uniformly
     routed tokens (sort: the same tokens sorted by adapter), fp16, scale 1;
-    us per add_lora call (a graph of 40 calls over distinct copies of the
-    inputs)."""
+    us per add_lora call (a graph of calls over distinct copies of the
+    inputs, FLAT_WORKING_SET bytes of them, so that no call finds its
+    operands in the last-level cache)."""
     import torch
 
     from adapterslotsplusplus_amd import WarpPipeEngine
     from adapterslotsplusplus_amd import workloads as wl
 
     dt = torch.float16
-    idx = wl.uniform_indices(64, 4, seed=0)
+    idx, x, wa, wb = cfg1_inputs()
     if sort:
         idx = torch.sort(idx).values
-    x = wl.normal((64, 4096), 1.0, dt, 10)
-    wa = wl.normal((4, 1, 16, 4096), 0.02, dt, 11)
-    wb = wl.normal((4, 1, 4096, 16), 0.02, dt, 12)
     nbytes = wl.algorithmic_bytes(64, 4096, 4096, [16] * len(set(idx.tolist())))
     engine = WarpPipeEngine()
     assert engine.build_seg_bounds(idx.cuda())
-    copies = [(x.cuda(), wa.cuda(), wb.cuda(), torch.zeros(64, 4096, dtype=dt, device="cuda")) for _ in range(40)]
+    per_copy = 4 * 64 * 4096 * 2  # x, A, B, y: 512 KiB each
+    copies = [(x.cuda(), wa.cuda(), wb.cuda(), torch.zeros(64, 4096, dtype=dt, device="cuda"))
+              for _ in range(-(-FLAT_WORKING_SET // per_copy))]
 
     def calls():
         for xc, ac, bc, yc in copies:
@@ -370,44 +389,67 @@ def measure_cfg1_gpu(reps, sort=False):
 
     us, _ = graph_us(calls, reps)
     us /= len(copies)
-    return {"us_per_call": round(us, 3), "bytes_per_call": nbytes, "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1)}
+    return {"us_per_call": round(us, 3), "bytes_per_call": nbytes, "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "calls_per_graph": len(copies), "working_set_MiB": round(len(copies) * per_copy / 2 ** 20, 1)}
 
 
-def run_cfg1(args):
-    """BASELINE configs[0]: one call on the GPU and the oracle on the host."""
+def cfg1_inputs():
+    """BASELINE configs[0]'s inputs on the host: 64 tokens uniform over 4
+    adapters (seed 0), h=4096, r=16, fp16."""
+    import torch
+
+    from adapterslotsplusplus_amd import workloads as wl
+
+    dt = torch.float16
+    idx = wl.uniform_indices(64, 4, seed=0)
+    x = wl.normal((64, 4096), 1.0, dt, 10)
+    wa = wl.normal((4, 1, 16, 4096), 0.02, dt, 11)
+    wb = wl.normal((4, 1, 4096, 16), 0.02, dt, 12)
+    return idx, x, wa, wb
+
+
+def cpu_baseline_cfg1(seconds):
+    """BASELINE configs[0] (the reference's CPU-runnable case) through the
+    oracle's per-segment torch fp32 path on this host's cores: us per
+    add_lora call (median)."""
     import torch
 
     from adapterslotsplusplus_amd import workloads as wl
     from oracle import bgmv
     from oracle import segments as so
 
-    gpu = measure_cfg1_gpu(max(5, args.steps))
-    gpu_s = measure_cfg1_gpu(max(5, args.steps), sort=True)
-    dt = torch.float16
-    idx = wl.uniform_indices(64, 4, seed=0)
-    x = wl.normal((64, 4096), 1.0, dt, 10)
-    wa = wl.normal((4, 1, 16, 4096), 0.02, dt, 11)
-    wb = wl.normal((4, 1, 4096, 16), 0.02, dt, 12)
-    nbytes = gpu["bytes_per_call"]
+    idx, x, wa, wb = cfg1_inputs()
+    nbytes = wl.algorithmic_bytes(64, 4096, 4096, [16] * len(set(idx.tolist())))
     segs = so.seg_bounds(idx.numpy()).tolist()
-    y = torch.zeros(64, 4096, dtype=dt)
+    y = torch.zeros(64, 4096, dtype=torch.float16)
     cores = os.cpu_count() or 1
     torch.set_num_threads(cores)
     for _ in range(3):
         bgmv.add_lora(y, x, wa, wb, 1.0, segs)
     times = []
-    t_end = time.perf_counter() + min(args.cpu_seconds, 10.0)
+    t_end = time.perf_counter() + seconds
     while time.perf_counter() < t_end or len(times) < 20:
         t0 = time.perf_counter()
         bgmv.add_lora(y, x, wa, wb, 1.0, segs)
         times.append(time.perf_counter() - t0)
     times.sort()
     cpu_us = times[len(times) // 2] * 1e6
+    return {"us_per_call": round(cpu_us, 1), "GB_s": round(nbytes / (cpu_us * 1e-6) / 1e9, 3), "cores": cores,
+            "kind": "port", "runs": len(times),
+            "sample": (f"{len(times)} add_lora calls of cfg1 (T=64, h=4096, r=16, 4 adapters uniform, seed 0, fp16; "
+                       f"{len(segs)} run-length segments), torch fp32 per segment")}
+
+
+def run_cfg1(args):
+    """BASELINE configs[0]: one call on the GPU and the oracle on the host."""
+    gpu = measure_cfg1_gpu(max(5, args.steps))
+    gpu_s = measure_cfg1_gpu(max(5, args.steps), sort=True)
+    cpu = cpu_baseline_cfg1(min(args.cpu_seconds, 10.0))
     emit({"workload": "cfg1: T=64, h=4096, r=16, 4 adapters uniform (seed 0), fp16, one add_lora call",
-          "bytes_per_call": nbytes, "gpu_us_per_call": gpu["us_per_call"], "gpu_GB_s": gpu["GB_s"],
+          "bytes_per_call": gpu["bytes_per_call"], "gpu_us_per_call": gpu["us_per_call"], "gpu_GB_s": gpu["GB_s"],
+          "gpu_calls_per_graph": gpu["calls_per_graph"], "gpu_working_set_MiB": gpu["working_set_MiB"],
           "gpu_sorted_routing": {"us_per_call": gpu_s["us_per_call"], "GB_s": gpu_s["GB_s"]},
-          "cpu_baseline": {"us_per_call": round(cpu_us, 1), "GB_s": round(nbytes / (cpu_us * 1e-6) / 1e9, 3),
-                           "cores": cores, "kind": "port", "runs": len(times)}})
+          "cpu_baseline": cpu})
 
 
 def run_cfg3(args):
@@ -1004,6 +1046,7 @@ def main():
         "o_proj": (a_side, 2 * touched * r * h + 2 * T * h, 2 * T * h)}, reps)
 
     copy_gbs = calibration_copy(dev)
+    traffic, traffic_on = pmc_traffic()
 
     out = {
         "metric": METRIC,
@@ -1034,7 +1077,8 @@ def main():
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": pmc_traffic(),
+            "traffic": traffic,
+            "traffic_measured_on": traffic_on,
             "kernel": "wp::apply_kernel<__bf16, 32, kFusedMulti, 1> (packed-qkv call: shrink + expand, one launch)",
             "bytes_per_launch": bytes_qkv,
             "us_per_launch": round(qkv_us, 3),
@@ -1080,7 +1124,8 @@ def main():
             "cfg2_sorted_routing": {"us_per_step": round(sorted_us, 2),
                                     "GB_s": round(bytes_step / (sorted_us * 1e-6) / 1e9, 2),
                                     "workload": "the cfg2 step with the same tokens sorted by adapter"},
-            "flatness": {**flat, "workload": "cfg2 shapes, 8 layers x (qkv, o_proj) per graph, N resident adapters",
+            "flatness": {**flat, "workload": "cfg2 shapes, N resident adapters, layers x (qkv, o_proj) per graph "
+                                             "(at least 8 layers and 512 MiB read per replay)",
                          "sorted_routing": flat_s},
             "cfg5_draft_step": {**c5, "workload": "h=2048, 22 layers x (q, k, v, o), T=128 (32 tenants x 4), r=32, "
                                                   "bf16, build_seg_bounds + the calls in one graph; cfg5_us_per_step "
@@ -1091,6 +1136,8 @@ def main():
     if not args.no_cpu_baseline:
         log("cpu baseline")
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        log("cpu baseline: cfg1")
+        out["cpu_baseline"]["cfg1"] = cpu_baseline_cfg1(min(args.cpu_seconds, 10.0))
     print(json.dumps(out), flush=True)
 
 
