@@ -9,6 +9,7 @@ so a test can tell which path produced a result.  The live wrapper is
 switched with install_warp_pipe_v1 and AS_WARP_PIPE=1."""
 from types import SimpleNamespace
 
+import numpy as np
 import pytest
 import torch
 
@@ -17,7 +18,7 @@ from adapterslotsplusplus_amd import punica_v1 as v1
 from adapterslotsplusplus_amd import punica_wrapper as pw
 from adapterslotsplusplus_amd import workloads as wl
 from oracle import v1_ops
-from tests.helpers import announce, assert_close, randn
+from tests.helpers import announce, assert_close, h_tie_flips, randn, seeds
 
 pytestmark = pytest.mark.gpu
 
@@ -289,3 +290,62 @@ def test_update_metadata_reports_skipped_tokens(wrapper, monkeypatch):
                 torch.cuda.synchronize()
     finally:
         pw.device_errors_seen |= before
+
+
+@pytest.mark.parametrize("seed", seeds(8))
+def test_random_v1_calls(wrapper, seed):
+    """Seeded V1 calls on the kernels: T across the 512-token switch (decode
+    and prefill tables), 1-3 slices of one rank (8-64) with ragged widths,
+    biases on some slices, both dtypes; add_lora_linear, then add_shrink +
+    add_expand (with an offset_start) on the same step.  No call may fall
+    back.  H is rounded to the I/O type before the expand; where an exact H
+    element sits within fp32 summation error of a rounding midpoint either
+    neighbour is correct, and the output may move by that step times |B|."""
+    rng = np.random.default_rng(5000 + seed)
+    dtype = (torch.bfloat16, torch.float16)[seed % 2]
+    T = int(rng.choice([1, 33, 200, 512, 513, 900]))
+    d = int(rng.choice([64, 520, 2048]))
+    r = int(rng.choice([8, 16, 32, 64]))
+    L = int(rng.integers(1, 20))
+    n = int(rng.integers(1, 4))
+    # Slice widths of 8-element multiples keep y's rows 16-byte aligned.
+    outs = tuple(int(rng.integers(1, 100)) * 8 for _ in range(n))
+    bias_slices = tuple(i for i in range(n) if rng.integers(2))
+    scale = float(rng.uniform(0.25, 2.0))
+    off0 = int(rng.integers(0, 8)) * 8
+    ids = torch.from_numpy(np.repeat(rng.integers(-1, L, size=T), rng.integers(1, 6, size=T))[:T].astype(np.int64))
+    prefill = T > 512
+    announce(f"v1 random seed {seed}: T={T} d={d} r={r} L={L} outs={outs} bias={bias_slices} off0={off0} {dtype}")
+    wrapper.calls.clear()
+    wrapper.update_metadata(mapping(ids, prefill), None, L, 0, 0)
+    was, wbs, bias = weights(L, r, d, outs, dtype, 6000 + 10 * seed, bias_slices)
+    x = randn((T, d), 6001 + 10 * seed, dtype)
+    y0 = randn((T, sum(outs)), 6002 + 10 * seed, dtype)
+    y = y0.cuda()
+    wrapper.add_lora_linear(y, x.cuda(), was, wbs, bias, scale, outs)
+    torch.cuda.synchronize()
+    slack = torch.zeros(y0.shape, dtype=torch.float32)
+    for a in torch.unique(ids[ids >= 0]).tolist():
+        rows = torch.nonzero(ids == a).flatten()
+        off = 0
+        for i, o in enumerate(outs):
+            flips = h_tie_flips(x[rows], was[i][a, 0].cpu(), scale, dtype)
+            slack[rows, off:off + o] += (flips @ wbs[i][a, 0].cpu().double().abs().T).float()
+            off += o
+    ref = v1_ops.add_lora_linear(y0, x, cpu(was), cpu(wbs), cpu(bias), scale, outs, ids)
+    assert_close(y, ref, f"add_lora_linear seed {seed}", slack=slack)
+    # V1's two-op form on the same step: the fp32 buffer, then the expand into
+    # windows from offset_start.
+    buf = torch.zeros(n, T, r, device="cuda")
+    wrapper.add_shrink(buf, x.cuda(), was, scale)
+    torch.cuda.synchronize()
+    buf_ref = v1_ops.lora_shrink(torch.zeros(n, T, r), x, cpu(was), scale, ids)
+    assert_close(buf, buf_ref, f"add_shrink seed {seed}", rtol=1e-4, atol=1e-4)
+    z0 = randn((T, off0 + sum(outs) + 8), 6003 + 10 * seed, dtype)
+    z = z0.cuda()
+    wrapper.add_expand(z, buf, wbs, bias, outs, offset_start=off0)
+    torch.cuda.synchronize()
+    zref = v1_ops.lora_expand(v1_ops.apply_bias(z0, cpu(bias), outs, ids, off0), buf.cpu(), cpu(wbs), outs, ids, off0)
+    assert_close(z, zref, f"add_expand seed {seed}")
+    assert wrapper.calls == ["update_metadata"], wrapper.calls
+    assert pw._engine.device_errors() == 0
