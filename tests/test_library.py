@@ -75,3 +75,20 @@ def test_null_engine_arguments_are_errors_not_crashes():
     with pytest.raises(RuntimeError, match="engine is NULL"):
         _lib.check(lib.wp_evict_adapter(None, 0, None), "evict_adapter")
     assert lib.wp_read_probe(None, None, 0, None, None) == _lib.WP_ERR_INVALID
+
+
+@pytest.mark.parametrize("compiler,std", [("gcc", "-std=c99"), ("g++", "-std=c++17")])
+def test_header_is_plain_c_and_cpp(tmp_path, compiler, std):
+    """The public header compiles on its own as C99 and as C++17 with every
+    warning an error (no HIP or torch headers needed by a caller)."""
+    import shutil
+    import subprocess
+
+    if shutil.which(compiler) is None:
+        pytest.skip(f"{compiler} not found")
+    src = tmp_path / ("use.c" if compiler == "gcc" else "use.cc")
+    src.write_text('#include "warppipe_mi355x.h"\n'
+                   "int probe(void) { return wp_rank_supported(32) + wp_abi_version(); }\n")
+    r = subprocess.run([compiler, std, "-Wall", "-Wextra", "-pedantic", "-Werror", "-fsyntax-only",
+                        "-I", os.path.join(ROOT, "include"), str(src)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
