@@ -1,12 +1,14 @@
 """The read probe bench.py times for the per-call floor (wp_read_probe): it
 reads what it is given without changing it, and rejects arguments it cannot
-take."""
+take.  Also the program the committed HBM counter summaries are read over
+(counter_run)."""
 import ctypes
 
 import pytest
 import torch
 
 from adapterslotsplusplus_amd import WarpPipeEngine, _lib
+from tests.helpers import announce
 
 pytestmark = pytest.mark.gpu
 
@@ -37,3 +39,13 @@ def test_read_probe_rejects_bad_arguments():
     assert _probe(engine, buf.data_ptr(), -16, sink.data_ptr()) == _lib.WP_ERR_INVALID
     assert _probe(engine, buf.data_ptr(), 16, None) == _lib.WP_ERR_INVALID
     assert "read_probe" in _lib.last_error()
+
+
+@pytest.mark.parametrize("workload", ["cfg2", "cfg3"])
+def test_counter_run_program_runs(workload):
+    """The program the committed HBM counter summaries are read over runs to
+    its end (one layer, one pass) with a clean error word."""
+    from adapterslotsplusplus_amd import counter_run
+
+    announce(f"counter_run --workload {workload}")
+    assert counter_run.main(["--workload", workload, "--layers", "1", "--passes", "1"]) == 0
