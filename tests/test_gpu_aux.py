@@ -10,7 +10,6 @@
     after capture, with and without wp_set_max_adapters."""
 import ctypes
 
-import numpy as np
 import pytest
 import torch
 

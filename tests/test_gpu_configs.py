@@ -1,7 +1,6 @@
 """GPU parity at the full sizes of the five benchmark configurations
 (BASELINE.json configs[0..4]) against the CPU oracle, on identical inputs
 drawn with seeded CPU generators (adapterslotsplusplus_amd.workloads)."""
-import numpy as np
 import pytest
 import torch
 
